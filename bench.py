@@ -1,0 +1,202 @@
+"""Benchmark of the sageattn_vc hot path on one MI355X (BASELINE.json metric).
+
+A step is one pass of the hot path over one batch: preprocessing (K centring,
+Sage INT8 Q/K, V E4M3 [+ grouping and block smoothing]) followed by the fused
+attention kernel, with bf16 inputs already resident in HBM. The headline value
+is the fused kernel's effective TOPS = 4*B*H*Nq*Nk*D / kernel time, timed with
+HIP events on the stream the kernels run on; preprocessing is timed separately.
+
+    python bench.py [--steps K] [--warmup W] [--config main|smooth|d64|long|cpu]
+
+Prints ONE JSON line (rank 0, N=1). --gpus N with N > 1 exits: this build runs
+on one GPU only.
+"""
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "cake-opt-vc_attention_amd"))
+sys.path.insert(0, str(ROOT))
+
+PEAK_TOPS = 5000.0      # MI355X dense INT8 / FP8 MFMA, TOPS (published)
+PEAK_HBM_GBS = 8000.0   # MI355X HBM3E, GB/s (published)
+
+CONFIGS = {
+    # name: (B, H, N, D, kind, v_smooth, description)
+    "main": (1, 28, 37741, 128, "normal", False,
+             "BNSD [1,28,37741,128] bf16, Q/K/V N(0,1) seed 0, non-causal, sm_scale=1/sqrt(128), "
+             "INT8 QK (Sage per-thread scales) + ExpCast FP8 E4M3 PV, V smoothing off"),
+    "smooth": (1, 28, 37741, 128, "outlier", True,
+               "BNSD [1,28,37741,128] bf16, K outlier channels, clustered V; ExpCast + V grouping "
+               "(8 clusters, 2 Lloyd iterations) + 128-token block-mean smoothing"),
+    "d64": (1, 40, 32760, 64, "normal", True,
+            "BNSD [1,40,32760,64] bf16, N(0,1); ExpCast + V smoothing"),
+    "long": (1, 28, 75482, 128, "student", True,
+             "BNSD [1,28,75482,128] bf16, Q,K 0.5*Student-t(4), V N(0,1); full pipeline"),
+    "cpu": (1, 2, 2048, 128, "normal", False,
+            "BNSD [1,2,2048,128] bf16 N(0,1), smoothing off (the reference's CPU plumbing case)"),
+}
+
+
+def make_inputs(B, H, N, D, kind, seed=0):
+    """Seeded CPU generation (q, then k, then v), cast to bf16."""
+    import numpy as np
+    import torch
+    g = torch.Generator().manual_seed(seed)
+    if kind == "normal":
+        q = torch.randn(B, H, N, D, generator=g)
+        k = torch.randn(B, H, N, D, generator=g)
+        v = torch.randn(B, H, N, D, generator=g)
+    elif kind == "outlier":
+        q = torch.randn(B, H, N, D, generator=g)
+        k = torch.randn(B, H, N, D, generator=g) + torch.randn(B, H, 1, D, generator=g) * 2.0
+        cent = torch.randn(B, H, 8, D, generator=g) * 2.0 ** 0.5
+        assign = torch.randint(0, 8, (B, H, N), generator=g)
+        v = torch.gather(cent, 2, assign[..., None].expand(B, H, N, D)) + torch.randn(B, H, N, D, generator=g) * 0.3 ** 0.5
+    elif kind == "student":
+        rng = np.random.Generator(np.random.PCG64(seed))
+        q = torch.from_numpy(0.5 * rng.standard_t(4, size=(B, H, N, D)).astype(np.float32))
+        k = torch.from_numpy(0.5 * rng.standard_t(4, size=(B, H, N, D)).astype(np.float32))
+        v = torch.randn(B, H, N, D, generator=g)
+    else:
+        raise ValueError(kind)
+    return q.to(torch.bfloat16), k.to(torch.bfloat16), v.to(torch.bfloat16)
+
+
+def cpu_baseline(q, k, v, smooth, rows, budget_s):
+    """The CPU oracle (C restatement, OpenMP over rows) on the box's host cores:
+    full preprocessing of the same workload plus attention for `rows` evenly
+    spaced query rows of every head against all keys, extrapolated to all rows."""
+    import numpy as np
+    import torch
+    from oracle import vc_oracle as o
+
+    bits = lambda x: x.contiguous().view(torch.int16).numpy().view(np.uint16)
+    B, H, N, D = q.shape
+    qb, kb, vb = bits(q), bits(k), bits(v)
+    t0 = time.perf_counter()
+    st = o.prepare(qb, kb, vb, v_smooth=smooth)
+    prep_s = time.perf_counter() - t0
+    ids = o.query_indices(N, rows)
+    t0 = time.perf_counter()
+    o.reference(st, query_indices=ids)
+    attn_s = time.perf_counter() - t0
+    ops = 4.0 * B * H * len(ids) * N * D
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    return {
+        "value": ops / attn_s / 1e12,
+        "unit": "TOPS",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"oracle/vc_oracle.c: attention of {len(ids)} evenly spaced query rows x all {N} keys x "
+                  f"{B * H} heads (ExpCast P bytes + decoded-payload fp64 accumulation), OpenMP over rows; "
+                  f"value = 4*B*H*rows*N*D / time. Full preprocessing of the same inputs (single thread) "
+                  f"took {prep_s:.2f} s; extrapolated full forward = {prep_s + attn_s * N / len(ids):.1f} s",
+        "attention_s": attn_s,
+        "prep_s": prep_s,
+        "cpu_model": platform.processor() or platform.machine(),
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", default="main", choices=sorted(CONFIGS))
+    ap.add_argument("--cpu-rows", type=int, default=32, help="query rows per head for the CPU baseline")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build runs the sageattn_vc path on ONE GPU; multi-GPU runs are not part of it "
+              "(the path would shard by (batch, head) with no communication).", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import vcx
+
+    B, H, N, D, kind, smooth, desc = CONFIGS[args.config]
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    qc, kc, vc_ = make_inputs(B, H, N, D, kind)
+    q, k, v = (x.to(dev) for x in (qc, kc, vc_))
+    scale = D ** -0.5
+    clusters, iterations = 8, 2
+
+    def prep():
+        perm = vcx.group_values(v, clusters, iterations) if smooth else None
+        q8, qs, k8, ks, _ = vcx.prepare_qk(q, k, perm)
+        v8, vs, means = vcx.prepare_v(v, perm, smooth=smooth, channel_scale=True)
+        return q8, qs, k8, ks, v8, vs, means
+
+    out = torch.empty((B, H, N, D), dtype=torch.bfloat16, device=dev)
+
+    def fused(p):
+        q8, qs, k8, ks, v8, vs, means = p
+        vcx.forward(q8, k8, v8, qs, ks, vs, means, True, smooth, 1, scale, out=out)
+
+    for _ in range(args.warmup):
+        fused(prep())
+    torch.cuda.synchronize()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True),
+           torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for e0, e1, e2 in ev:
+        e0.record()
+        p = prep()
+        e1.record()
+        fused(p)
+        e2.record()
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    prep_ms = sorted(e0.elapsed_time(e1) for e0, e1, _ in ev)
+    kern_ms = sorted(e1.elapsed_time(e2) for _, e1, e2 in ev)
+    med = lambda xs: xs[len(xs) // 2]
+    kernel_ms, prep_med = med(kern_ms), med(prep_ms)
+    ops = 4.0 * B * H * N * N * D
+    tops = ops / (kernel_ms * 1e-3) / 1e12
+    mean_kernel_ms = sum(kern_ms) / len(kern_ms)
+    achieved = ops / (mean_kernel_ms * 1e-3) / 1e12
+    tiles = (N + 127) // 128
+    prep_bytes = 6.0 * B * H * N * D + 3.0 * B * H * N * D + 4.0 * B * H * ((N + 63) // 64 * 32) \
+        + 4.0 * B * H * tiles * 4 + 4.0 * B * H * D + (2.0 * B * H * tiles * D if smooth else 0.0)
+    prep_gbs = prep_bytes / (prep_med * 1e-3) / 1e9
+    result = {
+        "metric": "sageattn_vc fused-kernel TOPS at BNSD [1,28,37741,128] bf16 (4*B*H*N^2*D / kernel time); "
+                  "kernel ms and fraction of INT8/FP8 MFMA peak",
+        "value": round(tops, 2),
+        "unit": "TOPS",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall_ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8 QK / fp8-e4m3 PV, fp32 accumulate",
+        "data": "synthetic (seeded torch.Generator on CPU, cast to bf16, copied to HBM before timing)",
+        "config": {"workload": desc, "shape_bnsd": [B, H, N, D], "config_name": args.config,
+                   "v_smooth": smooth, "expcast": True},
+        "kernel_ms": round(kernel_ms, 4),
+        "prep_ms": round(prep_med, 4),
+        "step_tops": round(ops / (wall_ms * 1e-3) / 1e12, 2),
+        "frac_of_mfma_peak": round(tops / PEAK_TOPS, 4),
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_TOPS, "unit": "TFLOP/s",
+                     "frac": round(achieved / PEAK_TOPS, 4), "traffic": None,
+                     "kernel": "attn_kernel (fused QK/ExpCast/PV)", "ops_per_launch": ops},
+        "roofline_prep": {"bound": "hbm", "achieved": round(prep_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                          "frac": round(prep_gbs / PEAK_HBM_GBS, 4), "algorithmic_bytes": prep_bytes},
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(qc, kc, vc_, smooth, args.cpu_rows, 30.0)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,449 @@
+// Fused sageattn_vc forward for gfx950 (MI355X).
+//
+// One workgroup = 4 waves = 128 query rows; each wave owns 32 rows as two
+// 16-row groups. Per 128-key tile:
+//   S^T = K Q^T       v_mfma_i32_16x16x64_i8   (A = K rows from LDS, B = Q^T in VGPRs)
+//   logits, online max, ExpCast codes         VALU, one query row per lane
+//   O^T += V^T P^T    v_mfma_f32_16x16x128_f8f6f4 (A = V^T from LDS, B = codes in VGPRs)
+//   row mass          the same MFMA with an all-ones A operand
+// The 16x16 accumulator layout (lane l holds rows 4*(l/16)+r, column l%16)
+// puts the 32 scores of one query row of a 16-key block in the 4 lanes
+// l%16 + 16*G; the codes of block j, rows r=0..3 form byte 4j+r of the lane's
+// PV B operand, so P never leaves the registers. K rows are loaded into the
+// A operand in the order key(j, 4G+r) = 16j + 8(r/2) + 2G + r%2, which gives
+// every lane group G exactly the keys of Sage K-scale group (key%8)/2 == G;
+// the V payload is stored in the matching order (vcx_value_token).
+//
+// K and V^T tiles stream through LDS with gfx950 direct-to-LDS loads
+// (global_load_lds_dwordx4), double buffered, XOR-swizzled so that the 16
+// lanes of a lane group hit 16 distinct 16-byte bank groups.
+//
+// Numerical contract (reference sal/csrc/vc/vc_sm90.cu:284-612, vc_math.cuh:268-474):
+//   tiles before the last: logit = RN(float(acc) * RN(sm * RN(qs*ks)))
+//   last tile:             logit = RN(RN(float(acc) * RN(qs*ks)) * sm), keys >= Nk -> -inf
+//   m' = max(m, rowmax), alpha = expf(m - m'), code = sat_u8(RNE(fmaf(RN(logit-m'), A, B)))
+//   O = alpha*O + PV (+ mass*mean), den = alpha*den + mass, out = O/den * vs.
+#include "vcx_common.hpp"
+
+namespace vcx {
+namespace {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+constexpr int kThreadsPerBlock = 256;
+constexpr int kRowsPerBlock = 128;
+
+struct AttnArgs {
+  const int8_t* q8;
+  const int8_t* k8;
+  const uint8_t* v8;
+  const float* qs;
+  const float* ks;
+  const float* vs;
+  const uint16_t* means;
+  void* out;
+  int64_t osb, osh, osn;
+  int64_t H, Nq, Nk, tiles, qblocks, qs_len;
+  float sm;
+  uint8_t* pdump;
+  int64_t prow0, prow1;
+};
+
+template <int D>
+__device__ inline int swz_k(int row) {
+  if constexpr (D == 128) return (row >> 1) & 7;
+  else return (row >> 2) & 3;
+}
+__device__ inline int swz_v(int row) { return (row >> 1) & 7; }
+
+typedef __attribute__((address_space(3))) void lds_void;
+typedef const __attribute__((address_space(1))) void global_void;
+
+// Direct-to-LDS loads of one key tile. Each of the 4 waves issues D/32
+// instructions for K and D/32 for V^T; instruction n of wave w fills the 64
+// consecutive 16-byte slots (w*(D/32) + n)*64 + lane. A slot holds row
+// s/(D/16) (K) or s/8 (V^T) and the 16-byte chunk given by the XOR swizzle.
+// Lane-constant parts of the addresses are precomputed once per kernel.
+template <int D, bool SMOOTH>
+struct TileLoader {
+  // Meta region of a buffer: SMOOTH ? fp16 means of the tile (2*D bytes) : nothing,
+  // followed by the tile's 4 K scales (16 bytes). Loaded by lanes 0..ML of wave 0.
+  static constexpr int ML = SMOOTH ? (2 * D) / 16 : 0;
+  static constexpr int KS_OFF = 16 * ML;
+  static constexpr int N = D / 32;  // instructions per wave per operand
+  int krow[N];                      // K row of each instruction (for the tail clamp)
+  int kcol[N];                      // byte offset of the chunk inside the K row
+  int voff[N];                      // byte offset inside the V^T tile column block
+  int64_t npad;
+
+  __device__ inline void init(int64_t tiles) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    npad = tiles * kTile;
+#pragma unroll
+    for (int n = 0; n < N; ++n) {
+      const int s = (wave * N + n) * 64 + lane;
+      const int row = s / (D / 16), phys = s % (D / 16);
+      krow[n] = row;
+      kcol[n] = (phys ^ swz_k<D>(row)) * 16;
+      const int ch = s >> 3, vphys = s & 7;
+      voff[n] = ch * static_cast<int>(npad) + ((vphys ^ swz_v(ch)) * 16);
+    }
+  }
+
+  __device__ inline void issue(const AttnArgs& a, int64_t bh, int64_t t, uint8_t* lk, uint8_t* lv,
+                               uint8_t* lm) const {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    if (wave == 0 && lane <= ML) {
+      const void* src = lane < ML ? static_cast<const void*>(a.means + (bh * a.tiles + t) * D + lane * 8)
+                                  : static_cast<const void*>(a.ks + (bh * a.tiles + t) * 4);
+      __builtin_amdgcn_global_load_lds((global_void*)src, (lds_void*)lm, 16, 0, 0);
+    }
+    const int8_t* kb = a.k8 + (bh * a.Nk + t * kTile) * D;
+    const int lim = static_cast<int>(a.Nk - t * kTile) - 1;  // last valid row of this tile
+    const uint8_t* vb = a.v8 + bh * D * npad + t * kTile;
+#pragma unroll
+    for (int n = 0; n < N; ++n) {
+      const int row = krow[n] < lim ? krow[n] : lim;  // rows past Nk: any in-bounds bytes (masked)
+      __builtin_amdgcn_global_load_lds((global_void*)(kb + row * D + kcol[n]),
+                                       (lds_void*)(lk + (wave * N + n) * 1024), 16, 0, 0);
+    }
+#pragma unroll
+    for (int n = 0; n < N; ++n)
+      __builtin_amdgcn_global_load_lds((global_void*)(vb + voff[n]),
+                                       (lds_void*)(lv + (wave * N + n) * 1024), 16, 0, 0);
+  }
+};
+
+__device__ inline v4f mfma_fp8(const v8i& a, const v8i& b, const v4f& c) {
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
+}
+
+template <int D, bool SMOOTH, bool DUMP>
+struct Wave {
+  static constexpr int DS = D / 64;  // 64-deep QK steps
+  static constexpr int CB = D / 16;  // 16-channel output blocks
+
+  v4i qf[2][DS];
+  float qsv[2];
+  int64_t row[2];
+  float m[2], den[2];
+  v4f O[2][CB];
+  int koff[DS], voff[2];
+  int G, li;
+  int64_t bh_;
+
+  __device__ inline v8i load_v(const uint8_t* lv, int cb) const {
+    const v4i lo = *reinterpret_cast<const v4i*>(lv + cb * 16 * kTile + voff[0]);
+    const v4i hi = *reinterpret_cast<const v4i*>(lv + cb * 16 * kTile + voff[1]);
+    return v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  }
+
+  template <bool LAST>
+  __device__ inline void tile(const AttnArgs& a, int64_t t, const uint8_t* lk, const uint8_t* lv, const uint8_t* lm) {
+    const float ksv = *reinterpret_cast<const float*>(lm + TileLoader<D, SMOOTH>::KS_OFF + 4 * G);
+
+    // ---- S^T = K Q^T
+    v4i S[2][8];
+    v4i kc[DS], kn[DS];
+#pragma unroll
+    for (int ds = 0; ds < DS; ++ds) kc[ds] = *reinterpret_cast<const v4i*>(lk + koff[ds]);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      if (j + 1 < 8) {
+#pragma unroll
+        for (int ds = 0; ds < DS; ++ds) kn[ds] = *reinterpret_cast<const v4i*>(lk + (j + 1) * 16 * D + koff[ds]);
+      }
+#pragma unroll
+      for (int qg = 0; qg < 2; ++qg) {
+        v4i acc = {0, 0, 0, 0};
+#pragma unroll
+        for (int ds = 0; ds < DS; ++ds) acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(kc[ds], qf[qg][ds], acc, 0, 0, 0);
+        S[qg][j] = acc;
+      }
+#pragma unroll
+      for (int ds = 0; ds < DS; ++ds) kc[ds] = kn[ds];
+      __builtin_amdgcn_sched_barrier(0);
+    }
+
+    // ---- logits, online max, ExpCast codes
+    v8i P[2];
+    float alpha[2];
+#pragma unroll
+    for (int qg = 0; qg < 2; ++qg) {
+      float lg[8][4];
+      float tmax = -INFINITY;
+      const float dq = qsv[qg] * ksv;
+      if constexpr (!LAST) {
+        const float c = a.sm * dq;
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            lg[j][r] = static_cast<float>(S[qg][j][r]) * c;
+            tmax = fmaxf(tmax, lg[j][r]);
+          }
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int64_t key = t * kTile + 16 * j + 8 * (r >> 1) + 2 * G + (r & 1);
+            float x = (static_cast<float>(S[qg][j][r]) * dq) * a.sm;
+            lg[j][r] = key < a.Nk ? x : -INFINITY;
+            tmax = fmaxf(tmax, lg[j][r]);
+          }
+      }
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+      const float mn = fmaxf(m[qg], tmax);
+      alpha[qg] = expf(m[qg] - mn);
+      m[qg] = mn;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        uint32_t w = 0;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float u = __builtin_fmaf(lg[j][r] - mn, kExpA, kExpB);
+          w = __builtin_amdgcn_cvt_pk_u8_f32(u, r, w);
+        }
+        P[qg][j] = static_cast<int>(w);
+      }
+      if constexpr (DUMP) {
+        if (row[qg] >= a.prow0 && row[qg] < a.prow1 && row[qg] < a.Nq) {
+          const int64_t npad = a.tiles * kTile;
+          uint8_t* dst = a.pdump + (bh_ * (a.prow1 - a.prow0) + (row[qg] - a.prow0)) * npad + t * kTile;
+#pragma unroll
+          for (int j = 0; j < 8; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              dst[16 * j + 8 * (r >> 1) + 2 * G + (r & 1)] = static_cast<uint8_t>((static_cast<uint32_t>(P[qg][j]) >> (8 * r)) & 0xffu);
+        }
+      }
+    }
+
+    // ---- rescale the history only when some row maximum moved
+#pragma unroll
+    for (int qg = 0; qg < 2; ++qg) {
+      if (__any(alpha[qg] != 1.0f)) {
+#pragma unroll
+        for (int cb = 0; cb < CB; ++cb) O[qg][cb] *= alpha[qg];
+      }
+    }
+
+    // ---- O^T += V^T P^T, mass = 1^T P^T
+    v8i vc = load_v(lv, 0), vn;
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb) {
+      if (cb + 1 < CB) vn = load_v(lv, cb + 1);
+#pragma unroll
+      for (int qg = 0; qg < 2; ++qg) O[qg][cb] = mfma_fp8(vc, P[qg], O[qg][cb]);
+      vc = vn;
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    const v8i ones = {0x38383838, 0x38383838, 0x38383838, 0x38383838,
+                      0x38383838, 0x38383838, 0x38383838, 0x38383838};
+#pragma unroll
+    for (int qg = 0; qg < 2; ++qg) {
+      const v4f zero = {0.0f, 0.0f, 0.0f, 0.0f};
+      const v4f ms = mfma_fp8(ones, P[qg], zero);
+      den[qg] = den[qg] * alpha[qg] + ms[0];
+      if constexpr (SMOOTH) {
+#pragma unroll
+        for (int cb = 0; cb < CB; ++cb) {
+          const uint2 hm = *reinterpret_cast<const uint2*>(lm + 32 * cb + 8 * G);
+          const float mean[4] = {f16_bits_to_f32(hm.x & 0xffffu), f16_bits_to_f32(hm.x >> 16),
+                                 f16_bits_to_f32(hm.y & 0xffffu), f16_bits_to_f32(hm.y >> 16)};
+#pragma unroll
+          for (int r = 0; r < 4; ++r) O[qg][cb][r] = __builtin_fmaf(ms[0], mean[r], O[qg][cb][r]);
+        }
+      }
+    }
+  }
+};
+
+template <int D, bool SMOOTH, bool DUMP, int OUT>
+__global__ __launch_bounds__(kThreadsPerBlock, 2) void attn_kernel(AttnArgs a) {
+  constexpr int KB = kTile * D, VB = D * kTile;
+  __shared__ __attribute__((aligned(16))) uint8_t lds0[KB + VB];
+  __shared__ __attribute__((aligned(16))) uint8_t lds1[KB + VB];
+  __shared__ __attribute__((aligned(16))) uint8_t meta0[512];
+  __shared__ __attribute__((aligned(16))) uint8_t meta1[512];
+
+  // XCD-aware order: the hardware deals blocks round-robin over 8 XCDs; give
+  // each XCD a contiguous range of (head, query block) so its L2 serves one head.
+  const int64_t nb = gridDim.x, p = blockIdx.x;
+  const int64_t per = nb / 8, rem = nb % 8, xcd = p % 8, idx = p / 8;
+  const int64_t logical = (xcd < rem ? xcd * (per + 1) : rem * (per + 1) + (xcd - rem) * per) + idx;
+  const int64_t bh = logical / a.qblocks, qb = logical % a.qblocks;
+
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  Wave<D, SMOOTH, DUMP> w;
+  w.G = lane >> 4;
+  w.li = lane & 15;
+  w.bh_ = bh;
+  // Lane-constant LDS offsets.
+  const int kr = 8 * ((w.li & 3) >> 1) + 2 * (w.li >> 2) + (w.li & 1);
+#pragma unroll
+  for (int ds = 0; ds < Wave<D, SMOOTH, DUMP>::DS; ++ds)
+    w.koff[ds] = kr * D + ((((D == 128) ? 4 * ds : 0) + w.G) ^ swz_k<D>(kr)) * 16;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) w.voff[h] = w.li * kTile + (((2 * w.G + h) ^ swz_v(w.li)) * 16);
+
+  // Q fragments (B operand) and per-row scales.
+#pragma unroll
+  for (int qg = 0; qg < 2; ++qg) {
+    const int64_t r = qb * kRowsPerBlock + wave * 32 + qg * 16 + w.li;
+    w.row[qg] = r;
+    const int64_t si = (r / 16) * 8 + r % 8;
+    w.qsv[qg] = si < a.qs_len ? a.qs[bh * a.qs_len + si] : 1.0f;
+#pragma unroll
+    for (int ds = 0; ds < Wave<D, SMOOTH, DUMP>::DS; ++ds) {
+      if (r < a.Nq) w.qf[qg][ds] = *reinterpret_cast<const v4i*>(a.q8 + (bh * a.Nq + r) * D + ds * 64 + w.G * 16);
+      else w.qf[qg][ds] = v4i{0, 0, 0, 0};
+    }
+    w.m[qg] = -5000000.0f;
+    w.den[qg] = 0.0f;
+#pragma unroll
+    for (int cb = 0; cb < Wave<D, SMOOTH, DUMP>::CB; ++cb) w.O[qg][cb] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+  }
+
+  TileLoader<D, SMOOTH> ld;
+  ld.init(a.tiles);
+  ld.issue(a, bh, 0, lds0, lds0 + KB, meta0);
+  // Tiles before the last, two per iteration so each buffer is a fixed LDS object.
+  const int64_t body = a.tiles - 1;
+  int64_t t = 0;
+  for (; t + 2 <= body; t += 2) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    ld.issue(a, bh, t + 1, lds1, lds1 + KB, meta1);
+    w.template tile<false>(a, t, lds0, lds0 + KB, meta0);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    ld.issue(a, bh, t + 2, lds0, lds0 + KB, meta0);
+    w.template tile<false>(a, t + 1, lds1, lds1 + KB, meta1);
+  }
+  if (t < body) {  // odd count of body tiles: one more from buffer 0, last tile lands in buffer 1
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    ld.issue(a, bh, t + 1, lds1, lds1 + KB, meta1);
+    w.template tile<false>(a, t, lds0, lds0 + KB, meta0);
+    ++t;
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (t & 1) w.template tile<true>(a, t, lds1, lds1 + KB, meta1);
+  else w.template tile<true>(a, t, lds0, lds0 + KB, meta0);
+
+  // ---- epilogue: normalise, per-channel V scale, store 4 channels per lane and block
+  const int64_t b = bh / a.H, h = bh % a.H;
+#pragma unroll
+  for (int qg = 0; qg < 2; ++qg) {
+    if (w.row[qg] >= a.Nq) continue;
+    const float inv = 1.0f / w.den[qg];
+    uint16_t* out = static_cast<uint16_t*>(a.out) + b * a.osb + h * a.osh + w.row[qg] * a.osn;
+#pragma unroll
+    for (int cb = 0; cb < Wave<D, SMOOTH, DUMP>::CB; ++cb) {
+      const int ch = 16 * cb + 4 * w.G;
+      const float4 sc = *reinterpret_cast<const float4*>(a.vs + bh * D + ch);
+      const float y0 = w.O[qg][cb][0] * inv * sc.x, y1 = w.O[qg][cb][1] * inv * sc.y;
+      const float y2 = w.O[qg][cb][2] * inv * sc.z, y3 = w.O[qg][cb][3] * inv * sc.w;
+      uint2 packed;
+      if constexpr (OUT == VCX_BFLOAT16) {
+        packed.x = f32_to_bf16_bits(y0) | (f32_to_bf16_bits(y1) << 16);
+        packed.y = f32_to_bf16_bits(y2) | (f32_to_bf16_bits(y3) << 16);
+      } else {
+        packed.x = f32_to_f16_bits(y0) | (f32_to_f16_bits(y1) << 16);
+        packed.y = f32_to_f16_bits(y2) | (f32_to_f16_bits(y3) << 16);
+      }
+      *reinterpret_cast<uint2*>(out + ch) = packed;
+    }
+  }
+}
+
+template <int D, bool SMOOTH, bool DUMP, int OUT>
+int launch(const AttnArgs& a, int64_t nblocks, hipStream_t st) {
+  attn_kernel<D, SMOOTH, DUMP, OUT><<<dim3(static_cast<unsigned>(nblocks)), kThreadsPerBlock, 0, st>>>(a);
+  return check_launch("attn_kernel");
+}
+
+template <int D, bool SMOOTH>
+int launch_out(const AttnArgs& a, int64_t nblocks, bool dump, int out_dtype, hipStream_t st) {
+  if (dump) {
+    return out_dtype == VCX_BFLOAT16 ? launch<D, SMOOTH, true, VCX_BFLOAT16>(a, nblocks, st)
+                                     : launch<D, SMOOTH, true, VCX_FLOAT16>(a, nblocks, st);
+  }
+  return out_dtype == VCX_BFLOAT16 ? launch<D, SMOOTH, false, VCX_BFLOAT16>(a, nblocks, st)
+                                   : launch<D, SMOOTH, false, VCX_FLOAT16>(a, nblocks, st);
+}
+
+}  // namespace
+}  // namespace vcx
+
+using namespace vcx;
+
+extern "C" int vcx_attention_fwd(const int8_t* q8, const int8_t* k8, const uint8_t* v8, const float* qs,
+                                 const float* ks, const float* vs, const uint16_t* means, int64_t B,
+                                 int64_t H, int64_t Nq, int64_t Nk, int64_t D, int expcast,
+                                 int block_values, int channel_scale, float sm_scale, int out_dtype,
+                                 void* out, int64_t o_sb, int64_t o_sh, int64_t o_sn, uint8_t* p_dump,
+                                 int64_t p_row_begin, int64_t p_row_end, void* stream) {
+  VCX_REQUIRE(B >= 1 && H >= 1 && Nq >= 1 && Nk >= 1, "B, H, Nq, Nk must be positive");
+  VCX_REQUIRE(D == 64 || D == 128, "D must be 64 or 128");
+  VCX_REQUIRE(B * H <= 65535, "B*H exceeds 65535");
+  VCX_REQUIRE(Nq < (int64_t(1) << 30) && Nk < (int64_t(1) << 30), "sequence too long");
+  if (expcast != 1) return fail(VCX_EUNSUPPORTED, "only the ExpCast probability encoding is implemented");
+  if (block_values && !channel_scale)
+    return fail(VCX_EUNSUPPORTED, "per-block V scales are not implemented in the fused kernel");
+  VCX_REQUIRE(out_dtype == VCX_FLOAT16 || out_dtype == VCX_BFLOAT16, "out_dtype must be float16 or bfloat16");
+  VCX_REQUIRE(std::isfinite(sm_scale) && sm_scale > 0.0f, "sm_scale must be positive and finite FP32");
+  VCX_REQUIRE(q8 && k8 && v8 && qs && ks && vs && out, "null tensor pointer");
+  VCX_REQUIRE(!block_values || means, "means must be non-null with block values");
+  VCX_REQUIRE(aligned(q8, 16) && aligned(k8, 16) && aligned(v8, 16), "q8/k8/v8 must be 16-byte aligned");
+  VCX_REQUIRE(aligned(qs, 4) && aligned(ks, 4) && aligned(vs, 16), "scale pointer alignment (vs needs 16 bytes)");
+  VCX_REQUIRE(!block_values || aligned(means, 8), "means must be 8-byte aligned");
+  VCX_REQUIRE(aligned(out, 8) && o_sb % 4 == 0 && o_sh % 4 == 0 && o_sn % 4 == 0 && o_sn >= D && o_sb >= 0 &&
+                  o_sh >= 0,
+              "out must be 8-byte aligned with strides that are multiples of 4 elements and sn >= D");
+  if (p_dump) {
+    VCX_REQUIRE(p_row_begin >= 0 && p_row_begin < p_row_end && p_row_end <= Nq, "invalid P dump row range");
+  }
+  AttnArgs a{};
+  a.q8 = q8; a.k8 = k8; a.v8 = v8; a.qs = qs; a.ks = ks; a.vs = vs; a.means = means; a.out = out;
+  a.osb = o_sb; a.osh = o_sh; a.osn = o_sn;
+  a.H = H; a.Nq = Nq; a.Nk = Nk; a.tiles = cdiv(Nk, kTile); a.qblocks = cdiv(Nq, kRowsPerBlock);
+  a.qs_len = cdiv(Nq, 64) * 32; a.sm = sm_scale;
+  a.pdump = p_dump; a.prow0 = p_row_begin; a.prow1 = p_row_end;
+  const int64_t nblocks = B * H * a.qblocks;
+  VCX_REQUIRE(nblocks < (int64_t(1) << 31), "too many blocks");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const bool dump = p_dump != nullptr;
+  if (D == 128) {
+    return block_values ? launch_out<128, true>(a, nblocks, dump, out_dtype, st)
+                        : launch_out<128, false>(a, nblocks, dump, out_dtype, st);
+  }
+  return block_values ? launch_out<64, true>(a, nblocks, dump, out_dtype, st)
+                      : launch_out<64, false>(a, nblocks, dump, out_dtype, st);
+}
+
+extern "C" int vcx_kernel_resources(int64_t D, int block_values, int64_t* out) {
+  VCX_REQUIRE(out != nullptr, "out is null");
+  VCX_REQUIRE(D == 64 || D == 128, "D must be 64 or 128");
+  hipFuncAttributes attr{};
+  const void* fn;
+  if (D == 128) fn = block_values ? reinterpret_cast<const void*>(&attn_kernel<128, true, false, VCX_BFLOAT16>)
+                                  : reinterpret_cast<const void*>(&attn_kernel<128, false, false, VCX_BFLOAT16>);
+  else fn = block_values ? reinterpret_cast<const void*>(&attn_kernel<64, true, false, VCX_BFLOAT16>)
+                         : reinterpret_cast<const void*>(&attn_kernel<64, false, false, VCX_BFLOAT16>);
+  hipError_t e = hipFuncGetAttributes(&attr, fn);
+  if (e != hipSuccess) return fail(VCX_EHIP, "hipFuncGetAttributes: %s", hipGetErrorString(e));
+  out[0] = attr.numRegs;
+  out[1] = 0;
+  out[2] = static_cast<int64_t>(attr.sharedSizeBytes);
+  out[3] = 0;
+  out[4] = attr.maxThreadsPerBlock;
+  out[5] = static_cast<int64_t>(attr.localSizeBytes);
+  return VCX_OK;
+}

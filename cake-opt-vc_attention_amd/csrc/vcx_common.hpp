@@ -1,0 +1,118 @@
+// Shared host/device helpers for the gfx950 sageattn_vc kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdint>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "../../include/vcx.h"
+
+namespace vcx {
+
+// ------------------------------------------------------------------ errors
+
+// Per-thread message behind vcx_last_error().
+std::string& last_error();
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+// Record the pending launch error of the last kernel (if any).
+int check_launch(const char* what);
+
+#define VCX_REQUIRE(cond, ...)                              \
+  do {                                                      \
+    if (!(cond)) return ::vcx::fail(VCX_EINVAL, __VA_ARGS__); \
+  } while (0)
+
+#define VCX_LAUNCHED(what)                      \
+  do {                                          \
+    int vcx_rc_ = ::vcx::check_launch(what);    \
+    if (vcx_rc_) return vcx_rc_;                \
+  } while (0)
+
+inline bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// ------------------------------------------------------------------ layout
+
+constexpr int kTile = 128;  // keys per tile (the reference's CTA_K and V block size)
+
+// Storage position p (0..127) inside a V tile -> token offset. Lane group G = p/32
+// of the fused kernel owns byte b = p%32 of its FP8 MFMA operand, which the QK
+// accumulator layout fills with key 16*(b/4) + 8*((b/2)%2) + 2*G + b%2.
+__host__ __device__ inline int value_token(int p) {
+  int G = p >> 5, b = p & 31;
+  return 16 * (b >> 2) + 8 * ((b >> 1) & 1) + 2 * G + (b & 1);
+}
+// Inverse of value_token.
+__host__ __device__ inline int value_position(int key) {
+  return 32 * ((key & 7) >> 1) + 4 * (key >> 4) + 2 * ((key >> 3) & 1) + (key & 1);
+}
+
+// ------------------------------------------------------------------ device formats
+
+__device__ inline float bf16_bits_to_f32(uint32_t b) { return __uint_as_float(b << 16); }
+
+__device__ inline float f16_bits_to_f32(uint32_t b) {
+  _Float16 h;
+  uint16_t s = static_cast<uint16_t>(b);
+  __builtin_memcpy(&h, &s, 2);
+  return static_cast<float>(h);
+}
+
+// IEEE RN-even float -> bfloat16 bits (NaN kept quiet).
+__device__ inline uint32_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return ((u >> 16) | 0x40u) & 0xffffu;
+  return ((u + 0x7fffu + ((u >> 16) & 1u)) >> 16) & 0xffffu;
+}
+
+// IEEE RN-even float -> binary16 bits (v_cvt_f16_f32 under the default RNE mode).
+__device__ inline uint32_t f32_to_f16_bits(float f) {
+  _Float16 h = static_cast<_Float16>(f);
+  uint16_t s;
+  __builtin_memcpy(&s, &h, 2);
+  return s;
+}
+
+template <int DT>
+__device__ inline float in_to_f32(uint32_t bits) {
+  if constexpr (DT == VCX_BFLOAT16) return bf16_bits_to_f32(bits);
+  else return f16_bits_to_f32(bits);
+}
+template <int DT>
+__device__ inline uint32_t f32_to_in(float f) {
+  if constexpr (DT == VCX_BFLOAT16) return f32_to_bf16_bits(f);
+  else return f32_to_f16_bits(f);
+}
+template <int DT>
+__device__ inline float round_in(float f) { return in_to_f32<DT>(f32_to_in<DT>(f)); }
+
+// OCP E4M3 with saturation: clamp to +-448 then the gfx950 conversion, which
+// rounds to nearest even (checked exhaustively on the E4M3 boundaries against
+// the CPU oracle by the convert probe).
+__device__ inline uint32_t e4m3_sat(float x) {
+  float y = fminf(448.0f, fmaxf(-448.0f, x));
+  return static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(y, 0.0f, 0, false)) & 0xffu;
+}
+
+// ExpCast constants (exact fp32 values of the reference, expcast.cuh:7).
+constexpr float kExpA = 11.541560173034668f;
+constexpr float kExpB = 119.6500015258789f;
+
+// Sage INT8 scale and code for one group (quant_per_thread.py:41-44, IEEE division).
+__device__ inline float int8_scale(float amax) { return __fadd_rn(__fdiv_rn(amax, 127.0f), 1e-7f); }
+__device__ inline int int8_code(float x, float s) {
+  float y = __fdiv_rn(x, s);
+  y = __fadd_rn(y, y >= 0.0f ? 0.5f : -0.5f);
+  return static_cast<int>(truncf(y));
+}
+
+// ------------------------------------------------------------------ wave helpers
+
+__device__ inline float wave_xor_max(float v, int mask) { return fmaxf(v, __shfl_xor(v, mask, 64)); }
+
+}  // namespace vcx

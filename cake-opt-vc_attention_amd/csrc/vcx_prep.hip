@@ -1,0 +1,565 @@
+// Preprocessing kernels for sageattn_vc on gfx950: K channel mean, Sage
+// per-thread INT8 Q/K, V E4M3 (per-channel amax or 128-token block-mean
+// smoothing), ExpCast and conversion probes, plus their C-ABI entry points.
+//
+// All kernels are HBM-bound streaming passes. A 128-token tile is handled by
+// 256 threads: thread (kk = tid/16, c = tid%16) owns channels [c*CPT, c*CPT+CPT)
+// (CPT = D/16) of the keys kk + 16*i, i = 0..7, loaded as one 16-byte (D128)
+// or 8-byte (D64) vector per key. Every fp64 tile sum uses the same fixed
+// tree: sequential over i, then lanes xor 16, xor 32, then (w0+w1)+(w2+w3).
+#include "vcx_common.hpp"
+
+namespace vcx {
+namespace {
+
+constexpr int kThreads = 256;
+
+template <int D>
+struct Row {
+  static constexpr int CPT = D / 16;  // channels per thread
+  uint32_t w[CPT / 2];                // packed 16-bit inputs
+};
+
+// Load CPT 16-bit values of token `tok` (already permuted) for chunk c.
+template <int D>
+__device__ inline void load_row(const uint16_t* base, int64_t sn, int64_t tok, int c, Row<D>& r) {
+  const uint16_t* p = base + tok * sn + c * Row<D>::CPT;
+  if constexpr (D == 128) {
+    uint4 v = *reinterpret_cast<const uint4*>(p);
+    r.w[0] = v.x; r.w[1] = v.y; r.w[2] = v.z; r.w[3] = v.w;
+  } else {
+    uint2 v = *reinterpret_cast<const uint2*>(p);
+    r.w[0] = v.x; r.w[1] = v.y;
+  }
+}
+
+template <int DT, int D>
+__device__ inline float row_val(const Row<D>& r, int j) {
+  uint32_t bits = (r.w[j >> 1] >> ((j & 1) * 16)) & 0xffffu;
+  return in_to_f32<DT>(bits);
+}
+
+__device__ inline int64_t source_token(const int64_t* perm, int64_t bh, int64_t n, int64_t key) {
+  return perm ? perm[bh * n + key] : key;
+}
+
+// Per-head base pointer of a strided [B,H,N,D] tensor.
+__device__ inline const uint16_t* head_base(const void* x, int64_t bh, int64_t H, int64_t sb, int64_t sh) {
+  int64_t b = bh / H, h = bh % H;
+  return reinterpret_cast<const uint16_t*>(x) + b * sb + h * sh;
+}
+
+// Fixed fp64 tree over the 16 key-lanes of a tile (see file header). `red` is
+// LDS [4][D]; the result for channel ch is returned to threads tid < D.
+template <int D>
+__device__ inline void tile_tree(double (&a)[D / 16], double* red, double* out_ch) {
+  constexpr int CPT = D / 16;
+  int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, c = tid & 15;
+#pragma unroll
+  for (int j = 0; j < CPT; ++j) {
+    double b = a[j] + __shfl_xor(a[j], 16, 64);
+    a[j] = b + __shfl_xor(b, 32, 64);
+  }
+  if (lane < 16)
+#pragma unroll
+    for (int j = 0; j < CPT; ++j) red[w * D + c * CPT + j] = a[j];
+  __syncthreads();
+  if (tid < D) *out_ch = (red[tid] + red[D + tid]) + (red[2 * D + tid] + red[3 * D + tid]);
+}
+
+// ---------------------------------------------------------------- tile statistics
+
+enum StatsMode { kKSum = 0, kVAmax = 1, kVSmooth = 2 };
+
+// grid (tiles, B*H), 256 threads.
+//  kKSum:    sum[bh][tile][ch] = fp64 tile-tree sum of K
+//  kVAmax:   amax[bh][tile][ch] = max |V|
+//  kVSmooth: mean[bh][tile][ch] = RN_f32(tile-tree sum / count),
+//            peak[bh][tile][ch] = max |RN(V - mean)| over valid tokens
+template <int DT, int D, int MODE>
+__global__ __launch_bounds__(kThreads) void tile_stats_kernel(
+    const void* x, int64_t H, int64_t n, int64_t sb, int64_t sh, int64_t sn, const int64_t* perm,
+    double* sum_out, float* f_out0, float* f_out1) {
+  constexpr int CPT = D / 16;
+  __shared__ double red[4 * D];
+  __shared__ float fred[4 * D];
+  __shared__ float mean_sh[D];
+  const int64_t tile = blockIdx.x, bh = blockIdx.y, tiles = gridDim.x;
+  const int tid = threadIdx.x, kk = tid >> 4, c = tid & 15, lane = tid & 63, w = tid >> 6;
+  const uint16_t* base = head_base(x, bh, H, sb, sh);
+  float v[8][CPT];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    int64_t key = tile * kTile + kk + 16 * i;
+    if (key < n) {
+      Row<D> r;
+      load_row<D>(base, sn, source_token(perm, bh, n, key), c, r);
+#pragma unroll
+      for (int j = 0; j < CPT; ++j) v[i][j] = row_val<DT, D>(r, j);
+    } else {
+#pragma unroll
+      for (int j = 0; j < CPT; ++j) v[i][j] = 0.0f;
+    }
+  }
+  const int64_t meta = (bh * tiles + tile) * D;
+  if constexpr (MODE == kVAmax) {
+    float m[CPT];
+#pragma unroll
+    for (int j = 0; j < CPT; ++j) {
+      m[j] = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) m[j] = fmaxf(m[j], fabsf(v[i][j]));
+      m[j] = wave_xor_max(m[j], 16);
+      m[j] = wave_xor_max(m[j], 32);
+    }
+    if (lane < 16)
+#pragma unroll
+      for (int j = 0; j < CPT; ++j) fred[w * D + c * CPT + j] = m[j];
+    __syncthreads();
+    if (tid < D) f_out0[meta + tid] = fmaxf(fmaxf(fred[tid], fred[D + tid]), fmaxf(fred[2 * D + tid], fred[3 * D + tid]));
+    return;
+  } else {
+    double a[CPT];
+#pragma unroll
+    for (int j = 0; j < CPT; ++j) {
+      a[j] = 0.0;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) a[j] = __dadd_rn(a[j], static_cast<double>(v[i][j]));
+    }
+    double total;
+    tile_tree<D>(a, red, &total);
+    if constexpr (MODE == kKSum) {
+      if (tid < D) sum_out[meta + tid] = total;
+      return;
+    } else {
+      const int64_t count = n - tile * kTile < kTile ? n - tile * kTile : kTile;
+      if (tid < D) {
+        float mu = static_cast<float>(__ddiv_rn(total, static_cast<double>(count)));
+        mean_sh[tid] = mu;
+        f_out0[meta + tid] = mu;
+      }
+      __syncthreads();
+      float pk[CPT];
+#pragma unroll
+      for (int j = 0; j < CPT; ++j) {
+        float mu = mean_sh[c * CPT + j];
+        pk[j] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+          if (tile * kTile + kk + 16 * i < n) pk[j] = fmaxf(pk[j], fabsf(__fsub_rn(v[i][j], mu)));
+        pk[j] = wave_xor_max(pk[j], 16);
+        pk[j] = wave_xor_max(pk[j], 32);
+      }
+      if (lane < 16)
+#pragma unroll
+        for (int j = 0; j < CPT; ++j) fred[w * D + c * CPT + j] = pk[j];
+      __syncthreads();
+      if (tid < D)
+        f_out1[meta + tid] = fmaxf(fmaxf(fred[tid], fred[D + tid]), fmaxf(fred[2 * D + tid], fred[3 * D + tid]));
+    }
+  }
+}
+
+// ---------------------------------------------------------------- finalize
+
+// grid (B*H), D threads. km = RN_in(RN_f32(sum over tiles / n)); also the
+// widened value for the K quantizer and, optionally, the caller's km_out.
+template <int DT>
+__global__ void k_mean_kernel(const double* sums, int64_t tiles, int64_t n, int D, float* km_f32,
+                              uint16_t* km_out) {
+  const int64_t bh = blockIdx.x;
+  const int ch = threadIdx.x;
+  double s = 0.0;
+  for (int64_t t = 0; t < tiles; ++t) s = __dadd_rn(s, sums[(bh * tiles + t) * D + ch]);
+  float mean = static_cast<float>(__ddiv_rn(s, static_cast<double>(n)));
+  uint32_t bits = f32_to_in<DT>(mean);
+  km_f32[bh * D + ch] = in_to_f32<DT>(bits);
+  if (km_out) km_out[bh * D + ch] = static_cast<uint16_t>(bits);
+}
+
+// grid (B*H), D threads. Smoothing off: vs = RN(amax/448), recip = RN(448/amax)
+// (0 for a zero channel). Smoothing on (channel scale): vs = max(P>0 ? RN(P/448) : 1, RN(M/65504)).
+__global__ void v_scale_kernel(const float* a0, const float* a1, int64_t tiles, int D, int smooth,
+                               float* vs, float* recip) {
+  const int64_t bh = blockIdx.x;
+  const int ch = threadIdx.x;
+  if (!smooth) {
+    float amax = 0.0f;
+    for (int64_t t = 0; t < tiles; ++t) amax = fmaxf(amax, a0[(bh * tiles + t) * D + ch]);
+    vs[bh * D + ch] = amax > 0.0f ? __fdiv_rn(amax, 448.0f) : 0.0f;
+    recip[bh * D + ch] = amax > 0.0f ? __fdiv_rn(448.0f, amax) : 0.0f;
+  } else {
+    float P = 0.0f, M = 0.0f;
+    for (int64_t t = 0; t < tiles; ++t) {
+      P = fmaxf(P, a1[(bh * tiles + t) * D + ch]);
+      M = fmaxf(M, fabsf(a0[(bh * tiles + t) * D + ch]));
+    }
+    float s = P > 0.0f ? __fdiv_rn(P, 448.0f) : 1.0f;
+    vs[bh * D + ch] = fmaxf(s, __fdiv_rn(M, 65504.0f));
+  }
+}
+
+// ---------------------------------------------------------------- Q INT8
+
+// grid (ceil(n/64), B*H), 256 threads. Groups of rows {16g+t, 16g+t+8}; each
+// group is 32 lanes (16 per row) of one wave; 4 passes of 8 groups.
+template <int DT, int D>
+__global__ __launch_bounds__(kThreads) void quant_q_kernel(const void* q, int64_t H, int64_t n,
+                                                           int64_t sb, int64_t sh, int64_t sn,
+                                                           int8_t* q8, float* qs) {
+  constexpr int CPT = D / 16;
+  const int64_t blk = blockIdx.x, bh = blockIdx.y;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, c = lane & 15, sel = (lane >> 4) & 1;
+  const uint16_t* base = head_base(q, bh, H, sb, sh);
+  const int64_t qs_len = (n + 63) / 64 * 32;
+#pragma unroll
+  for (int pass = 0; pass < 4; ++pass) {
+    const int grp = pass * 8 + w * 2 + (lane >> 5);  // 0..31 inside the 64-row block
+    const int g = grp >> 3, t = grp & 7;
+    const int64_t row = blk * 64 + 16 * g + t + 8 * sel;
+    float x[CPT];
+    if (row < n) {
+      Row<D> r;
+      load_row<D>(base, sn, row, c, r);
+#pragma unroll
+      for (int j = 0; j < CPT; ++j) x[j] = row_val<DT, D>(r, j);
+    } else {
+#pragma unroll
+      for (int j = 0; j < CPT; ++j) x[j] = 0.0f;
+    }
+    float amax = 0.0f;
+#pragma unroll
+    for (int j = 0; j < CPT; ++j) amax = fmaxf(amax, fabsf(x[j]));
+#pragma unroll
+    for (int m = 1; m < 32; m <<= 1) amax = wave_xor_max(amax, m);
+    const float s = int8_scale(amax);
+    if (row < n) {
+      uint32_t packed[CPT / 4];
+#pragma unroll
+      for (int j = 0; j < CPT / 4; ++j) {
+        uint32_t wv = 0;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) wv |= (static_cast<uint32_t>(int8_code(x[4 * j + e], s)) & 0xffu) << (8 * e);
+        packed[j] = wv;
+      }
+      int8_t* dst = q8 + (bh * n + row) * D + c * CPT;
+      if constexpr (CPT == 8) *reinterpret_cast<uint2*>(dst) = make_uint2(packed[0], packed[1]);
+      else *reinterpret_cast<uint32_t*>(dst) = packed[0];
+    }
+    if ((lane & 31) == 0) qs[bh * qs_len + (blk * 4 + g) * 8 + t] = s;
+  }
+}
+
+// ---------------------------------------------------------------- K INT8
+
+// grid (tiles, B*H), 256 threads. Thread (kk, c) holds keys kk+16i, all in
+// scale group g = (kk%8)/2; a group is lanes 0-31 or 32-63 of waves w and w+2.
+template <int DT, int D>
+__global__ __launch_bounds__(kThreads) void quant_k_kernel(const void* k, int64_t H, int64_t n,
+                                                           int64_t sb, int64_t sh, int64_t sn,
+                                                           const int64_t* perm, const float* km,
+                                                           int8_t* k8, float* ks) {
+  constexpr int CPT = D / 16;
+  __shared__ float gred[4][2];
+  const int64_t tile = blockIdx.x, bh = blockIdx.y, tiles = gridDim.x;
+  const int tid = threadIdx.x, kk = tid >> 4, c = tid & 15, lane = tid & 63, w = tid >> 6;
+  const uint16_t* base = head_base(k, bh, H, sb, sh);
+  float mean[CPT];
+#pragma unroll
+  for (int j = 0; j < CPT; ++j) mean[j] = km[bh * D + c * CPT + j];
+  float v[8][CPT];
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    int64_t key = tile * kTile + kk + 16 * i;
+    if (key < n) {
+      Row<D> r;
+      load_row<D>(base, sn, source_token(perm, bh, n, key), c, r);
+#pragma unroll
+      for (int j = 0; j < CPT; ++j) {
+        v[i][j] = round_in<DT>(__fsub_rn(row_val<DT, D>(r, j), mean[j]));
+        amax = fmaxf(amax, fabsf(v[i][j]));
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < CPT; ++j) v[i][j] = 0.0f;
+    }
+  }
+#pragma unroll
+  for (int m = 1; m < 32; m <<= 1) amax = wave_xor_max(amax, m);
+  if ((lane & 31) == 0) gred[w][lane >> 5] = amax;
+  __syncthreads();
+  amax = fmaxf(gred[w][lane >> 5], gred[w ^ 2][lane >> 5]);
+  const float s = int8_scale(amax);
+  const int g = (kk & 7) >> 1;
+  if (w < 2 && (lane & 31) == 0) ks[bh * tiles * 4 + tile * 4 + g] = s;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    int64_t key = tile * kTile + kk + 16 * i;
+    if (key >= n) continue;
+    uint32_t packed[CPT / 4];
+#pragma unroll
+    for (int j = 0; j < CPT / 4; ++j) {
+      uint32_t wv = 0;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) wv |= (static_cast<uint32_t>(int8_code(v[i][4 * j + e], s)) & 0xffu) << (8 * e);
+      packed[j] = wv;
+    }
+    int8_t* dst = k8 + (bh * n + key) * D + c * CPT;
+    if constexpr (CPT == 8) *reinterpret_cast<uint2*>(dst) = make_uint2(packed[0], packed[1]);
+    else *reinterpret_cast<uint32_t*>(dst) = packed[0];
+  }
+}
+
+// ---------------------------------------------------------------- V E4M3
+
+// grid (tiles, B*H), 256 threads. Bytes are staged in LDS as [D][128] storage
+// positions, then written as 16-byte rows of the [D][tiles*128] payload.
+//  SMOOTH = 0: byte = e4m3(RN(x * recip[ch])), zero channel -> 0.
+//  SMOOTH = 1: byte = e4m3(RN(RN(x - mean_t) / s)), with s the channel scale
+//              (CHANNEL) or the tile's block scale, written with the fp16 means.
+template <int DT, int D, int SMOOTH, int CHANNEL>
+__global__ __launch_bounds__(kThreads) void quant_v_kernel(
+    const void* vin, int64_t H, int64_t n, int64_t sb, int64_t sh, int64_t sn, const int64_t* perm,
+    const float* scale_or_recip, const float* tile_mean, const float* tile_peak, uint8_t* v8,
+    float* vs_block, uint16_t* means) {
+  constexpr int CPT = D / 16;
+  __shared__ uint8_t stage[D * kTile];
+  __shared__ float sc_sh[D], mu_sh[D];
+  const int64_t tile = blockIdx.x, bh = blockIdx.y, tiles = gridDim.x;
+  const int tid = threadIdx.x, kk = tid >> 4, c = tid & 15;
+  const uint16_t* base = head_base(vin, bh, H, sb, sh);
+  if (tid < D) {
+    const int64_t meta = (bh * tiles + tile) * D + tid;
+    if constexpr (SMOOTH) {
+      float mu = tile_mean[meta], s;
+      if constexpr (CHANNEL) {
+        s = scale_or_recip[bh * D + tid];
+      } else {
+        float pk = tile_peak[meta];
+        s = pk > 0.0f ? __fdiv_rn(pk, 448.0f) : 1.0f;
+        s = fmaxf(s, __fdiv_rn(fabsf(mu), 65504.0f));
+        vs_block[meta] = s;
+      }
+      mu_sh[tid] = mu;
+      sc_sh[tid] = s;
+      means[meta] = static_cast<uint16_t>(f32_to_f16_bits(__fdiv_rn(mu, s)));
+    } else {
+      sc_sh[tid] = scale_or_recip[bh * D + tid];
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int kt = kk + 16 * i;
+    const int64_t key = tile * kTile + kt;
+    const int pos = value_position(kt);
+    if (key < n) {
+      Row<D> r;
+      load_row<D>(base, sn, source_token(perm, bh, n, key), c, r);
+#pragma unroll
+      for (int j = 0; j < CPT; ++j) {
+        const int ch = c * CPT + j;
+        float x = row_val<DT, D>(r, j);
+        uint32_t byte;
+        if constexpr (SMOOTH) {
+          byte = e4m3_sat(__fdiv_rn(__fsub_rn(x, mu_sh[ch]), sc_sh[ch]));
+        } else {
+          float rc = sc_sh[ch];
+          byte = rc == 0.0f ? 0u : e4m3_sat(__fmul_rn(x, rc));
+        }
+        stage[ch * kTile + pos] = static_cast<uint8_t>(byte);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < CPT; ++j) stage[(c * CPT + j) * kTile + pos] = 0;
+    }
+  }
+  __syncthreads();
+  const int64_t npad = tiles * kTile;
+  for (int s = tid; s < D * 8; s += kThreads) {
+    const int ch = s >> 3, part = s & 7;
+    uint4 val = *reinterpret_cast<const uint4*>(&stage[ch * kTile + part * 16]);
+    *reinterpret_cast<uint4*>(v8 + (bh * D + ch) * npad + tile * kTile + part * 16) = val;
+  }
+}
+
+// ---------------------------------------------------------------- probes
+
+__global__ void expcast_kernel(const float* x, uint8_t* y, int64_t n) {
+  int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  // Same FMA + saturating RNE byte conversion as the fused kernel; the clamps
+  // reproduce the reference's fminf(120, fmaxf(0, u)) for arbitrary inputs.
+  float u = __builtin_fmaf(x[i], kExpA, kExpB);
+  u = fminf(120.0f, fmaxf(0.0f, u));
+  y[i] = static_cast<uint8_t>(__builtin_amdgcn_cvt_pk_u8_f32(u, 0, 0u) & 0xffu);
+}
+
+__global__ void convert_probe_kernel(const float* x, uint8_t* u8, uint8_t* f8, int64_t n) {
+  int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  u8[i] = static_cast<uint8_t>(__builtin_amdgcn_cvt_pk_u8_f32(x[i], 0, 0u) & 0xffu);
+  f8[i] = static_cast<uint8_t>(e4m3_sat(x[i]));
+}
+
+// ---------------------------------------------------------------- host helpers
+
+struct Strided {
+  const void* p;
+  int64_t sb, sh, sn;
+};
+
+int check_input(const char* name, const void* p, int64_t B, int64_t H, int64_t N, int64_t D,
+                int64_t sb, int64_t sh, int64_t sn) {
+  VCX_REQUIRE(p != nullptr, "%s is null", name);
+  VCX_REQUIRE(aligned(p, D == 128 ? 16 : 8), "%s pointer alignment: need %d bytes", name, D == 128 ? 16 : 8);
+  const int64_t vec = D / 16;  // elements per vector load
+  VCX_REQUIRE(sb % vec == 0 && sh % vec == 0 && sn % vec == 0,
+              "%s strides must be multiples of %lld elements", name, (long long)vec);
+  VCX_REQUIRE(sb >= 0 && sh >= 0 && sn >= D, "%s strides invalid (need sn >= D, last dim contiguous)", name);
+  (void)B; (void)H; (void)N;
+  return VCX_OK;
+}
+
+int check_shape(int64_t B, int64_t H, int64_t N, int64_t D) {
+  VCX_REQUIRE(B >= 1 && H >= 1 && N >= 1, "B, H, N must be positive");
+  VCX_REQUIRE(D == 64 || D == 128, "D must be 64 or 128");
+  VCX_REQUIRE(B * H <= 65535, "B*H exceeds 65535");
+  VCX_REQUIRE(N < (int64_t(1) << 31) / 2, "N too large");
+  return VCX_OK;
+}
+
+template <typename F>
+int dispatch(int dtype, int64_t D, F&& f) {
+  if (dtype == VCX_BFLOAT16) {
+    if (D == 128) return f(std::integral_constant<int, VCX_BFLOAT16>(), std::integral_constant<int, 128>());
+    return f(std::integral_constant<int, VCX_BFLOAT16>(), std::integral_constant<int, 64>());
+  }
+  if (D == 128) return f(std::integral_constant<int, VCX_FLOAT16>(), std::integral_constant<int, 128>());
+  return f(std::integral_constant<int, VCX_FLOAT16>(), std::integral_constant<int, 64>());
+}
+
+size_t align_up(size_t x) { return (x + 255) & ~size_t(255); }
+
+}  // namespace
+
+// Workspace layouts (all 256-byte aligned slices).
+size_t ws_prepare_qk(int64_t BH, int64_t N, int64_t D) {
+  int64_t tiles = cdiv(N, kTile);
+  return align_up(sizeof(double) * BH * tiles * D) + align_up(sizeof(float) * BH * D);
+}
+size_t ws_prepare_v(int64_t BH, int64_t N, int64_t D) {
+  int64_t tiles = cdiv(N, kTile);
+  return 2 * align_up(sizeof(float) * BH * tiles * D) + align_up(sizeof(float) * BH * D);
+}
+
+}  // namespace vcx
+
+using namespace vcx;
+
+extern "C" int vcx_prepare_qk_int8(const void* q, const void* k, int dtype, int64_t B, int64_t H,
+                                   int64_t Nq, int64_t Nk, int64_t D, int64_t q_sb, int64_t q_sh,
+                                   int64_t q_sn, int64_t k_sb, int64_t k_sh, int64_t k_sn,
+                                   const int64_t* perm, int8_t* q8, float* qs, int8_t* k8, float* ks,
+                                   void* km_out, void* workspace, size_t workspace_bytes,
+                                   void* stream) {
+  if (int rc = check_shape(B, H, Nq, D)) return rc;
+  if (int rc = check_shape(B, H, Nk, D)) return rc;
+  VCX_REQUIRE(dtype == VCX_FLOAT16 || dtype == VCX_BFLOAT16, "dtype must be float16 or bfloat16");
+  if (int rc = check_input("q", q, B, H, Nq, D, q_sb, q_sh, q_sn)) return rc;
+  if (int rc = check_input("k", k, B, H, Nk, D, k_sb, k_sh, k_sn)) return rc;
+  VCX_REQUIRE(q8 && qs && k8 && ks, "output pointers must be non-null");
+  VCX_REQUIRE(aligned(q8, 8) && aligned(k8, 8), "q8/k8 must be 8-byte aligned");
+  VCX_REQUIRE(aligned(perm, 8) && aligned(km_out, 2), "perm/km_out misaligned");
+  const int64_t BH = B * H, tiles = cdiv(Nk, kTile);
+  VCX_REQUIRE(workspace != nullptr && aligned(workspace, 256), "workspace must be non-null and 256-byte aligned");
+  VCX_REQUIRE(workspace_bytes >= ws_prepare_qk(BH, Nk, D), "workspace too small: need %zu bytes",
+              ws_prepare_qk(BH, Nk, D));
+  auto* ws = static_cast<char*>(workspace);
+  double* ksum = reinterpret_cast<double*>(ws);
+  float* km = reinterpret_cast<float*>(ws + align_up(sizeof(double) * BH * tiles * D));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  return dispatch(dtype, D, [&](auto dt, auto dd) -> int {
+    constexpr int DT = decltype(dt)::value, DD = decltype(dd)::value;
+    quant_q_kernel<DT, DD><<<dim3(cdiv(Nq, 64), BH), kThreads, 0, st>>>(q, H, Nq, q_sb, q_sh, q_sn, q8, qs);
+    VCX_LAUNCHED("quant_q_kernel");
+    tile_stats_kernel<DT, DD, kKSum><<<dim3(tiles, BH), kThreads, 0, st>>>(k, H, Nk, k_sb, k_sh, k_sn, perm,
+                                                                          ksum, nullptr, nullptr);
+    VCX_LAUNCHED("tile_stats_kernel<K>");
+    k_mean_kernel<DT><<<dim3(BH), DD, 0, st>>>(ksum, tiles, Nk, DD, km, static_cast<uint16_t*>(km_out));
+    VCX_LAUNCHED("k_mean_kernel");
+    quant_k_kernel<DT, DD><<<dim3(tiles, BH), kThreads, 0, st>>>(k, H, Nk, k_sb, k_sh, k_sn, perm, km, k8, ks);
+    VCX_LAUNCHED("quant_k_kernel");
+    return VCX_OK;
+  });
+}
+
+extern "C" int vcx_prepare_v_fp8(const void* v, int dtype, int64_t B, int64_t H, int64_t N, int64_t D,
+                                 int64_t v_sb, int64_t v_sh, int64_t v_sn, const int64_t* perm,
+                                 int smooth, int channel_scale, uint8_t* v8, float* vs,
+                                 uint16_t* means, void* workspace, size_t workspace_bytes,
+                                 void* stream) {
+  if (int rc = check_shape(B, H, N, D)) return rc;
+  VCX_REQUIRE(dtype == VCX_FLOAT16 || dtype == VCX_BFLOAT16, "dtype must be float16 or bfloat16");
+  if (int rc = check_input("v", v, B, H, N, D, v_sb, v_sh, v_sn)) return rc;
+  VCX_REQUIRE(v8 && vs, "v8/vs must be non-null");
+  VCX_REQUIRE(aligned(v8, 16), "v8 must be 16-byte aligned");
+  VCX_REQUIRE(!smooth || means != nullptr, "means must be non-null when smoothing");
+  VCX_REQUIRE(aligned(perm, 8), "perm misaligned");
+  const int64_t BH = B * H, tiles = cdiv(N, kTile);
+  VCX_REQUIRE(workspace != nullptr && aligned(workspace, 256), "workspace must be non-null and 256-byte aligned");
+  VCX_REQUIRE(workspace_bytes >= ws_prepare_v(BH, N, D), "workspace too small: need %zu bytes",
+              ws_prepare_v(BH, N, D));
+  auto* ws = static_cast<char*>(workspace);
+  const size_t slice = align_up(sizeof(float) * BH * tiles * D);
+  float* a0 = reinterpret_cast<float*>(ws);
+  float* a1 = reinterpret_cast<float*>(ws + slice);
+  float* recip = reinterpret_cast<float*>(ws + 2 * slice);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  return dispatch(dtype, D, [&](auto dt, auto dd) -> int {
+    constexpr int DT = decltype(dt)::value, DD = decltype(dd)::value;
+    dim3 grid(tiles, BH);
+    if (!smooth) {
+      tile_stats_kernel<DT, DD, kVAmax><<<grid, kThreads, 0, st>>>(v, H, N, v_sb, v_sh, v_sn, perm, nullptr, a0, nullptr);
+      VCX_LAUNCHED("tile_stats_kernel<Vamax>");
+      v_scale_kernel<<<dim3(BH), DD, 0, st>>>(a0, nullptr, tiles, DD, 0, vs, recip);
+      VCX_LAUNCHED("v_scale_kernel");
+      quant_v_kernel<DT, DD, 0, 1><<<grid, kThreads, 0, st>>>(v, H, N, v_sb, v_sh, v_sn, perm, recip, nullptr,
+                                                              nullptr, v8, nullptr, nullptr);
+      VCX_LAUNCHED("quant_v_kernel");
+      return VCX_OK;
+    }
+    tile_stats_kernel<DT, DD, kVSmooth><<<grid, kThreads, 0, st>>>(v, H, N, v_sb, v_sh, v_sn, perm, nullptr, a0, a1);
+    VCX_LAUNCHED("tile_stats_kernel<Vsmooth>");
+    if (channel_scale) {
+      v_scale_kernel<<<dim3(BH), DD, 0, st>>>(a0, a1, tiles, DD, 1, vs, nullptr);
+      VCX_LAUNCHED("v_scale_kernel");
+      quant_v_kernel<DT, DD, 1, 1><<<grid, kThreads, 0, st>>>(v, H, N, v_sb, v_sh, v_sn, perm, vs, a0, a1, v8,
+                                                              nullptr, means);
+    } else {
+      quant_v_kernel<DT, DD, 1, 0><<<grid, kThreads, 0, st>>>(v, H, N, v_sb, v_sh, v_sn, perm, nullptr, a0, a1,
+                                                              v8, vs, means);
+    }
+    VCX_LAUNCHED("quant_v_kernel");
+    return VCX_OK;
+  });
+}
+
+extern "C" int vcx_expcast_codes(const float* x, uint8_t* y, int64_t n, void* stream) {
+  VCX_REQUIRE(n >= 0, "n must be non-negative");
+  if (n == 0) return VCX_OK;
+  VCX_REQUIRE(x && y, "null pointer");
+  expcast_kernel<<<cdiv(n, 256), 256, 0, static_cast<hipStream_t>(stream)>>>(x, y, n);
+  VCX_LAUNCHED("expcast_kernel");
+  return VCX_OK;
+}
+
+extern "C" int vcx_convert_probe(const float* x, uint8_t* u8, uint8_t* f8, int64_t n, void* stream) {
+  VCX_REQUIRE(n >= 0, "n must be non-negative");
+  if (n == 0) return VCX_OK;
+  VCX_REQUIRE(x && u8 && f8, "null pointer");
+  convert_probe_kernel<<<cdiv(n, 256), 256, 0, static_cast<hipStream_t>(stream)>>>(x, u8, f8, n);
+  VCX_LAUNCHED("convert_probe_kernel");
+  return VCX_OK;
+}

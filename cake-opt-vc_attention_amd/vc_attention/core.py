@@ -1,0 +1,192 @@
+"""``vc_attention`` surface with a ``hip`` backend for the sageattn_vc contract.
+
+Mirrors the reference's src/vc_attention/core.py: a frozen ``Config`` with
+validation (core.py:15-65), the request-scoped ``LayoutCache`` of the
+denoising-step schedule (core.py:181-226) and ``attention(...) -> (out,
+counters)`` with backend dispatch (core.py:263-371).
+
+Backends of this build:
+* ``"hip"``: the gfx950 sageattn_vc path (Sage per-thread INT8 QK, ExpCast,
+  FP8 PV, optional V grouping + block smoothing) through libvcx. It requires
+  ``qk_format="int8"`` and the sageattn_vc block geometry (q_block=64,
+  k_quant_block=128, kv_block=128, k_smooth=True, qk_hadamard=False,
+  mean_dtype="float16", expcast=True, quantize=True).
+* ``"reference"``: accepted by ``Config`` for compatibility; ``attention``
+  raises NotImplementedError for it (the reference's eager FP8-QK prototype is
+  a different numerical contract that this build does not carry).
+"""
+import math
+from dataclasses import dataclass
+
+import torch
+
+
+@dataclass(frozen=True)
+class Config:
+    expcast: bool = False
+    v_smooth: bool = False
+    quantize: bool = True
+    q_block: int = 128
+    k_quant_block: int = 256
+    kv_block: int = 128
+    clusters: int = 8
+    iterations: int = 2
+    active_fraction: float = 0.25
+    refresh_interval: int = 4
+    mean_dtype: str = "float16"
+    backend: str = "reference"
+    k_smooth: bool = True
+    qk_hadamard: bool = True
+    qk_format: str = "fp8_block"
+
+    def __post_init__(self):
+        for name in ("expcast", "v_smooth", "quantize", "k_smooth", "qk_hadamard"):
+            if not isinstance(getattr(self, name), bool):
+                raise ValueError(f"{name} must be a bool")
+        for name in ("q_block", "k_quant_block", "kv_block", "clusters", "iterations", "refresh_interval"):
+            value = getattr(self, name)
+            if isinstance(value, bool) or not isinstance(value, int) or value < 1:
+                raise ValueError(f"{name} must be a positive integer")
+        if not math.isfinite(self.active_fraction) or not 0 <= self.active_fraction <= 1:
+            raise ValueError("active_fraction must be in [0, 1]")
+        if self.mean_dtype not in ("float16", "bfloat16", "float32"):
+            raise ValueError("Unsupported mean_dtype")
+        if self.backend not in ("reference", "hip"):
+            raise ValueError("backend must be reference or hip")
+        if self.qk_format not in ("fp8_block", "int8"):
+            raise ValueError("qk_format must be fp8_block or int8")
+        if self.backend == "hip":
+            required = dict(qk_format="int8", quantize=True, expcast=True, q_block=64, k_quant_block=128,
+                            kv_block=128, k_smooth=True, qk_hadamard=False, mean_dtype="float16")
+            bad = [f"{k}={v!r}" for k, v in required.items() if getattr(self, k) != v]
+            if bad:
+                raise ValueError("hip backend implements the sageattn_vc contract; it requires " + ", ".join(bad))
+            if self.clusters > 8:
+                raise ValueError("hip backend groups V into at most 8 clusters")
+
+
+class LayoutCache:
+    """Request-scoped layout state (reference core.py:181-226).
+
+    Only the permutation is cached; means and residuals are recomputed on every
+    call. Grouping always starts from the linspace initialisation (the fused
+    sageattn_vc grouping), so cached centers are not reused as a warm start.
+    """
+
+    def __init__(self, config):
+        self.config = config
+        self._request_id = None
+        self._states = {}
+
+    @property
+    def entries(self):
+        return len(self._states)
+
+    def reset(self):
+        self._request_id = None
+        self._states.clear()
+
+    def layout(self, v, *, step, total_steps, request_id, layer_id, grouping=None):
+        if request_id is None:
+            raise ValueError("A persistent layout cache requires request_id")
+        if total_steps < 1 or not 0 <= step < total_steps:
+            raise ValueError("Invalid denoising step/total_steps")
+        if request_id != self._request_id:
+            self.reset()
+            self._request_id = request_id
+        signature = (tuple(v.shape), str(v.device), v.dtype, total_steps)
+        state = self._states.get(layer_id)
+        if state is not None and (state["signature"] != signature or step < state["step"]):
+            state = None
+            self._states.pop(layer_id, None)
+        active = self.config.v_smooth and step < math.ceil(total_steps * self.config.active_fraction)
+        refresh = active and (state is None or step - state["refresh_step"] >= self.config.refresh_interval)
+        if refresh:
+            if grouping is None:
+                grouping = _hip_grouping(self.config)
+            pi = grouping(v)
+            state = {"signature": signature, "pi": pi, "refresh_step": step, "step": step}
+            self._states[layer_id] = state
+        if state is not None:
+            state["step"] = step
+        return (None if state is None else state["pi"]), active, refresh
+
+
+def _hip_grouping(cfg):
+    import vcx
+
+    return lambda v: vcx.group_values(v, cfg.clusters, cfg.iterations)
+
+
+def _validate(q, k, v, causal, mask):
+    if causal:
+        raise ValueError("This experiment does not support causal attention")
+    if mask is not None:
+        raise ValueError("This experiment does not support a mask/bias")
+    if any(x.ndim != 4 for x in (q, k, v)):
+        raise ValueError("Expected BNSD tensors")
+    if q.shape[:2] != k.shape[:2] or k.shape[:2] != v.shape[:2]:
+        raise ValueError("Batch and heads must match; GQA is not implemented")
+    if k.shape[-2] != v.shape[-2] or q.shape[-1] != k.shape[-1] or v.shape[-1] != q.shape[-1]:
+        raise ValueError("Incompatible Q/K/V shape")
+    if any(0 in x.shape for x in (q, k, v)):
+        raise ValueError("Empty Q/K/V are not supported")
+    if any(x.device != q.device or x.dtype != q.dtype for x in (k, v)):
+        raise ValueError("Q/K/V must have the same device and dtype")
+    if q.dtype not in (torch.float16, torch.bfloat16, torch.float32):
+        raise ValueError("Inputs must be FP16/BF16/FP32 before quantization")
+    if not all(bool(torch.isfinite(x).all()) for x in (q, k, v)):
+        raise ValueError("Q/K/V must be finite")
+
+
+@torch.no_grad()
+def attention(q, k, v, config=None, *, cache=None, step=0, total_steps=1, request_id=None, layer_id=0,
+              scale=None, causal=False, mask=None):
+    """Return (output, counters) (reference core.py:263-371)."""
+    cfg = config or Config()
+    _validate(q, k, v, causal, mask)
+    scale = q.shape[-1] ** -0.5 if scale is None else scale
+    if not math.isfinite(scale) or scale <= 0:
+        raise ValueError("scale must be positive and finite")
+    if cfg.backend != "hip":
+        raise NotImplementedError("the eager FP8-QK reference backend is not part of this build; "
+                                  "use Config(backend='hip', qk_format='int8', ...)")
+    from sageattention_local import vc as sage
+
+    if q.dtype not in (torch.float16, torch.bfloat16):
+        raise ValueError("hip backend requires FP16/BF16 inputs")
+    if q.shape[-1] not in (64, 128):
+        raise ValueError("hip backend requires head_dim 64 or 128")
+    sage._require_gfx950(q.device)
+    if cache is None:
+        cache = LayoutCache(cfg)
+        request_id = "one-shot" if request_id is None else request_id
+    elif cache.config != cfg:
+        raise ValueError("cache.config must match config")
+    pi, active, refreshed = cache.layout(v, step=step, total_steps=total_steps, request_id=request_id,
+                                         layer_id=layer_id)
+    import vcx
+
+    q8, qs, k8, ks, km = vcx.prepare_qk(q, k, pi)
+    v8, vs, means = vcx.prepare_v(v, pi, smooth=active, channel_scale=True)
+    out = vcx.forward(q8, k8, v8, qs, ks, vs, means, True, active, 0 if q.dtype == torch.float16 else 1, scale)
+    return out, {
+        "backend": "hip",
+        "smoothing_active": active,
+        "layout_refreshed": refreshed,
+        "expcast": True,
+        "k_smooth": True,
+        "qk_hadamard": False,
+        "qk_format": "int8",
+        "numerical_contract_version": "sageattn_vc-1",
+        "tiles": math.ceil(q.shape[-2] / 128) * math.ceil(k.shape[-2] / 128),
+        "native_fused_attention": True,
+        "preprocessing_fused": True,
+    }
+
+
+def expcast_codes(shifted_scores):
+    """ExpCast bytes of shifted scores via the gfx950 probe kernel (GPU tensors only)."""
+    import vcx
+
+    return vcx.expcast_codes(shifted_scores)

@@ -1,0 +1,283 @@
+"""ctypes binding of libvcx.so (include/vcx.h) for PyTorch-ROCm tensors.
+
+This module is the only Python code that touches the native library. It
+allocates outputs and workspaces with torch (so the caching allocator and the
+current HIP stream semantics hold), passes raw pointers, shapes and strides to
+the C ABI, and turns nonzero status codes into exceptions. There is no CPU or
+eager fallback: a missing or stale library raises RuntimeError.
+"""
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+import torch
+
+ABI_VERSION = 1
+LIB_PATH = Path(__file__).resolve().parents[1] / "lib" / "libvcx.so"
+
+_OK, _EINVAL, _EUNSUPPORTED, _EHIP = 0, 1, 2, 3
+WS_PREPARE_QK, WS_PREPARE_V, WS_GROUP = 1, 2, 3
+_DTYPE = {torch.float16: 0, torch.bfloat16: 1}
+_lib = None
+
+
+class VcxError(RuntimeError):
+    """A libvcx call returned an error status."""
+
+
+def _declare(L):
+    P, i64, i32, f32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_float
+    L.vcx_abi_version.restype = i32
+    L.vcx_abi_version.argtypes = []
+    L.vcx_last_error.restype = ctypes.c_char_p
+    L.vcx_last_error.argtypes = []
+    L.vcx_value_token.restype = i32
+    L.vcx_value_token.argtypes = [i32]
+    L.vcx_workspace_bytes.restype = i32
+    L.vcx_workspace_bytes.argtypes = [i32, i64, i64, i64, i64, i32, i32, ctypes.POINTER(ctypes.c_size_t)]
+    L.vcx_group_values.restype = i32
+    L.vcx_group_values.argtypes = [P, i32, i64, i64, i64, i64, i64, i64, i64, i32, i32, P, P, P, P,
+                                   ctypes.c_size_t, P]
+    L.vcx_prepare_qk_int8.restype = i32
+    L.vcx_prepare_qk_int8.argtypes = [P, P, i32, i64, i64, i64, i64, i64, i64, i64, i64, i64, i64, i64,
+                                      P, P, P, P, P, P, P, ctypes.c_size_t, P]
+    L.vcx_prepare_v_fp8.restype = i32
+    L.vcx_prepare_v_fp8.argtypes = [P, i32, i64, i64, i64, i64, i64, i64, i64, P, i32, i32, P, P, P, P,
+                                    ctypes.c_size_t, P]
+    L.vcx_attention_fwd.restype = i32
+    L.vcx_attention_fwd.argtypes = [P, P, P, P, P, P, P, i64, i64, i64, i64, i64, i32, i32, i32, f32, i32,
+                                    P, i64, i64, i64, P, i64, i64, P]
+    L.vcx_expcast_codes.restype = i32
+    L.vcx_expcast_codes.argtypes = [P, P, i64, P]
+    L.vcx_convert_probe.restype = i32
+    L.vcx_convert_probe.argtypes = [P, P, P, i64, P]
+    L.vcx_kernel_resources.restype = i32
+    L.vcx_kernel_resources.argtypes = [i64, i32, ctypes.POINTER(ctypes.c_int64)]
+
+
+EXPORTED = ("vcx_abi_version", "vcx_last_error", "vcx_value_token", "vcx_workspace_bytes",
+            "vcx_group_values", "vcx_prepare_qk_int8", "vcx_prepare_v_fp8", "vcx_attention_fwd",
+            "vcx_expcast_codes", "vcx_convert_probe", "vcx_kernel_resources")
+
+
+def lib():
+    """Load libvcx.so once and check its ABI version (raises RuntimeError, never falls back)."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(f"libvcx.so is missing at {LIB_PATH}; build it with "
+                               "python cake-opt-vc_attention_amd/build.py. No fallback was used.")
+        L = ctypes.CDLL(str(LIB_PATH))
+        _declare(L)
+        if L.vcx_abi_version() != ABI_VERSION:
+            raise RuntimeError("Stale libvcx.so (ABI %d, expected %d): rebuild it" % (L.vcx_abi_version(), ABI_VERSION))
+        _lib = L
+    return _lib
+
+
+def _check(rc: int, what: str):
+    if rc == _OK:
+        return
+    msg = lib().vcx_last_error().decode(errors="replace")
+    if rc == _EUNSUPPORTED:
+        raise NotImplementedError(f"{what}: {msg}")
+    raise VcxError(f"{what}: {msg}")
+
+
+def _ptr(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(device):
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def _require_device(*tensors):
+    dev = tensors[0].device
+    if dev.type != "cuda":
+        raise VcxError("libvcx requires GPU (HIP) tensors; no CPU fallback")
+    for t in tensors:
+        if t is not None and t.device != dev:
+            raise VcxError("all tensors must be on the same device")
+    return dev
+
+
+def _strides4(x):
+    if x.dim() != 4 or x.stride(3) != 1:
+        raise VcxError("expected [B,H,N,D] with a contiguous last dimension")
+    return x.stride(0), x.stride(1), x.stride(2)
+
+
+def workspace_bytes(op: int, B: int, H: int, N: int, D: int, smooth: bool = False, clusters: int = 8) -> int:
+    out = ctypes.c_size_t(0)
+    _check(lib().vcx_workspace_bytes(op, B, H, N, D, int(smooth), clusters, ctypes.byref(out)),
+           "vcx_workspace_bytes")
+    return out.value
+
+
+def _workspace(nbytes: int, device):
+    # torch allocations are at least 256-byte aligned on ROCm.
+    return torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
+
+
+def value_token():
+    """Token offset stored at each byte position of a 128-token V tile (storage order)."""
+    return [lib().vcx_value_token(p) for p in range(128)]
+
+
+def value_position_index(device=None):
+    """Index tensor that maps storage order -> logical token order inside each tile."""
+    tok = value_token()
+    pos = [0] * 128
+    for p, t in enumerate(tok):
+        pos[t] = p
+    return torch.tensor(pos, dtype=torch.long, device=device)
+
+
+def abi_version() -> int:
+    return lib().vcx_abi_version()
+
+
+# ---------------------------------------------------------------- preprocessing
+
+@torch.no_grad()
+def group_values(v, clusters: int, iterations: int, debug: bool = False):
+    """int64 permutation [B,H,N] (+ int32 labels and fp32 centers when debug)."""
+    dev = _require_device(v)
+    if v.dtype not in _DTYPE:
+        raise VcxError("grouping requires float16/bfloat16 V")
+    B, H, N, D = v.shape
+    sb, sh, sn = _strides4(v)
+    count = min(clusters, N)
+    perm = torch.empty((B, H, N), dtype=torch.int64, device=dev)
+    labels = torch.empty((B, H, N), dtype=torch.int32, device=dev) if debug else None
+    centers = torch.empty((B, H, count, D), dtype=torch.float32, device=dev) if debug else None
+    ws = _workspace(workspace_bytes(WS_GROUP, B, H, N, D, clusters=clusters), dev)
+    _check(lib().vcx_group_values(_ptr(v), _DTYPE[v.dtype], B, H, N, D, sb, sh, sn, clusters, iterations,
+                                  _ptr(perm), _ptr(labels), _ptr(centers), _ptr(ws), ws.numel(), _stream(dev)),
+           "vcx_group_values")
+    return (perm, labels, centers) if debug else perm
+
+
+@torch.no_grad()
+def prepare_qk(q, k, perm=None):
+    """INT8 Q/K with Sage per-thread scales after K centring: (q8, qs, k8, ks, km)."""
+    dev = _require_device(q, k, perm)
+    if q.dtype not in _DTYPE or k.dtype != q.dtype:
+        raise VcxError("Q/K require matching float16/bfloat16")
+    B, H, Nq, D = q.shape
+    Nk = k.shape[2]
+    qsb, qsh, qsn = _strides4(q)
+    ksb, ksh, ksn = _strides4(k)
+    if perm is not None and (perm.dtype != torch.int64 or tuple(perm.shape) != (B, H, Nk) or not perm.is_contiguous()):
+        raise VcxError("perm must be contiguous int64 [B,H,Nk]")
+    q8 = torch.empty((B, H, Nq, D), dtype=torch.int8, device=dev)
+    k8 = torch.empty((B, H, Nk, D), dtype=torch.int8, device=dev)
+    qs = torch.empty((B, H, (Nq + 63) // 64 * 32), dtype=torch.float32, device=dev)
+    ks = torch.empty((B, H, (Nk + 127) // 128 * 4), dtype=torch.float32, device=dev)
+    km = torch.empty((B, H, 1, D), dtype=q.dtype, device=dev)
+    ws = _workspace(workspace_bytes(WS_PREPARE_QK, B, H, Nk, D), dev)
+    _check(lib().vcx_prepare_qk_int8(_ptr(q), _ptr(k), _DTYPE[q.dtype], B, H, Nq, Nk, D, qsb, qsh, qsn,
+                                     ksb, ksh, ksn, _ptr(perm), _ptr(q8), _ptr(qs), _ptr(k8), _ptr(ks), _ptr(km),
+                                     _ptr(ws), ws.numel(), _stream(dev)), "vcx_prepare_qk_int8")
+    return q8, qs, k8, ks, km
+
+
+@torch.no_grad()
+def prepare_v(v, perm=None, smooth: bool = False, channel_scale: bool = True):
+    """E4M3 V in storage order: (v8 [B,H,D,tiles*128], vs, means or empty)."""
+    dev = _require_device(v, perm)
+    if v.dtype not in _DTYPE:
+        raise VcxError("V requires float16/bfloat16")
+    B, H, N, D = v.shape
+    sb, sh, sn = _strides4(v)
+    if perm is not None and (perm.dtype != torch.int64 or tuple(perm.shape) != (B, H, N) or not perm.is_contiguous()):
+        raise VcxError("perm must be contiguous int64 [B,H,N]")
+    tiles = (N + 127) // 128
+    v8 = torch.empty((B, H, D, tiles * 128), dtype=torch.float8_e4m3fn, device=dev)
+    if smooth:
+        vs = torch.empty((B, H, D) if channel_scale else (B, H, tiles, D), dtype=torch.float32, device=dev)
+        means = torch.empty((B, H, tiles, D), dtype=torch.float16, device=dev)
+    else:
+        vs = torch.empty((B, H, D), dtype=torch.float32, device=dev)
+        means = torch.empty(0, dtype=torch.float16, device=dev)
+    ws = _workspace(workspace_bytes(WS_PREPARE_V, B, H, N, D, smooth), dev)
+    _check(lib().vcx_prepare_v_fp8(_ptr(v), _DTYPE[v.dtype], B, H, N, D, sb, sh, sn, _ptr(perm), int(smooth),
+                                   int(channel_scale), _ptr(v8), _ptr(vs), _ptr(means) if smooth else None,
+                                   _ptr(ws), ws.numel(), _stream(dev)), "vcx_prepare_v_fp8")
+    return v8, vs, means
+
+
+# ---------------------------------------------------------------- attention
+
+@torch.no_grad()
+def forward(q8, k8, v8, qs, ks, vs, means, expcast: bool, block_values: bool, output_type: int, scale: float,
+            *, channel_scale: bool = True, out=None, p_rows=None):
+    """Fused attention on prepared payloads -> out [B,H,Nq,D] (fp16 if output_type == 0 else bf16).
+
+    p_rows=(begin, end) additionally returns the E4M3 P bytes of those query rows
+    (uint8 [B,H,end-begin,tiles*128], logical key order) from the diagnostic variant.
+    """
+    dev = _require_device(q8, k8, v8, qs, ks, vs)
+    B, H, Nq, D = q8.shape
+    Nk = k8.shape[2]
+    tiles = (Nk + 127) // 128
+    for name, t, dt in (("q", q8, torch.int8), ("k", k8, torch.int8), ("qs", qs, torch.float32),
+                        ("ks", ks, torch.float32), ("vs", vs, torch.float32)):
+        if t.dtype != dt or not t.is_contiguous():
+            raise VcxError(f"{name} must be contiguous {dt}")
+    if v8.dtype not in (torch.float8_e4m3fn, torch.uint8) or not v8.is_contiguous():
+        raise VcxError("v must be contiguous float8_e4m3fn")
+    if tuple(k8.shape) != (B, H, Nk, D) or tuple(v8.shape) != (B, H, D, tiles * 128):
+        raise VcxError("K/V payload shapes do not match Q")
+    if tuple(qs.shape) != (B, H, (Nq + 63) // 64 * 32) or tuple(ks.shape) != (B, H, tiles * 4):
+        raise VcxError("qs/ks shapes do not match the payloads")
+    if block_values:
+        if means is None or means.dtype != torch.float16 or tuple(means.shape) != (B, H, tiles, D) \
+                or not means.is_contiguous():
+            raise VcxError("means must be contiguous float16 [B,H,tiles,D]")
+    vs_shape = (B, H, D) if (channel_scale or not block_values) else (B, H, tiles, D)
+    if tuple(vs.shape) != vs_shape:
+        raise VcxError(f"vs must have shape {vs_shape}")
+    out_dtype = torch.float16 if output_type == 0 else torch.bfloat16
+    if out is None:
+        out = torch.empty((B, H, Nq, D), dtype=out_dtype, device=dev)
+    osb, osh, osn = _strides4(out)
+    pd = None
+    r0 = r1 = 0
+    if p_rows is not None:
+        r0, r1 = int(p_rows[0]), int(p_rows[1])
+        pd = torch.zeros((B, H, max(r1 - r0, 0), tiles * 128), dtype=torch.uint8, device=dev)
+    _check(lib().vcx_attention_fwd(_ptr(q8), _ptr(k8), _ptr(v8), _ptr(qs), _ptr(ks), _ptr(vs),
+                                   _ptr(means) if block_values else None, B, H, Nq, Nk, D, int(expcast),
+                                   int(block_values), int(channel_scale), float(scale), 1 if output_type else 0,
+                                   _ptr(out), osb, osh, osn, _ptr(pd), r0, r1, _stream(dev)),
+           "vcx_attention_fwd")
+    return (out, pd) if p_rows is not None else out
+
+
+@torch.no_grad()
+def expcast_codes(x):
+    dev = _require_device(x)
+    x = x.float().contiguous()
+    y = torch.empty(x.shape, dtype=torch.uint8, device=dev)
+    _check(lib().vcx_expcast_codes(_ptr(x), _ptr(y), x.numel(), _stream(dev)), "vcx_expcast_codes")
+    return y
+
+
+@torch.no_grad()
+def convert_probe(x):
+    dev = _require_device(x)
+    x = x.float().contiguous()
+    u8 = torch.empty(x.shape, dtype=torch.uint8, device=dev)
+    f8 = torch.empty(x.shape, dtype=torch.uint8, device=dev)
+    _check(lib().vcx_convert_probe(_ptr(x), _ptr(u8), _ptr(f8), x.numel(), _stream(dev)), "vcx_convert_probe")
+    return u8, f8
+
+
+def kernel_resources(D: int = 128, block_values: bool = False) -> dict:
+    arr = (ctypes.c_int64 * 6)()
+    _check(lib().vcx_kernel_resources(D, int(block_values), arr), "vcx_kernel_resources")
+    return {"vgprs": arr[0], "agprs": arr[1], "static_lds_bytes": arr[2], "dynamic_lds_bytes": arr[3],
+            "threads_per_block": arr[4], "scratch_bytes_per_lane": arr[5]}

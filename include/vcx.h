@@ -1,0 +1,149 @@
+/*
+ * vcx.h -- C ABI of the MI355X (gfx950) sageattn_vc implementation.
+ *
+ * The library libvcx.so (built from cake-opt-vc_attention_amd/csrc) exports
+ * exactly the functions declared here. Every entry point:
+ *   - takes raw device pointers plus explicit shapes and element strides;
+ *   - never allocates: the caller owns every output and workspace buffer;
+ *   - enqueues all work on the given HIP stream (hipStream_t passed as void*;
+ *     NULL means the null stream) and never synchronizes;
+ *   - returns VCX_OK (0) or a nonzero error code, with a message available
+ *     from vcx_last_error() on the calling thread; no C++ exception crosses
+ *     this boundary;
+ *   - validates shapes, strides, alignment and sizes before any launch.
+ *
+ * Tensor conventions (B batch, H heads, N tokens, D head dim in {64,128}):
+ *   q, k, v        fp16/bf16, element strides (sb, sh, sn), unit stride over D;
+ *                  HND and NHD layouts are both expressed by these strides.
+ *   q8 / k8        int8 [B,H,N,D] contiguous (logical token order; k8 is in
+ *                  permuted order when a permutation is given).
+ *   qs             fp32 [B,H,ceil(Nq/64)*32], index (row/16)*8 + row%8.
+ *   ks             fp32 [B,H,ceil(Nk/128)*4], index tile*4 + (key%8)/2.
+ *   v8             E4M3 bytes [B,H,D,ceil(Nk/128)*128] in STORAGE order: inside
+ *                  every 128-token tile, byte position p holds token
+ *                  vcx_value_token(p) (see below); padding tokens are 0x00.
+ *   vs             fp32 [B,H,D] (per-channel) or [B,H,tiles,D] (per-block).
+ *   means          binary16 [B,H,tiles,D] (V smoothing only).
+ */
+#ifndef VCX_H
+#define VCX_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define VCX_ABI_VERSION 1
+
+enum vcx_status {
+  VCX_OK = 0,
+  VCX_EINVAL = 1,       /* invalid argument, shape, stride, alignment or size */
+  VCX_EUNSUPPORTED = 2, /* valid request this build does not implement */
+  VCX_EHIP = 3          /* a HIP runtime call failed */
+};
+
+enum vcx_dtype { VCX_FLOAT16 = 0, VCX_BFLOAT16 = 1 };
+
+enum vcx_workspace_op {
+  VCX_WS_PREPARE_QK = 1, /* vcx_prepare_qk_int8 */
+  VCX_WS_PREPARE_V = 2,  /* vcx_prepare_v_fp8 (smoothing off or on) */
+  VCX_WS_GROUP = 3       /* vcx_group_values */
+};
+
+/* Library ABI version (VCX_ABI_VERSION). Replaces the reference's build-stamp
+ * attributes sage_vc_api_version / sage_vc_kernel_version checked at
+ * third_party/sageattention_local/sageattention_local/vc.py:49-55. */
+int vcx_abi_version(void);
+
+/* Message of the last failing call on this thread ("" if none). Replaces the
+ * TORCH_CHECK messages of third_party/sageattention_local/csrc/vc/vc_sm90.cu:1030-1064. */
+const char* vcx_last_error(void);
+
+/* Storage position -> token offset inside a 128-token V tile (p in 0..127).
+ * The reference stores Sage's 16-token permutation instead
+ * (third_party/sageattention_local/sageattention_local/vc_reference.py:14-17,
+ * csrc/fused/fused.cu:287-291); this order feeds the gfx950 FP8 MFMA B layout. */
+int vcx_value_token(int p);
+
+/* Bytes of caller-provided workspace needed by one call of the given op.
+ * clusters/iterations matter for VCX_WS_GROUP only; smooth for VCX_WS_PREPARE_V. */
+int vcx_workspace_bytes(int op, int64_t B, int64_t H, int64_t N, int64_t D, int smooth,
+                        int clusters, size_t* bytes);
+
+/* V grouping: count = min(clusters, N) <= 8 clusters per head, `iterations`
+ * Lloyd passes (fp64 distances, ties to the lowest id, empty clusters keep
+ * their center), then a stable counting sort by label.
+ * Outputs: perm int64 [B,H,N]; labels int32 [B,H,N] (nullable);
+ * centers fp32 [B,H,count,D] used by the final assignment (nullable).
+ * Replaces _vc_sm90.group_values / group_values_debug
+ * (third_party/sageattention_local/csrc/vc/pybind.cpp:39-44, clustering.cu:140-167). */
+int vcx_group_values(const void* v, int dtype, int64_t B, int64_t H, int64_t N, int64_t D,
+                     int64_t v_sb, int64_t v_sh, int64_t v_sn, int clusters, int iterations,
+                     int64_t* perm, int32_t* labels, float* centers, void* workspace,
+                     size_t workspace_bytes, void* stream);
+
+/* Q/K INT8 with Sage per-thread scales, after K channel-mean centring.
+ * perm (nullable, int64 [B,H,Nk]) gathers K tokens first. km_out (nullable)
+ * receives the channel mean [B,H,D] in the input dtype.
+ * Replaces `km = k.mean(2); per_thread_int8(q, k, km, BLKQ=64, WARPQ=16,
+ * BLKK=128, WARPK=128)` (third_party/sageattention_local/sageattention_local/vc.py:155-159,
+ * triton/quant_per_thread.py:154-204). */
+int vcx_prepare_qk_int8(const void* q, const void* k, int dtype, int64_t B, int64_t H,
+                        int64_t Nq, int64_t Nk, int64_t D, int64_t q_sb, int64_t q_sh,
+                        int64_t q_sn, int64_t k_sb, int64_t k_sh, int64_t k_sn,
+                        const int64_t* perm, int8_t* q8, float* qs, int8_t* k8, float* ks,
+                        void* km_out, void* workspace, size_t workspace_bytes, void* stream);
+
+/* V to E4M3. smooth = 0: per-channel amax scale (vs [B,H,D], means unused).
+ * smooth = 1: 128-token block-mean residuals with per-channel (channel_scale=1,
+ * vs [B,H,D]) or per-block (channel_scale=0, vs [B,H,tiles,D]) scales and
+ * binary16 scaled means [B,H,tiles,D]. perm (nullable) gathers tokens first.
+ * Replaces per_channel_fp8 (third_party/sageattention_local/sageattention_local/quant.py:224-293,
+ * with the zero padding of vc.py:163-166) and _vc_sm90.prepare_values
+ * (third_party/sageattention_local/csrc/vc/preprocess.cu:138-168). */
+int vcx_prepare_v_fp8(const void* v, int dtype, int64_t B, int64_t H, int64_t N, int64_t D,
+                      int64_t v_sb, int64_t v_sh, int64_t v_sn, const int64_t* perm, int smooth,
+                      int channel_scale, uint8_t* v8, float* vs, uint16_t* means,
+                      void* workspace, size_t workspace_bytes, void* stream);
+
+/* Fused attention forward: INT8 QK^T on MFMA, ExpCast E4M3 probabilities,
+ * FP8 PV on MFMA, online max/sum, block-mean restore, epilogue.
+ * expcast must be 1. block_values = 1 consumes means/vs as written by
+ * vcx_prepare_v_fp8(smooth=1, channel_scale); block_values = 0 uses vs [B,H,D]
+ * and ignores means. out: fp16/bf16 (out_dtype) with element strides.
+ * p_dump (nullable): diagnostic copy of the E4M3 P bytes for query rows
+ * [p_row_begin, p_row_end) of every head, uint8 [B,H,rows,ceil(Nk/128)*128]
+ * in logical key order (padding keys 0); slower kernel variant.
+ * Replaces _vc_sm90.forward (third_party/sageattention_local/csrc/vc/pybind.cpp:51-55,
+ * vc_sm90.cu:1027-1123). */
+int vcx_attention_fwd(const int8_t* q8, const int8_t* k8, const uint8_t* v8, const float* qs,
+                      const float* ks, const float* vs, const uint16_t* means, int64_t B,
+                      int64_t H, int64_t Nq, int64_t Nk, int64_t D, int expcast,
+                      int block_values, int channel_scale, float sm_scale, int out_dtype,
+                      void* out, int64_t o_sb, int64_t o_sh, int64_t o_sn, uint8_t* p_dump,
+                      int64_t p_row_begin, int64_t p_row_end, void* stream);
+
+/* ExpCast byte probe: y[i] = clamp(RNE(fmaf(x[i], 11.54156, 119.65)), 0, 120).
+ * Replaces _vc_sm90.expcast_codes (third_party/sageattention_local/csrc/vc/preprocess.cu:170-179). */
+int vcx_expcast_codes(const float* x, uint8_t* y, int64_t n, void* stream);
+
+/* Diagnostic probe of the gfx950 conversions the kernels rely on:
+ * u8[i] = v_cvt_pk_u8_f32(x[i]) and f8[i] = v_cvt_pk_fp8_f32(clamp(x[i], +-448)).
+ * No counterpart in the reference (which probes only ExpCast); used by the
+ * parity tests to pin the instructions' rounding against the CPU oracle. */
+int vcx_convert_probe(const float* x, uint8_t* u8, uint8_t* f8, int64_t n, void* stream);
+
+/* Compiled resources of the fused kernel for (D, block_values):
+ * out[0] VGPRs, out[1] AGPRs (0 if not reported), out[2] static LDS bytes,
+ * out[3] dynamic LDS bytes per block, out[4] threads per block,
+ * out[5] scratch (spill) bytes per lane.
+ * Replaces _vc_sm90.kernel_resources (third_party/sageattention_local/csrc/vc/vc_sm90.cu:786-822). */
+int vcx_kernel_resources(int64_t D, int block_values, int64_t* out);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* VCX_H */

@@ -1,0 +1,278 @@
+"""CPU oracle for the sageattn_vc contract (numpy + the C restatement in vc_oracle.c).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and the
+cpu_baseline leg of bench.py, never by the product package. The functions keep
+the reference's names and argument meaning so the parity tests read like the
+reference's own tests:
+
+* ``expcast_codes``      -- sal/sageattention_local/vc_reference.py:9-11
+* ``value_permutation``  -- sal/sageattention_local/vc_reference.py:14-17 (Sage layout)
+* ``group_values``       -- sal/csrc/vc/clustering.cu:140-167, pybind.cpp:39-44
+* ``per_thread_int8``    -- sal/sageattention_local/triton/quant_per_thread.py:154-204
+* ``per_channel_fp8``    -- sal/sageattention_local/quant.py:224-293
+* ``prepare_values``     -- sal/csrc/vc/preprocess.cu:138-168
+* ``prepare``            -- sal/sageattention_local/vc.py:141-170
+* ``reference``          -- sal/sageattention_local/vc_reference.py:20-91
+
+("sal/" abbreviates third_party/sageattention_local/ of the reference.)
+Arrays are numpy; 16-bit inputs are passed as raw uint16 bit patterns plus a
+dtype tag ("bfloat16" or "float16"). V payloads are LOGICAL: [B,H,D,tiles*128]
+in token order (the reference stores the Sage 16-token permutation instead;
+``value_permutation`` converts).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+_HERE = Path(__file__).resolve().parent
+_LIB_PATH = _HERE / "lib" / "libvc_oracle.so"
+_lib = None
+
+DTYPES = {"float16": 0, "bfloat16": 1}
+
+
+def build(force: bool = True) -> Path:
+    """Compile vc_oracle.c with gcc (no FMA contraction, IEEE semantics)."""
+    if _LIB_PATH.exists() and not force:
+        return _LIB_PATH
+    _LIB_PATH.parent.mkdir(parents=True, exist_ok=True)
+    tmp = _LIB_PATH.with_suffix(".so.tmp%d" % os.getpid())
+    cmd = ["gcc", "-O2", "-fPIC", "-shared", "-ffp-contract=off", "-fno-fast-math",
+           "-fopenmp", "-Wall", "-o", str(tmp), str(_HERE / "vc_oracle.c"), "-lm"]
+    subprocess.run(cmd, check=True)
+    os.replace(tmp, _LIB_PATH)
+    return _LIB_PATH
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not _LIB_PATH.exists():
+            build()
+        _lib = ctypes.CDLL(str(_LIB_PATH))
+        _declare(_lib)
+    return _lib
+
+
+def _declare(L):
+    P = ctypes.c_void_p
+    i64, i32, f32 = ctypes.c_int64, ctypes.c_int, ctypes.c_float
+    L.vco_expcast_code.restype = ctypes.c_uint8
+    L.vco_expcast_code.argtypes = [f32]
+    for name in ("vco_expcast_codes", "vco_e4m3_encode_array", "vco_e4m3_decode_array",
+                 "vco_cvt_u8_array"):
+        getattr(L, name).argtypes = [P, P, i64]
+        getattr(L, name).restype = None
+    L.vco_tile_tree_sum.restype = ctypes.c_double
+    L.vco_tile_tree_sum.argtypes = [P]
+    L.vco_linspace_ids.argtypes = [i64, i32, P]
+    L.vco_group_values.restype = i32
+    L.vco_group_values.argtypes = [P, i32, i64, i64, i32, i32, i32, P, P, P]
+    L.vco_k_mean.argtypes = [P, i32, i64, i64, i32, P, P]
+    L.vco_quant_q.argtypes = [P, i32, i64, i64, i32, P, P]
+    L.vco_quant_k.argtypes = [P, i32, i64, i64, i32, P, P, P, P]
+    L.vco_quant_v_channel.argtypes = [P, i32, i64, i64, i32, P, P, P]
+    L.vco_quant_v_smooth.argtypes = [P, i32, i64, i64, i32, P, i32, P, P, P]
+    L.vco_attention.argtypes = [P, P, P, P, P, P, P, i32, i64, i64, i64, i32, f32, P, i64, P, P]
+
+
+def _ptr(a):
+    return None if a is None else a.ctypes.data_as(ctypes.c_void_p)
+
+
+def _c(a, dtype):
+    return np.ascontiguousarray(a, dtype=dtype)
+
+
+# ---------------------------------------------------------------- scalar maps
+
+def expcast_codes(shifted) -> np.ndarray:
+    x = _c(shifted, np.float32)
+    y = np.empty(x.shape, np.uint8)
+    lib().vco_expcast_codes(_ptr(x), _ptr(y), x.size)
+    return y
+
+
+def e4m3_encode(x) -> np.ndarray:
+    x = _c(x, np.float32)
+    y = np.empty(x.shape, np.uint8)
+    lib().vco_e4m3_encode_array(_ptr(x), _ptr(y), x.size)
+    return y
+
+
+def e4m3_decode(b) -> np.ndarray:
+    b = _c(b, np.uint8)
+    y = np.empty(b.shape, np.float32)
+    lib().vco_e4m3_decode_array(_ptr(b), _ptr(y), b.size)
+    return y
+
+
+def cvt_u8(x) -> np.ndarray:
+    x = _c(x, np.float32)
+    y = np.empty(x.shape, np.uint8)
+    lib().vco_cvt_u8_array(_ptr(x), _ptr(y), x.size)
+    return y
+
+
+def tile_tree_sum(x) -> float:
+    x = _c(x, np.float64)
+    assert x.shape == (128,)
+    return lib().vco_tile_tree_sum(_ptr(x))
+
+
+def value_permutation(n: int) -> np.ndarray:
+    """Sage's stored order within 16 tokens (reference vc_reference.py:14-17)."""
+    i = np.arange(n)
+    r = i % 16
+    return (i // 16) * 16 + (r // 8) * 2 + ((r // 2) % 4) * 4 + r % 2
+
+
+def linspace_ids(n: int, count: int) -> np.ndarray:
+    ids = np.empty(count, np.int64)
+    lib().vco_linspace_ids(n, count, _ptr(ids))
+    return ids
+
+
+# ---------------------------------------------------------------- preprocessing
+
+def _shape4(x):
+    x = np.asarray(x)
+    if x.ndim != 4:
+        raise ValueError("expected [B,H,N,D]")
+    return x.shape
+
+
+def group_values(v, clusters: int, iterations: int, dtype: str = "bfloat16"):
+    B, H, N, D = _shape4(v)
+    v = _c(v, np.uint16)
+    count = min(clusters, N)
+    perm = np.empty((B, H, N), np.int64)
+    labels = np.empty((B, H, N), np.int32)
+    centers = np.empty((B, H, count, D), np.float32)
+    rc = lib().vco_group_values(_ptr(v), DTYPES[dtype], B * H, N, D, clusters, iterations,
+                                _ptr(perm), _ptr(labels), _ptr(centers))
+    if rc:
+        raise ValueError("invalid clustering parameters")
+    return perm, labels, centers
+
+
+def k_mean(k, perm=None, dtype: str = "bfloat16") -> np.ndarray:
+    B, H, N, D = _shape4(k)
+    k = _c(k, np.uint16)
+    perm = None if perm is None else _c(perm, np.int64)
+    km = np.empty((B, H, D), np.uint16)
+    lib().vco_k_mean(_ptr(k), DTYPES[dtype], B * H, N, D, _ptr(perm), _ptr(km))
+    return km
+
+
+def quant_q(q, dtype: str = "bfloat16"):
+    B, H, N, D = _shape4(q)
+    q = _c(q, np.uint16)
+    q8 = np.zeros((B, H, N, D), np.int8)
+    qs = np.empty((B, H, (N + 63) // 64 * 32), np.float32)
+    lib().vco_quant_q(_ptr(q), DTYPES[dtype], B * H, N, D, _ptr(q8), _ptr(qs))
+    return q8, qs
+
+
+def quant_k(k, km=None, perm=None, dtype: str = "bfloat16"):
+    B, H, N, D = _shape4(k)
+    k = _c(k, np.uint16)
+    km = None if km is None else _c(km, np.uint16)
+    perm = None if perm is None else _c(perm, np.int64)
+    k8 = np.zeros((B, H, N, D), np.int8)
+    ks = np.empty((B, H, (N + 127) // 128 * 4), np.float32)
+    lib().vco_quant_k(_ptr(k), DTYPES[dtype], B * H, N, D, _ptr(perm), _ptr(km), _ptr(k8), _ptr(ks))
+    return k8, ks
+
+
+def per_thread_int8(q, k, km=None, perm=None, dtype: str = "bfloat16"):
+    """Q per row-pair and K per key-set INT8 with FP32 scales (BLKQ=64, WARPQ=16, BLKK=128, WARPK=128)."""
+    q8, qs = quant_q(q, dtype)
+    k8, ks = quant_k(k, km, perm, dtype)
+    return q8, qs, k8, ks
+
+
+def per_channel_fp8(v, perm=None, dtype: str = "bfloat16"):
+    """Smoothing-off V: LOGICAL payload [B,H,D,tiles*128] + per-channel scales [B,H,D]."""
+    B, H, N, D = _shape4(v)
+    v = _c(v, np.uint16)
+    perm = None if perm is None else _c(perm, np.int64)
+    npad = (N + 127) // 128 * 128
+    v8 = np.empty((B, H, D, npad), np.uint8)
+    vs = np.empty((B, H, D), np.float32)
+    lib().vco_quant_v_channel(_ptr(v), DTYPES[dtype], B * H, N, D, _ptr(perm), _ptr(v8), _ptr(vs))
+    return v8, vs
+
+
+def prepare_values(v, perm=None, channel_scale: bool = True, dtype: str = "bfloat16"):
+    """Smoothing-on V: LOGICAL payload, scales ([B,H,D] or [B,H,tiles,D]), fp16 means bits [B,H,tiles,D]."""
+    B, H, N, D = _shape4(v)
+    v = _c(v, np.uint16)
+    perm = None if perm is None else _c(perm, np.int64)
+    tiles = (N + 127) // 128
+    v8 = np.empty((B, H, D, tiles * 128), np.uint8)
+    vs = np.empty((B, H, D) if channel_scale else (B, H, tiles, D), np.float32)
+    means = np.empty((B, H, tiles, D), np.uint16)
+    lib().vco_quant_v_smooth(_ptr(v), DTYPES[dtype], B * H, N, D, _ptr(perm), int(channel_scale),
+                             _ptr(v8), _ptr(vs), _ptr(means))
+    return v8, vs, means
+
+
+def prepare(q, k, v, *, expcast=True, v_smooth=True, clusters=8, iterations=2, sm_scale=None,
+            v_scale_mode="channel", dtype="bfloat16"):
+    """State dict of the sageattn_vc contract (reference vc.py:141-170); v is LOGICAL."""
+    if not expcast:
+        raise ValueError("the oracle restates the ExpCast contract only")
+    perm = None
+    if v_smooth:
+        perm, _, _ = group_values(v, clusters, iterations, dtype)
+    km = k_mean(k, perm, dtype)
+    q8, qs = quant_q(q, dtype)
+    k8, ks = quant_k(k, km, perm, dtype)
+    if v_smooth:
+        v8, vs, means = prepare_values(v, perm, v_scale_mode == "channel", dtype)
+    else:
+        v8, vs = per_channel_fp8(v, perm, dtype)
+        means = None
+    D = np.asarray(q).shape[-1]
+    return {"q": q8, "k": k8, "v": v8, "qs": qs, "ks": ks, "vs": vs, "means": means, "km": km,
+            "expcast": True, "block_values": v_smooth, "output_type": 1 if dtype == "bfloat16" else 0,
+            "scale": D ** -0.5 if sm_scale is None else sm_scale, "permutation": perm}
+
+
+def reference(state, query_indices=None, return_codes=False):
+    """Decoded-payload oracle (vc_reference.py:20-91) with the exact ExpCast P codes.
+
+    Returns float32 [B,H,len(ids),D] (and uint8 codes [B,H,len(ids),tiles*128]).
+    """
+    q8, k8, v8 = state["q"], state["k"], state["v"]
+    B, H, Nq, D = q8.shape
+    Nk = k8.shape[2]
+    tiles = (Nk + 127) // 128
+    ids = np.arange(Nq, dtype=np.int64) if query_indices is None else np.asarray(query_indices, np.int64)
+    if ids.size == 0:
+        raise ValueError("Reference requires nonempty queries")
+    vs = state["vs"]
+    means = state.get("means")
+    block_scale = int(means is not None and vs is not None and vs.ndim == 4)
+    out = np.empty((B, H, ids.size, D), np.float32)
+    codes = np.empty((B, H, ids.size, tiles * 128), np.uint8) if return_codes else None
+    lib().vco_attention(_ptr(_c(q8, np.int8)), _ptr(_c(k8, np.int8)), _ptr(_c(v8, np.uint8)),
+                        _ptr(_c(state["qs"], np.float32)), _ptr(_c(state["ks"], np.float32)),
+                        _ptr(None if vs is None else _c(vs, np.float32)),
+                        _ptr(None if means is None else _c(means, np.uint16)), block_scale,
+                        B * H, Nq, Nk, D, float(np.float32(state["scale"])), _ptr(ids), ids.size,
+                        _ptr(out), _ptr(codes))
+    return (out, codes) if return_codes else out
+
+
+def query_indices(n: int, count: int = 128) -> np.ndarray:
+    """Evenly spaced sample rows i*(n-1)//(count-1) (reference scripts/benchmark_cuda.py:224-228)."""
+    if n <= count:
+        return np.arange(n, dtype=np.int64)
+    return np.array([i * (n - 1) // (count - 1) for i in range(count)], np.int64)

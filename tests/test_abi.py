@@ -1,0 +1,81 @@
+"""The C-ABI library: loads, exports every symbol of include/vcx.h, reports its
+version and layout, and rejects invalid calls before any GPU work. CPU only:
+no call here reaches a kernel launch."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+import vcx
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def declared_functions():
+    text = (ROOT / "include" / "vcx.h").read_text()
+    return sorted(set(re.findall(r"^(?:int|const char\*)\s+(vcx_\w+)\s*\(", text, re.M)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = ctypes.CDLL(str(vcx.LIB_PATH))
+    names = declared_functions()
+    assert len(names) >= 10
+    for name in names:
+        assert hasattr(lib, name), name
+    assert sorted(vcx.EXPORTED) == names
+
+
+def test_abi_version_and_value_order():
+    assert vcx.abi_version() == vcx.ABI_VERSION == 1
+    tok = vcx.value_token()
+    assert sorted(tok) == list(range(128))
+    # closed form: position p = 32G + b holds token 16(b/4) + 8((b/2)%2) + 2G + b%2
+    for p, t in enumerate(tok):
+        G, b = divmod(p, 32)
+        assert t == 16 * (b // 4) + 8 * ((b // 2) % 2) + 2 * G + b % 2
+    # lane group G holds exactly the keys of Sage K-scale group (key % 8) // 2 == G
+    for G in range(4):
+        assert {(t % 8) // 2 for t in tok[32 * G:32 * G + 32]} == {G}
+    assert vcx.lib().vcx_value_token(128) == -1
+
+
+def test_workspace_sizes():
+    for op in (vcx.WS_PREPARE_QK, vcx.WS_PREPARE_V, vcx.WS_GROUP):
+        assert vcx.workspace_bytes(op, 1, 28, 37741, 128, True) > 0
+    with pytest.raises(vcx.VcxError, match="unknown workspace op"):
+        vcx.workspace_bytes(9, 1, 1, 1, 128)
+    with pytest.raises(vcx.VcxError, match="invalid shape"):
+        vcx.workspace_bytes(1, 1, 1, 1, 96)
+
+
+def _fwd(**kw):
+    args = dict(q8=None, k8=None, v8=None, qs=None, ks=None, vs=None, means=None, B=1, H=1, Nq=1, Nk=1, D=128,
+                expcast=1, block_values=0, channel_scale=1, sm=0.088, out_dtype=1, out=None, osb=128, osh=128,
+                osn=128, pd=None, r0=0, r1=0, stream=None)
+    args.update(kw)
+    L = vcx.lib()
+    rc = L.vcx_attention_fwd(*args.values())
+    return rc, L.vcx_last_error().decode()
+
+
+def test_invalid_calls_rejected_before_launch():
+    assert _fwd(D=96) == (1, "D must be 64 or 128")
+    rc, msg = _fwd(expcast=0)
+    assert rc == 2 and "ExpCast" in msg
+    rc, msg = _fwd(sm=float("inf"))
+    assert rc == 1 and "sm_scale" in msg
+    rc, msg = _fwd()
+    assert rc == 1 and "null" in msg
+    rc, msg = _fwd(block_values=1, channel_scale=0)
+    assert rc == 2 and "per-block" in msg
+    L = vcx.lib()
+    assert L.vcx_expcast_codes(None, None, -1, None) == 1
+    assert L.vcx_group_values(None, 1, 1, 1, 10, 128, 0, 0, 128, 9, 2, None, None, None, None, 0, None) == 2
+    assert "8 effective clusters" in L.vcx_last_error().decode()
+
+
+def test_python_binding_refuses_cpu_tensors():
+    import torch
+    with pytest.raises(vcx.VcxError, match="no CPU fallback"):
+        vcx.prepare_qk(torch.zeros(1, 1, 4, 64, dtype=torch.bfloat16), torch.zeros(1, 1, 4, 64, dtype=torch.bfloat16))

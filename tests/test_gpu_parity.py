@@ -1,0 +1,311 @@
+"""GPU parity of libvcx (through its C ABI) against the CPU oracle.
+
+Bit-exact: ExpCast codes, conversions, INT8 Q/K payloads and scales, K mean,
+E4M3 V payloads (logical order), V scales and fp16 means, grouping labels /
+permutation / centers, and the E4M3 P bytes produced inside the fused kernel.
+Tolerance (written in helpers.output_bound): the fp16/bf16 attention output vs
+the oracle's decoded-payload path, plus cosine >= 0.9999.
+"""
+import numpy as np
+import pytest
+import torch
+
+import vcx
+from helpers import bits, cosine, dtype_name, logical_to_storage, make_qkv, output_bound, storage_to_logical
+from oracle import vc_oracle as o
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda:0")
+
+
+def _print_case(*args):
+    print("case:", *args, flush=True)
+
+
+def test_device_is_gfx950_and_library_loaded():
+    assert torch.cuda.is_available()
+    arch = torch.cuda.get_device_properties(DEV).gcnArchName
+    assert arch.startswith("gfx950"), arch
+    assert vcx.abi_version() == vcx.ABI_VERSION
+    tok = vcx.value_token()
+    assert sorted(tok) == list(range(128))
+
+
+# ------------------------------------------------------------------ scalar maps
+
+def test_expcast_codes_sweep_bit_exact():
+    # scripts/validate_sage_vc.py:22-24 sweep, plus every code boundary +- 8 ulps.
+    xs = [np.linspace(-15, 1, 65537, dtype=np.float32), np.array([-np.inf, -20.0, 0.0, np.nan, 3.0], np.float32)]
+    A, B = np.float32(11.541560173034668), np.float32(119.6500015258789)
+    for c in range(0, 121):
+        x0 = np.float32((c + 0.5 - np.float64(B)) / np.float64(A))
+        xs.append((x0.view(np.int32) + np.arange(-8, 9)).astype(np.int32).view(np.float32))
+    x = np.concatenate(xs).astype(np.float32)
+    _print_case("expcast sweep", x.size)
+    got = vcx.expcast_codes(torch.from_numpy(x).to(DEV)).cpu().numpy()
+    np.testing.assert_array_equal(got, o.expcast_codes(x))
+
+
+def test_conversion_instructions_bit_exact():
+    rng = np.random.default_rng(5)
+    parts = [np.array([-np.inf, np.inf, 0.0, -0.0, 1e-30, -1e-30, 1e-45], np.float32)]
+    for k in range(-2, 257):  # every half-integer +- 64 ulps (cvt_pk_u8 rounding)
+        h = np.float32(k + 0.5)
+        parts.append((h.view(np.int32) + np.arange(-64, 65)).astype(np.int32).view(np.float32))
+    dec = o.e4m3_decode(np.arange(0, 0x7F, dtype=np.uint8)).astype(np.float64)
+    for a, b in zip(dec[:-1], dec[1:]):  # every E4M3 midpoint +- 64 ulps, both signs
+        m = np.float32((a + b) / 2)
+        s = (m.view(np.int32) + np.arange(-64, 65)).astype(np.int32).view(np.float32)
+        parts += [s, -s]
+    parts.append((rng.standard_normal(1 << 20) * 200).astype(np.float32))
+    parts.append(np.ldexp(rng.random(1 << 20), rng.integers(-20, 10, 1 << 20)).astype(np.float32))
+    x = np.concatenate(parts)
+    _print_case("conversion probe", x.size)
+    u8, f8 = vcx.convert_probe(torch.from_numpy(x).to(DEV))
+    np.testing.assert_array_equal(u8.cpu().numpy(), o.cvt_u8(x))
+    np.testing.assert_array_equal(f8.cpu().numpy(), o.e4m3_encode(np.clip(x, -448, 448)))
+
+
+# ------------------------------------------------------------------ preprocessing
+
+SHAPES = [  # B, H, Nq, Nk, D, dtype
+    (1, 2, 2048, 2048, 128, torch.bfloat16),
+    (1, 1, 1, 1, 128, torch.bfloat16),
+    (2, 3, 65, 129, 64, torch.float16),
+    (1, 2, 257, 385, 128, torch.float16),
+    (1, 1, 63, 127, 64, torch.bfloat16),
+    (1, 1, 300, 4097, 128, torch.bfloat16),
+]
+
+
+def _ids(shape):
+    return "B%dH%dq%dk%dD%d%s" % (*shape[:5], "bf16" if shape[5] == torch.bfloat16 else "f16")
+
+
+@pytest.mark.parametrize("shape", SHAPES, ids=_ids)
+@pytest.mark.parametrize("kind", ["normal", "outlier"])
+def test_prepare_qk_bit_exact(shape, kind):
+    B, H, Nq, Nk, D, dt = shape
+    _print_case("prepare_qk", _ids(shape), kind)
+    q, k, v = make_qkv(B, H, Nq, Nk, D, dt, seed=1, kind=kind)
+    q8, qs, k8, ks, km = vcx.prepare_qk(q.to(DEV), k.to(DEV))
+    name = dtype_name(dt)
+    ekm = o.k_mean(bits(k), None, name)
+    eq8, eqs = o.quant_q(bits(q), name)
+    ek8, eks = o.quant_k(bits(k), ekm, None, name)
+    np.testing.assert_array_equal(km.view(torch.int16).cpu().numpy().view(np.uint16).reshape(B, H, D), ekm)
+    np.testing.assert_array_equal(q8.cpu().numpy(), eq8)
+    np.testing.assert_array_equal(qs.cpu().numpy().view(np.uint32), eqs.view(np.uint32))
+    np.testing.assert_array_equal(k8.cpu().numpy(), ek8)
+    np.testing.assert_array_equal(ks.cpu().numpy().view(np.uint32), eks.view(np.uint32))
+
+
+def test_prepare_qk_strided_nhd_and_permutation():
+    B, H, N, D = 1, 3, 333, 128
+    q, k, v = make_qkv(B, H, N, N, D, torch.bfloat16, seed=3)
+    g = torch.Generator().manual_seed(4)
+    perm = torch.stack([torch.randperm(N, generator=g) for _ in range(B * H)]).view(B, H, N)
+    qn, kn = (x.transpose(1, 2).contiguous().to(DEV) for x in (q, k))  # NHD storage
+    q8, qs, k8, ks, km = vcx.prepare_qk(qn.transpose(1, 2), kn.transpose(1, 2), perm.to(DEV))
+    ekm = o.k_mean(bits(k), perm.numpy())
+    ek8, eks = o.quant_k(bits(k), ekm, perm.numpy())
+    eq8, eqs = o.quant_q(bits(q))
+    np.testing.assert_array_equal(q8.cpu().numpy(), eq8)
+    np.testing.assert_array_equal(k8.cpu().numpy(), ek8)
+    np.testing.assert_array_equal(ks.cpu().numpy().view(np.uint32), eks.view(np.uint32))
+    np.testing.assert_array_equal(qs.cpu().numpy().view(np.uint32), eqs.view(np.uint32))
+
+
+@pytest.mark.parametrize("shape", SHAPES, ids=_ids)
+@pytest.mark.parametrize("mode", ["channel_fp8", "smooth_channel", "smooth_block"])
+def test_prepare_v_bit_exact(shape, mode):
+    B, H, Nq, Nk, D, dt = shape
+    _print_case("prepare_v", _ids(shape), mode)
+    _, _, v = make_qkv(B, H, Nq, Nk, D, dt, seed=2, kind="outlier")
+    if Nk > 3:
+        v[0, 0, :, 3] = 0  # zero channel
+    name = dtype_name(dt)
+    smooth = mode != "channel_fp8"
+    channel = mode != "smooth_block"
+    v8, vs, means = vcx.prepare_v(v.to(DEV), None, smooth=smooth, channel_scale=channel)
+    tok = vcx.value_token()
+    got = storage_to_logical(v8, tok)
+    if smooth:
+        ev8, evs, emeans = o.prepare_values(bits(v), None, channel, name)
+        np.testing.assert_array_equal(means.view(torch.int16).cpu().numpy().view(np.uint16), emeans)
+    else:
+        ev8, evs = o.per_channel_fp8(bits(v), None, name)
+    np.testing.assert_array_equal(got, ev8)
+    np.testing.assert_array_equal(vs.cpu().numpy().view(np.uint32), evs.view(np.uint32))
+
+
+@pytest.mark.parametrize("dim", [64, 128])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("n,clusters,iterations", [(1, 8, 2), (7, 8, 1), (127, 3, 3), (128, 1, 2), (129, 8, 2),
+                                                   (2049, 8, 2), (5000, 8, 3)])
+def test_grouping_bit_exact(dim, dtype, n, clusters, iterations):
+    _print_case("grouping", dim, dtype, n, clusters, iterations)
+    torch.manual_seed(211 + n)
+    v = torch.randn(2, 2, n, dim).to(dtype)
+    perm, labels, centers = vcx.group_values(v.to(DEV), clusters, iterations, debug=True)
+    eperm, elabels, ecenters = o.group_values(bits(v), clusters, iterations, dtype_name(dtype))
+    np.testing.assert_array_equal(labels.cpu().numpy(), elabels)
+    np.testing.assert_array_equal(centers.cpu().numpy().view(np.uint32), ecenters.view(np.uint32))
+    np.testing.assert_array_equal(perm.cpu().numpy(), eperm)
+
+
+def test_grouping_known_answers():
+    x = torch.tensor([2, 0, 1, 2, 1, 0], dtype=torch.float32)
+    v = x.view(1, 1, 6, 1).expand(2, 2, 6, 64).contiguous().to(torch.bfloat16).to(DEV)
+    perm = vcx.group_values(v, 3, 2)
+    for row in perm.cpu().reshape(-1, 6):
+        assert row.tolist() == [0, 3, 2, 4, 1, 5]
+    v = torch.full((2, 3, 257, 128), 2.0, dtype=torch.bfloat16, device=DEV)
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        perm, labels, centers = vcx.group_values(v, 8, 3, debug=True)
+        total = labels.sum()
+    stream.synchronize()
+    assert total.item() == 0
+    assert torch.equal(perm.cpu(), torch.arange(257).expand(2, 3, 257))
+    assert (centers == 2).all().item()
+
+
+# ------------------------------------------------------------------ fused attention
+
+def _to_dev(a):
+    a = np.ascontiguousarray(a)
+    if a.dtype == np.uint16:
+        a = a.view(np.int16)
+    return torch.from_numpy(a).to(DEV)
+
+
+def _oracle_state(q, k, v, smooth, dt):
+    return o.prepare(bits(q), bits(k), bits(v), v_smooth=smooth, dtype=dtype_name(dt))
+
+
+ATTN = [  # B, H, Nq, Nk, D, dtype, smooth
+    (1, 2, 2048, 2048, 128, torch.bfloat16, False),
+    (1, 2, 2048, 2048, 128, torch.bfloat16, True),
+    (1, 1, 1, 1, 128, torch.bfloat16, False),
+    (2, 3, 65, 129, 64, torch.float16, True),
+    (1, 2, 257, 385, 128, torch.float16, False),
+    (1, 1, 63, 127, 64, torch.bfloat16, False),
+    (1, 1, 129, 513, 64, torch.bfloat16, True),
+    (1, 1, 200, 4097, 128, torch.bfloat16, True),
+]
+
+
+@pytest.mark.parametrize("case", ATTN, ids=lambda c: _ids(c[:6]) + ("_smooth" if c[6] else ""))
+def test_attention_p_bytes_bit_exact_and_output_tolerance(case):
+    B, H, Nq, Nk, D, dt, smooth = case
+    _print_case("attention", case)
+    q, k, v = make_qkv(B, H, Nq, Nk, D, dt, seed=7, kind="outlier" if smooth else "normal")
+    st = _oracle_state(q, k, v, smooth, dt)
+    tok = vcx.value_token()
+    # Feed the kernel the oracle's payloads (storage order) so the kernel is tested on its own.
+    to = _to_dev
+    v8 = to(logical_to_storage(st["v"], tok)).view(torch.float8_e4m3fn)
+    means = to(st["means"]).view(torch.float16) if smooth else None
+    rows = (0, Nq)
+    out, pd = vcx.forward(to(st["q"]), to(st["k"]), v8, to(st["qs"]), to(st["ks"]), to(st["vs"]), means,
+                          True, smooth, st["output_type"], st["scale"], p_rows=rows)
+    eout, ecodes = o.reference(st, return_codes=True)
+    np.testing.assert_array_equal(pd.cpu().numpy(), ecodes)
+    got = out.float().cpu().numpy()
+    assert np.isfinite(got).all()
+    err, bound = output_bound(got, eout)
+    assert np.all(err <= bound), float((err - bound).max())
+    assert cosine(got, eout) >= 0.9999
+    # the production (non-dump) kernel gives the same output bits
+    out2 = vcx.forward(to(st["q"]), to(st["k"]), v8, to(st["qs"]), to(st["ks"]), to(st["vs"]), means,
+                       True, smooth, st["output_type"], st["scale"])
+    assert torch.equal(out2, out)
+
+
+def test_uniform_attention_three_unequal_blocks_known_answer():
+    # scripts/validate_sage_vc.py:479-492: q = k = 0, three unequal V blocks; output = mean of V.
+    from sageattention_local import sageattn_vc
+    for dtype in (torch.float16, torch.bfloat16):
+        q = torch.zeros(1, 2, 65, 128, device=DEV, dtype=dtype)
+        k = torch.zeros(1, 2, 257, 128, device=DEV, dtype=dtype)
+        channels = torch.linspace(-2, 2, 128, device=DEV)
+        v = torch.empty_like(k)
+        v[:, :, :128] = channels
+        v[:, :, 128:256] = channels * 2 + 3
+        v[:, :, 256:] = channels * 0.25 - 6
+        expected = v.float().mean(2, keepdim=True).expand_as(q).to(dtype)
+        # With smoothing every block is its own mean: residual bytes are zero and the
+        # mean restoration alone must give the exact average (the reference's check).
+        out = sageattn_vc(q, k, v, expcast=True, v_smooth=True)
+        torch.testing.assert_close(out, expected, rtol=0.004, atol=0.004)
+        # Without smoothing the weights are still uniform: the output is the mean of
+        # the DECODED FP8 payload times the channel scale.
+        state_v8, vs, _ = vcx.prepare_v(v)
+        dec = torch.from_numpy(o.e4m3_decode(storage_to_logical(state_v8, vcx.value_token())[..., :257]))
+        expected_fp8 = (dec.double().mean(-1) * vs.cpu().double()).unsqueeze(2).expand(1, 2, 65, 128)
+        out = sageattn_vc(q, k, v, expcast=True, v_smooth=False)
+        torch.testing.assert_close(out.double().cpu(), expected_fp8, rtol=0.004, atol=0.004)
+
+
+def test_sageattn_vc_end_to_end_config1_payloads_and_output():
+    # Config 1 of the benchmark: BNSD [1,2,2048,128] bf16, smoothing off and on.
+    from sageattention_local import prepare, forward_prepared, sageattn_vc
+    q, k, v = make_qkv(1, 2, 2048, 2048, 128, torch.bfloat16, seed=0)
+    qd, kd, vd = (x.to(DEV) for x in (q, k, v))
+    tok = vcx.value_token()
+    for smooth in (False, True):
+        _print_case("end-to-end config1", smooth)
+        st = prepare(qd, kd, vd, v_smooth=smooth)
+        ost = _oracle_state(q, k, v, smooth, torch.bfloat16)
+        for key in ("q", "k", "qs", "ks"):
+            np.testing.assert_array_equal(st[key].cpu().numpy(), ost[key])
+        np.testing.assert_array_equal(storage_to_logical(st["v"], tok), ost["v"])
+        np.testing.assert_array_equal(st["vs"].cpu().numpy(), ost["vs"])
+        if smooth:
+            np.testing.assert_array_equal(st["permutation"].cpu().numpy(), ost["permutation"])
+            np.testing.assert_array_equal(st["means"].view(torch.int16).cpu().numpy().view(np.uint16), ost["means"])
+        out = forward_prepared(st).float().cpu().numpy()
+        eout = o.reference(ost)
+        err, bound = output_bound(out, eout)
+        assert np.all(err <= bound)
+        assert cosine(out, eout) >= 0.9999
+        full = sageattn_vc(qd, kd, vd, v_smooth=smooth)
+        assert torch.equal(full.float().cpu(), torch.from_numpy(out))
+
+
+def test_hnd_and_nhd_layouts_exact():
+    # scripts/validate_sage_vc.py:493-498
+    from sageattention_local import sageattn_vc
+    q, k, v = (x.to(DEV) for x in make_qkv(1, 2, 257, 300, 128, torch.bfloat16, seed=338))
+    for smooth in (False, True):
+        hnd = sageattn_vc(q, k, v, v_smooth=smooth)
+        nhd = sageattn_vc(*(x.transpose(1, 2).contiguous() for x in (q, k, v)), tensor_layout="NHD", v_smooth=smooth)
+        assert torch.equal(hnd, nhd.transpose(1, 2))
+
+
+def test_full_length_prep_exact_and_sampled_p_bytes():
+    # The main shape's sequence length (37741) with 2 heads: every payload byte,
+    # and P bytes of a sampled row range, against the oracle.
+    B, H, N, D = 1, 2, 37741, 128
+    q, k, v = make_qkv(B, H, N, N, D, torch.bfloat16, seed=0)
+    _print_case("full-length", N)
+    qd, kd, vd = (x.to(DEV) for x in (q, k, v))
+    q8, qs, k8, ks, km = vcx.prepare_qk(qd, kd)
+    v8, vs, _ = vcx.prepare_v(vd)
+    st = _oracle_state(q, k, v, False, torch.bfloat16)
+    np.testing.assert_array_equal(q8.cpu().numpy(), st["q"])
+    np.testing.assert_array_equal(k8.cpu().numpy(), st["k"])
+    np.testing.assert_array_equal(qs.cpu().numpy(), st["qs"])
+    np.testing.assert_array_equal(ks.cpu().numpy(), st["ks"])
+    np.testing.assert_array_equal(storage_to_logical(v8, vcx.value_token()), st["v"])
+    np.testing.assert_array_equal(vs.cpu().numpy(), st["vs"])
+    r0, r1 = 18800, 18816
+    out, pd = vcx.forward(q8, k8, v8, qs, ks, vs, None, True, False, 1, D ** -0.5, p_rows=(r0, r1))
+    eout, ecodes = o.reference(st, query_indices=np.arange(r0, r1), return_codes=True)
+    np.testing.assert_array_equal(pd.cpu().numpy(), ecodes)
+    got = out[:, :, r0:r1].float().cpu().numpy()
+    err, bound = output_bound(got, eout)
+    assert np.all(err <= bound)
+    assert cosine(got, eout) >= 0.9999

@@ -1,0 +1,429 @@
+"""Pins of the CPU oracle (oracle/vc_oracle.c) against the reference's known answers,
+golden vectors, closed forms and library routines. CPU only.
+
+Each test names the reference file:line whose known answer it reproduces, or the
+independent check it relies on (torch's E4M3 cast, exact rational sums, an FP64
+Lloyd written differently from the oracle, the Triton quantizer's own outputs).
+"""
+import math
+from fractions import Fraction
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import bits, make_qkv
+from oracle import vc_oracle as o
+
+GOLDEN = Path(__file__).resolve().parent / "golden" / "int8_per_thread.npz"
+
+
+# ------------------------------------------------------------------ ExpCast / E4M3
+
+def test_expcast_known_answers_core():
+    # tests/test_core.py:17-22 of the reference (paper worked example included).
+    u = torch.tensor([0.0, -1.0, -1.6, -8.0, -14.0, -100.0, -float("inf")])
+    codes = o.expcast_codes((u / math.log2(math.e)).numpy())
+    assert codes.tolist() == [120, 112, 107, 56, 8, 0, 0]
+    assert o.e4m3_decode(codes).tolist() == [256, 128, 88, 1, 2 ** -6, 0, 0]
+
+
+def test_expcast_known_answers_sage_vc():
+    # tests/test_sage_vc.py:22-25 of the reference.
+    codes = o.expcast_codes(np.array([-np.inf, -20.0, 0.0, 1.0], np.float32))
+    assert codes.tolist() == [0, 0, 120, 120]
+    assert o.e4m3_decode(codes).tolist() == [0.0, 0.0, 256.0, 256.0]
+
+
+def test_expcast_paper_example():
+    # tests/test_paper_expcast.py:38-44: -1.60/log2(e) -> 107 -> 88.0
+    shifted = np.float32(torch.tensor(-1.60 / 1.4426950408889634).item())
+    c = o.expcast_codes(np.array([shifted], np.float32))
+    assert c[0] == 107 and o.e4m3_decode(c)[0] == 88.0
+
+
+def test_expcast_single_rounding_fma_against_exact_arithmetic():
+    # The encoder is RNE(fl32(x*A + B)) with ONE rounding of the exact x*A+B.
+    # Check against exact rational arithmetic on values spread over the domain,
+    # including the reference sweep points (scripts/validate_sage_vc.py:22-24).
+    A, B = Fraction(float(np.float32(11.541560173034668))), Fraction(float(np.float32(119.6500015258789)))
+    xs = np.concatenate([np.linspace(-15, 1, 4001, dtype=np.float32), np.array([-20.0, 0.0], np.float32)])
+    codes = o.expcast_codes(xs)
+    for x, c in zip(xs.tolist(), codes.tolist()):
+        exact = Fraction(x) * A + B
+        f = float(np.float32(float(exact)))  # round exact value once to fp32 (RN via double: exact fits 2*24+ bits)
+        # float(exact) rounds to double first; recheck the tie case exactly
+        v = Fraction(f)
+        expect = min(120, max(0, round(v)))  # Python round: half to even, exact on Fractions
+        assert c == expect, (x, c, expect)
+
+
+def test_e4m3_decode_closed_form_all_codes():
+    # tests/test_core.py:89-91 numpy decode formula, all positive codes below NaN.
+    code = np.arange(0, 127, dtype=np.uint8)
+    exponent, mantissa = code >> 3, code & 7
+    values = np.where(exponent == 0, mantissa * 2.0 ** -9, (1 + mantissa / 8) * 2.0 ** (exponent.astype(int) - 7))
+    np.testing.assert_array_equal(o.e4m3_decode(code), values.astype(np.float32))
+    np.testing.assert_array_equal(o.e4m3_decode(code | 0x80), -values.astype(np.float32))
+    assert np.isnan(o.e4m3_decode(np.array([0x7F, 0xFF], np.uint8))).all()
+
+
+def test_e4m3_encode_matches_torch_cast_and_roundtrips():
+    rng = np.random.default_rng(0)
+    x = np.concatenate([rng.standard_normal(200000).astype(np.float32) * 40,
+                        (rng.random(100000).astype(np.float32) - 0.5) * 0.05,
+                        np.array([0.0, -0.0, 448.0, -448.0, 1e-30, -1e-30], np.float32)])
+    # torch's CPU cast does not saturate (F7), so clamp first, as the kernels do.
+    ref = torch.from_numpy(np.clip(x, -448, 448)).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    np.testing.assert_array_equal(o.e4m3_encode(x), ref)
+    codes = np.array([c for c in range(256) if (c & 0x7F) != 0x7F], np.uint8)
+    np.testing.assert_array_equal(o.e4m3_encode(o.e4m3_decode(codes)), codes)
+    # midpoints between neighbours round to the even code; saturation above 448
+    for c in range(1, 0x7E):
+        lo, hi = o.e4m3_decode(np.array([c, c + 1], np.uint8))
+        mid = np.float32((np.float64(lo) + np.float64(hi)) / 2)
+        assert o.e4m3_encode(np.array([mid], np.float32))[0] == (c if c % 2 == 0 else c + 1)
+    assert o.e4m3_encode(np.array([500.0, 1e30, np.inf], np.float32)).tolist() == [0x7E, 0x7E, 0x7E]
+
+
+def test_cvt_u8_model():
+    x = np.array([-np.inf, -1.0, -0.4, 0.5, 1.5, 2.5, 119.5, 120.49, 254.5, 255.6, 1e9, np.nan], np.float32)
+    assert o.cvt_u8(x).tolist() == [0, 0, 0, 0, 2, 2, 120, 120, 254, 255, 255, 0]
+
+
+def test_value_permutation_known_answer():
+    # tests/test_sage_vc.py:26-28 of the reference.
+    perm = o.value_permutation(256)
+    assert perm[:16].tolist() == [0, 1, 4, 5, 8, 9, 12, 13, 2, 3, 6, 7, 10, 11, 14, 15]
+    assert sorted(perm.tolist()) == list(range(256))
+
+
+# ------------------------------------------------------------------ fixed-order sums
+
+def test_tile_tree_sum_is_exact_when_representable_and_order_sensitive_otherwise():
+    rng = np.random.default_rng(1)
+    x = rng.integers(-1000, 1000, 128).astype(np.float64) / 64
+    assert o.tile_tree_sum(x) == float(sum(Fraction(v) for v in x))
+    # A case where order matters: the documented tree pairs key kk with kk^1 first.
+    y = np.zeros(128)
+    y[0], y[1], y[16] = 1e16, 1.0, -1e16   # kk=0 chain: 1e16 + (-1e16) = 0, then + a[1] = 1
+    assert o.tile_tree_sum(y) == 1.0
+
+
+# ------------------------------------------------------------------ INT8 quantizer
+
+def test_int8_quantizer_matches_reference_triton_golden_vectors():
+    # Vectors written by tests/golden/make_int8_vectors.py from the reference's
+    # own per_thread_int8 (quant_per_thread.py:154-204) under TRITON_INTERPRET=1.
+    z = np.load(GOLDEN)
+    cases = sorted({k.split("_")[0] for k in z.files})
+    assert len(cases) == 4
+    for c in cases:
+        B, H, Nq, Nk, D, bf, _ = z[f"{c}_meta"].tolist()
+        dt = "bfloat16" if bf else "float16"
+        q8, qs = o.quant_q(z[f"{c}_q"], dt)
+        k8, ks = o.quant_k(z[f"{c}_k"], z[f"{c}_km"].reshape(B, H, D), None, dt)
+        np.testing.assert_array_equal(q8, z[f"{c}_q8"])
+        np.testing.assert_array_equal(qs.view(np.uint32), z[f"{c}_qs"].view(np.uint32))
+        np.testing.assert_array_equal(k8, z[f"{c}_k8"])
+        np.testing.assert_array_equal(ks.view(np.uint32), z[f"{c}_ks"].view(np.uint32))
+
+
+def test_int8_quantizer_invariants():
+    q, k, _ = make_qkv(1, 2, 193, 300, 64, seed=5)
+    q8, qs = o.quant_q(bits(q))
+    assert np.abs(q8.astype(int)).max() <= 127
+    qf = q.float().numpy()
+    rows = np.arange(193)
+    sidx = (rows // 16) * 8 + rows % 8
+    s = qs[:, :, sidx][..., None]
+    assert np.all(np.abs(qf - q8 * s) <= s / 2 * (1 + 1e-5) + 1e-12)
+    # the element of largest magnitude of each group maps to +-127
+    g = qf[0, 0]
+    for blk in range(0, 193, 16):
+        for t in range(8):
+            grp = [r for r in (blk + t, blk + t + 8) if r < 193]
+            if not grp:
+                continue
+            vals = g[grp]
+            i = np.unravel_index(np.abs(vals).argmax(), vals.shape)
+            assert abs(int(q8[0, 0][grp][i])) == 127
+    # padded groups (rows >= N) get the 1e-7 floor
+    assert qs[0, 0, -1] == np.float32(np.float32(0.0) / np.float32(127.0) + np.float32(1e-7))
+
+
+# ------------------------------------------------------------------ K mean
+
+def test_k_mean_exact_and_within_torch_mean():
+    _, k, _ = make_qkv(2, 2, 8, 1000, 128, seed=7)
+    km = o.k_mean(bits(k))
+    kf = k.double().numpy()
+    exact = np.float32(kf.sum(axis=2) / 1000)  # exact here: all values sum without rounding in fp64
+    assert np.array_equal(km, bits(torch.from_numpy(exact).to(torch.bfloat16)))
+    torch_mean = k.mean(dim=2).float().numpy()   # the reference's formula (vc.py:158)
+    ours = torch.from_numpy(km.view(np.int16)).view(torch.bfloat16).float().numpy()
+    ulp = np.abs(torch_mean) * 2 ** -7 + 1e-30
+    assert np.all(np.abs(ours - torch_mean) <= ulp)
+
+
+# ------------------------------------------------------------------ V quantizers
+
+def test_v_channel_matches_torch_formula_and_invariants():
+    _, _, v = make_qkv(1, 2, 1, 300, 64, seed=9)
+    v[0, 1, :, 5] = 0  # a zero channel
+    v8, vs = o.per_channel_fp8(bits(v))
+    vf = v.float()
+    amax = vf.abs().amax(dim=2)
+    r = torch.tensor(448.0) / amax                       # IEEE fp32 division
+    expect = (vf * r.unsqueeze(2)).clamp(-448, 448).to(torch.float8_e4m3fn).view(torch.uint8)
+    expect[0, 1, :, 5] = 0
+    got = v8[..., :300].transpose(0, 1, 3, 2)
+    np.testing.assert_array_equal(got, expect.numpy())
+    assert np.all(v8[..., 300:] == 0)
+    np.testing.assert_array_equal(vs, (amax / torch.tensor(448.0)).numpy())
+    assert vs[0, 1, 5] == 0
+    # the channel maximum encodes to 448 (0x7E, or 0xFE if negative)
+    idx = vf.abs().argmax(dim=2)
+    for h in range(2):
+        for d in range(64):
+            if d == 5 and h == 1:
+                continue
+            assert v8[0, h, d, idx[0, h, d]] & 0x7F == 0x7E
+
+
+@pytest.mark.parametrize("n", [1, 127, 128, 129, 257])
+@pytest.mark.parametrize("channel", [True, False])
+def test_v_smoothing_reference_tolerances(n, channel):
+    # scripts/validate_sage_vc.py:29-65 of the reference: unequal block means and
+    # scales, constant channels; scale rtol 2e-5, means*vs rtol 8e-4, residual
+    # bound 0.063|r| + vs/512 + 3e-6, zero padding.
+    torch.manual_seed(339)
+    v = torch.randn(2, 2, n, 64)
+    for t, begin in enumerate(range(0, n, 128)):
+        v[:, :, begin:begin + 128] = v[:, :, begin:begin + 128] * (t + 1) + t * 3
+    v[..., 0] = 1.5
+    v[..., 1] = -2.0
+    v = v.to(torch.bfloat16)
+    v8, vs, means = o.prepare_values(bits(v), channel_scale=channel)
+    unpacked = torch.from_numpy(o.e4m3_decode(v8)).transpose(-1, -2)
+    meansf = torch.from_numpy(means.view(np.float16).astype(np.float32))
+    blocks = []
+    for begin in range(0, n, 128):
+        rows = v[:, :, begin:begin + 128].float()
+        mean = rows.mean(2)
+        residual = rows - mean.unsqueeze(2)
+        blocks.append((mean, residual, residual.abs().amax(2)))
+    vs_t = torch.from_numpy(vs)
+    if channel:
+        peak = torch.stack([b[2] for b in blocks]).amax(0)
+        mean_peak = torch.stack([b[0].abs() for b in blocks]).amax(0)
+        expected_scale = torch.maximum(torch.where(peak > 0, peak / 448., 1.), mean_peak / 65504.)
+        torch.testing.assert_close(vs_t, expected_scale, rtol=2e-5, atol=1e-7)
+    for t, (mean, residual, peak) in enumerate(blocks):
+        scale = vs_t if channel else vs_t[:, :, t]
+        if not channel:
+            expected_scale = torch.maximum(torch.where(peak > 0, peak / 448., 1.), mean.abs() / 65504.)
+            torch.testing.assert_close(scale, expected_scale, rtol=2e-5, atol=1e-7)
+        torch.testing.assert_close(meansf[:, :, t] * scale, mean, rtol=8e-4, atol=2e-6)
+        decoded = unpacked[:, :, t * 128:t * 128 + residual.shape[2]]
+        err = (decoded * scale.unsqueeze(2) - residual).abs()
+        bound = residual.abs() * .063 + scale.unsqueeze(2) / 512 + 3e-6
+        assert torch.all(err <= bound)
+    if n % 128:
+        assert np.count_nonzero(v8[..., n:]) == 0
+
+
+@pytest.mark.parametrize("n", [1, 129, 4097])
+def test_v_smoothing_constant_blocks_and_large_means(n):
+    # tests/test_sage_vc_preprocess_cuda.py:48-65: constants per block/channel above
+    # the FP16 range; residual bytes all zero; means*scale restore the constants.
+    v = torch.zeros(2, 3, n, 64)
+    for t, start in enumerate(range(0, n, 128)):
+        v[:, :, start:start + 128] = (torch.arange(64) - 31) * (t + 1) * 10000.
+    v = v.to(torch.bfloat16)
+    v8, vs, means = o.prepare_values(bits(v))
+    restored = torch.from_numpy(means.view(np.float16).astype(np.float32)) * torch.from_numpy(vs).unsqueeze(2)
+    assert np.isfinite(vs).all() and np.isfinite(means.view(np.float16)).all()
+    assert np.count_nonzero(o.e4m3_decode(v8)) == 0
+    torch.testing.assert_close(restored, v[:, :, ::128].float(), rtol=5e-4, atol=1e-6)
+
+
+def test_v_smoothing_reduction_beyond_one_warp():
+    # tests/test_sage_vc_preprocess_cuda.py:68-80 (fp32 input there; bf16 here).
+    torch.manual_seed(919)
+    v = torch.randn(2, 3, 4353, 128) * .01
+    v[:, :, 4224:4352] *= 1000
+    v[:, :, -1] = 90000
+    v = v.to(torch.bfloat16)
+    v8, vs, means = o.prepare_values(bits(v))
+    vf = v.float()
+    blocks = [vf[:, :, i:i + 128] for i in range(0, vf.shape[2], 128)]
+    raw_means = torch.stack([x.mean(2) for x in blocks], 2)
+    peaks = torch.stack([(x - x.mean(2, keepdim=True)).abs().amax(2) for x in blocks], 2).amax(2)
+    expected = torch.maximum(peaks / 448, raw_means.abs().amax(2) / 65504)
+    torch.testing.assert_close(torch.from_numpy(vs), expected, rtol=2e-5, atol=1e-7)
+    m = torch.from_numpy(means.view(np.float16).astype(np.float32))
+    torch.testing.assert_close(m * torch.from_numpy(vs).unsqueeze(2), raw_means, rtol=1e-3, atol=1e-5)
+
+
+# ------------------------------------------------------------------ grouping
+
+def fp64_lloyd(v, clusters, iterations):
+    """The reference's independent FP64 oracle (tests/test_sage_vc_grouping_cuda.py:8-23)."""
+    count = min(clusters, v.shape[2])
+    ids = torch.linspace(0, v.shape[2] - 1, count).long()
+    x = v.double()
+    centers = x.index_select(2, ids)
+    for step in range(iterations):
+        distances = (x.unsqueeze(-2) - centers.unsqueeze(2)).square().sum(-1)
+        labels = distances.argmin(-1)
+        if step + 1 < iterations:
+            centers = torch.stack([
+                torch.where((labels == c).sum(-1, keepdim=True) > 0,
+                            (x * (labels == c).unsqueeze(-1)).sum(2) / (labels == c).sum(-1, keepdim=True).clamp_min(1),
+                            centers[:, :, c]) for c in range(count)], 2)
+    return labels, centers
+
+
+@pytest.mark.parametrize("n,clusters,iterations", [(1, 8, 2), (7, 8, 1), (127, 3, 3), (128, 1, 2), (129, 8, 2), (2049, 8, 2)])
+def test_grouping_matches_independent_fp64_lloyd(n, clusters, iterations):
+    torch.manual_seed(211 + n)
+    v = torch.randn(2, 2, n, 64).to(torch.bfloat16)
+    perm, labels, centers = o.group_values(bits(v), clusters, iterations)
+    expected, expected_centers = fp64_lloyd(v, clusters, iterations)
+    np.testing.assert_array_equal(labels, expected.numpy())
+    np.testing.assert_allclose(centers, expected_centers.numpy(), rtol=2e-5, atol=2e-6)
+    np.testing.assert_array_equal(perm, expected.argsort(dim=-1, stable=True).numpy())
+
+
+def test_grouping_known_answers():
+    # scripts/validate_sage_vc.py:66-76: labels [2,0,1,2,1,0] -> perm [0,3,2,4,1,5]
+    x = torch.tensor([2, 0, 1, 2, 1, 0], dtype=torch.float32)
+    v = x.view(1, 1, 6, 1).expand(2, 2, 6, 64).contiguous().to(torch.bfloat16)
+    perm, labels, _ = o.group_values(bits(v), 3, 2)
+    for row in perm.reshape(-1, 6):
+        assert row.tolist() == [0, 3, 2, 4, 1, 5]
+    # tests/test_sage_vc_grouping_cuda.py:122-133: constant V -> label 0, identity, centers kept
+    v = torch.full((2, 3, 257, 128), 2.0).to(torch.bfloat16)
+    for it in (1, 2, 3):
+        perm, labels, centers = o.group_values(bits(v), 8, it)
+        assert labels.sum() == 0
+        np.testing.assert_array_equal(perm, np.broadcast_to(np.arange(257), (2, 3, 257)))
+        assert (centers == 2).all()
+
+
+def test_linspace_ids_match_torch():
+    for n in list(range(1, 300)) + [37741, 32760, 75482]:
+        for count in range(1, 9):
+            c = min(count, n)
+            assert o.linspace_ids(n, c).tolist() == torch.linspace(0, n - 1, c).long().tolist()
+
+
+# ------------------------------------------------------------------ attention oracle known answers
+
+def payload(nq, nk, block_values, dim=64):
+    """The reference's fixed payload (tests/test_sage_vc.py:31-39), ExpCast only."""
+    tiles = (nk + 127) // 128
+    return {"q": np.zeros((1, 1, nq, dim), np.int8), "k": np.zeros((1, 1, nk, dim), np.int8),
+            "v": np.zeros((1, 1, dim, tiles * 128), np.uint8),
+            "qs": np.ones((1, 1, ((nq + 63) // 64) * 32), np.float32), "ks": np.ones((1, 1, tiles * 4), np.float32),
+            "vs": np.ones((1, 1, tiles, dim), np.float32) if block_values else np.ones((1, 1, dim), np.float32),
+            "means": np.zeros((1, 1, tiles, dim), np.uint16) if block_values else None,
+            "expcast": True, "block_values": block_values, "scale": dim ** -0.5}
+
+
+def f16bits(values):
+    return np.asarray(values, np.float16).view(np.uint16)
+
+
+def test_block_mean_restoration_and_tail_weight_known_answer():
+    # tests/test_sage_vc.py:42-49 (expcast=True arm).
+    s = payload(65, 257, True)
+    s["means"][0, 0] = f16bits(np.array([1., -2., 6.])[:, None] * np.ones((1, 64)))
+    s["vs"][0, 0] = np.array([2., 3., 4.])[:, None]
+    out = o.reference(s)
+    np.testing.assert_allclose(out, (128 * 2 + 128 * (-6) + 24) / 257, rtol=2e-6, atol=1e-6)
+
+
+@pytest.mark.parametrize("block_values", [False, True])
+def test_single_key_preserves_nonzero_value(block_values):
+    # tests/test_sage_vc.py:52-65 (expcast=True arm: weight 1).
+    s = payload(17, 1, block_values)
+    data = (np.arange(64) % 9 - 4).astype(np.float32)
+    s["v"][0, 0, :, 0] = o.e4m3_encode(data)
+    s["vs"][...] = 0.125
+    if block_values:
+        s["means"][...] = f16bits(2.0)
+    out = o.reference(s)
+    expected = (data + (2 if block_values else 0)) * 0.125
+    np.testing.assert_allclose(out, np.broadcast_to(expected, out.shape), rtol=1e-6, atol=1e-6)
+
+
+def test_query_sampling_keeps_original_scale_indices():
+    # tests/test_sage_vc.py:68-79
+    s = payload(129, 129, False)
+    rng = np.random.default_rng(778)
+    s["q"][...] = rng.integers(-3, 4, s["q"].shape)
+    s["k"][...] = rng.integers(-3, 4, s["k"].shape)
+    s["qs"][...] = rng.uniform(0.1, 0.3, s["qs"].shape)
+    s["ks"][...] = rng.uniform(0.2, 0.5, s["ks"].shape)
+    s["v"][...] = o.e4m3_encode(rng.standard_normal(s["v"].shape).astype(np.float32))
+    ids = [0, 7, 8, 15, 16, 63, 64, 128]
+    all_rows, all_codes = o.reference(s, return_codes=True)
+    sampled, codes = o.reference(s, query_indices=ids, return_codes=True)
+    np.testing.assert_array_equal(sampled, all_rows[:, :, ids])
+    np.testing.assert_array_equal(codes, all_codes[:, :, ids])
+
+
+def test_channel_scale_epilogue_matches_expanded_per_tile_scales():
+    # tests/test_sage_vc.py:82-95
+    rng = np.random.default_rng(918)
+    s = payload(65, 257, True)
+    s["q"][...] = rng.integers(-4, 5, s["q"].shape)
+    s["k"][...] = rng.integers(-4, 5, s["k"].shape)
+    s["qs"][...] = .1
+    s["ks"][...] = .15
+    s["v"][...] = o.e4m3_encode(rng.standard_normal(s["v"].shape).astype(np.float32))
+    s["means"][...] = f16bits(rng.standard_normal(s["means"].shape))
+    scales = np.linspace(.01, 1, 64, dtype=np.float32).reshape(1, 1, 64)
+    channel = dict(s, vs=scales)
+    old = dict(s, vs=np.ascontiguousarray(np.broadcast_to(scales[:, :, None], (1, 1, 3, 64))))
+    np.testing.assert_allclose(o.reference(channel), o.reference(old), rtol=5e-5, atol=1e-6)
+
+
+def test_shared_scale_nonzero_mean_known_answer():
+    # tests/test_sage_vc.py:98-105
+    s = payload(65, 257, True)
+    s["vs"] = np.full((1, 1, 64), .25, np.float32)
+    s["means"][0, 0] = f16bits(np.array([8., -24., 96.])[:, None] * np.ones((1, 64)))
+    out = o.reference(s)
+    np.testing.assert_allclose(out, (128 * 2 - 128 * 6 + 24) / 257, rtol=2e-6, atol=1e-6)
+
+
+def test_expcast_codes_agree_with_dense_numpy_formula_one_tile():
+    # tests/test_core.py:80-93: codes from clip(rint(8u + 119.65)) with u in double;
+    # the oracle's fp32 RN logits/subtraction/FMA may differ only at rounding ties.
+    rng = np.random.default_rng(3)
+    s = payload(19, 35, False, dim=64)
+    s["q"][...] = rng.integers(-20, 21, s["q"].shape)
+    s["k"][...] = rng.integers(-20, 21, s["k"].shape)
+    _, codes = o.reference(s, return_codes=True)
+    logits = (s["q"][0, 0].astype(np.float64) @ s["k"][0, 0].T.astype(np.float64)) * np.float32(64 ** -0.5)
+    u = (logits - logits.max(-1, keepdims=True)) * math.log2(math.e)
+    ref = np.clip(np.rint(8 * u + 119.65), 0, 120).astype(np.uint8)
+    got = codes[0, 0, :, :35]
+    assert np.mean(got == ref) > 0.99 and np.abs(got.astype(int) - ref).max() <= 1
+    assert np.all(codes[0, 0, :, 35:] == 0)
+
+
+def test_uniform_attention_equals_decoded_value_mean():
+    # scripts/validate_sage_vc.py:161-182 (ExpCast weight 1): q = k = 0.
+    rng = np.random.default_rng(4)
+    s = payload(65, 513, False)
+    s["v"][..., :513] = o.e4m3_encode((np.arange(513) / 128 - 2).astype(np.float32))[None, None, None, :]
+    s["vs"][...] = np.linspace(0.5, 1.5, 64)
+    dec = o.e4m3_decode(s["v"][0, 0, :, :513]).astype(np.float64)
+    expected = dec.mean(-1) * s["vs"][0, 0]
+    np.testing.assert_allclose(o.reference(s)[0, 0], np.broadcast_to(expected, (65, 64)), rtol=1e-6, atol=1e-6)
+    del rng

@@ -109,8 +109,12 @@ def main():
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="main", choices=sorted(CONFIGS))
-    ap.add_argument("--cpu-rows", type=int, default=32, help="query rows per head for the CPU baseline")
+    ap.add_argument("--cpu-rows", type=int, default=1024, help="query rows per head for the CPU baseline")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--mode", default="full", choices=("full", "kernel", "copy"),
+                    help="full: the benchmark; kernel: prepare once, then only the fused kernel "
+                         "(--steps launches, for profilers); copy: a plain 1 GiB device copy "
+                         "(calibrates profiler byte counters)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build runs the sageattn_vc path on ONE GPU; multi-GPU runs are not part of it "
@@ -123,6 +127,15 @@ def main():
     B, H, N, D, kind, smooth, desc = CONFIGS[args.config]
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.mode == "copy":
+        src = torch.ones(1 << 29, dtype=torch.int16, device=dev)  # 1 GiB
+        dst = torch.empty_like(src)
+        for _ in range(max(args.steps, 1)):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"mode": "copy", "bytes_read_per_launch": src.numel() * 2,
+                          "bytes_written_per_launch": dst.numel() * 2, "launches": max(args.steps, 1)}))
+        return
     qc, kc, vc_ = make_inputs(B, H, N, D, kind)
     q, k, v = (x.to(dev) for x in (qc, kc, vc_))
     scale = D ** -0.5
@@ -140,6 +153,13 @@ def main():
         q8, qs, k8, ks, v8, vs, means = p
         vcx.forward(q8, k8, v8, qs, ks, vs, means, True, smooth, 1, scale, out=out)
 
+    if args.mode == "kernel":
+        p = prep()
+        for _ in range(args.warmup + args.steps):
+            fused(p)
+        torch.cuda.synchronize()
+        print(json.dumps({"mode": "kernel", "launches": args.warmup + args.steps, "config": args.config}))
+        return
     for _ in range(args.warmup):
         fused(prep())
     torch.cuda.synchronize()

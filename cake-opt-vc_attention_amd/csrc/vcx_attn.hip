@@ -51,12 +51,17 @@ struct AttnArgs {
   int64_t prow0, prow1;
 };
 
+// XOR swizzles of the 16-byte chunk index inside an LDS row. A lane group
+// (16 lanes) of the QK A operand reads rows 16j + kr(l), kr = 0..15, at one
+// logical chunk; of the PV A operand rows 16cb + l. Both maps are bijective on
+// every 8-lane half (one 128-byte LDS pass) and on the whole 16-lane group (one
+// 256-byte pass), so neither reading model has bank conflicts.
 template <int D>
 __device__ inline int swz_k(int row) {
-  if constexpr (D == 128) return (row >> 1) & 7;
-  else return (row >> 2) & 3;
+  if constexpr (D == 128) return ((row >> 1) & 1) | (((row >> 3) & 1) << 1) | (((row ^ (row >> 2)) & 1) << 2);
+  else return (((row >> 1) ^ (row >> 2)) & 1) | (((row >> 3) & 1) << 1);
 }
-__device__ inline int swz_v(int row) { return (row >> 1) & 7; }
+__device__ inline int swz_v(int row) { return ((row >> 1) & 3) | (((row ^ (row >> 3)) & 1) << 2); }
 
 typedef __attribute__((address_space(3))) void lds_void;
 typedef const __attribute__((address_space(1))) void global_void;
@@ -66,6 +71,11 @@ typedef const __attribute__((address_space(1))) void global_void;
 // consecutive 16-byte slots (w*(D/32) + n)*64 + lane. A slot holds row
 // s/(D/16) (K) or s/8 (V^T) and the 16-byte chunk given by the XOR swizzle.
 // Lane-constant parts of the addresses are precomputed once per kernel.
+// Raw buffer resource over [base, base + bytes): out-of-range lanes read zeros.
+__device__ inline __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(bytes), 0x00020000);
+}
+
 template <int D, bool SMOOTH>
 struct TileLoader {
   // Meta region of a buffer: SMOOTH ? fp16 means of the tile (2*D bytes) : nothing,
@@ -73,46 +83,52 @@ struct TileLoader {
   static constexpr int ML = SMOOTH ? (2 * D) / 16 : 0;
   static constexpr int KS_OFF = 16 * ML;
   static constexpr int N = D / 32;  // instructions per wave per operand
-  int krow[N];                      // K row of each instruction (for the tail clamp)
-  int kcol[N];                      // byte offset of the chunk inside the K row
-  int voff[N];                      // byte offset inside the V^T tile column block
-  int64_t npad;
+  uint32_t koff[N];                 // lane byte offset inside the K tile (row*D + chunk*16)
+  uint32_t voff[N];                 // lane byte offset inside the V^T tile columns
+  uint32_t moff;                    // lane byte offset of the meta load (wave 0)
+  __amdgpu_buffer_rsrc_t rk, rv, rm, rs;
+  int wave;
 
-  __device__ inline void init(int64_t tiles) {
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    npad = tiles * kTile;
+  __device__ inline void init(const AttnArgs& a, int64_t bh) {
+    wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int64_t npad = a.tiles * kTile;
 #pragma unroll
     for (int n = 0; n < N; ++n) {
       const int s = (wave * N + n) * 64 + lane;
       const int row = s / (D / 16), phys = s % (D / 16);
-      krow[n] = row;
-      kcol[n] = (phys ^ swz_k<D>(row)) * 16;
+      koff[n] = static_cast<uint32_t>(row * D + ((phys ^ swz_k<D>(row)) * 16));
       const int ch = s >> 3, vphys = s & 7;
-      voff[n] = ch * static_cast<int>(npad) + ((vphys ^ swz_v(ch)) * 16);
+      voff[n] = static_cast<uint32_t>(ch * static_cast<int>(npad) + ((vphys ^ swz_v(ch)) * 16));
     }
+    // Per-head resources. K rows past Nk read zeros (their logits are masked anyway).
+    rk = make_rsrc(a.k8 + bh * a.Nk * D, static_cast<uint32_t>(a.Nk * D));
+    rv = make_rsrc(a.v8 + bh * D * npad, static_cast<uint32_t>(D * npad));
+    rs = make_rsrc(a.ks + bh * a.tiles * 4, static_cast<uint32_t>(a.tiles * 16));
+    if constexpr (SMOOTH) rm = make_rsrc(a.means + bh * a.tiles * D, static_cast<uint32_t>(a.tiles * D * 2));
+    moff = static_cast<uint32_t>(lane * 16);
   }
 
-  __device__ inline void issue(const AttnArgs& a, int64_t bh, int64_t t, uint8_t* lk, uint8_t* lv,
-                               uint8_t* lm) const {
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    if (wave == 0 && lane <= ML) {
-      const void* src = lane < ML ? static_cast<const void*>(a.means + (bh * a.tiles + t) * D + lane * 8)
-                                  : static_cast<const void*>(a.ks + (bh * a.tiles + t) * 4);
-      __builtin_amdgcn_global_load_lds((global_void*)src, (lds_void*)lm, 16, 0, 0);
+  // All addresses are a wave-uniform soffset (the tile) plus lane-constant
+  // voffsets: no per-lane address arithmetic in the loop.
+  __device__ inline void issue(int64_t t, uint8_t* lk, uint8_t* lv, uint8_t* lm) const {
+    const int lane = threadIdx.x & 63;
+    if (wave == 0) {
+      if constexpr (SMOOTH) {
+        if (lane < ML)
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(rm, (lds_void*)lm, 16, moff, static_cast<int>(t * D * 2), 0, 0);
+      }
+      if (lane == 0)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)(lm + KS_OFF), 16, 0, static_cast<int>(t * 16), 0, 0);
     }
-    const int8_t* kb = a.k8 + (bh * a.Nk + t * kTile) * D;
-    const int lim = static_cast<int>(a.Nk - t * kTile) - 1;  // last valid row of this tile
-    const uint8_t* vb = a.v8 + bh * D * npad + t * kTile;
-#pragma unroll
-    for (int n = 0; n < N; ++n) {
-      const int row = krow[n] < lim ? krow[n] : lim;  // rows past Nk: any in-bounds bytes (masked)
-      __builtin_amdgcn_global_load_lds((global_void*)(kb + row * D + kcol[n]),
-                                       (lds_void*)(lk + (wave * N + n) * 1024), 16, 0, 0);
-    }
+    const int kso = static_cast<int>(t * kTile * D);
 #pragma unroll
     for (int n = 0; n < N; ++n)
-      __builtin_amdgcn_global_load_lds((global_void*)(vb + voff[n]),
-                                       (lds_void*)(lv + (wave * N + n) * 1024), 16, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_void*)(lk + (wave * N + n) * 1024), 16, koff[n], kso, 0, 0);
+    const int vso = static_cast<int>(t * kTile);
+#pragma unroll
+    for (int n = 0; n < N; ++n)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (lds_void*)(lv + (wave * N + n) * 1024), 16, voff[n], vso, 0, 0);
   }
 };
 
@@ -310,25 +326,25 @@ __global__ __launch_bounds__(kThreadsPerBlock, 2) void attn_kernel(AttnArgs a) {
   }
 
   TileLoader<D, SMOOTH> ld;
-  ld.init(a.tiles);
-  ld.issue(a, bh, 0, lds0, lds0 + KB, meta0);
+  ld.init(a, bh);
+  ld.issue(0, lds0, lds0 + KB, meta0);
   // Tiles before the last, two per iteration so each buffer is a fixed LDS object.
   const int64_t body = a.tiles - 1;
   int64_t t = 0;
   for (; t + 2 <= body; t += 2) {
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-    ld.issue(a, bh, t + 1, lds1, lds1 + KB, meta1);
+    ld.issue(t + 1, lds1, lds1 + KB, meta1);
     w.template tile<false>(a, t, lds0, lds0 + KB, meta0);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-    ld.issue(a, bh, t + 2, lds0, lds0 + KB, meta0);
+    ld.issue(t + 2, lds0, lds0 + KB, meta0);
     w.template tile<false>(a, t + 1, lds1, lds1 + KB, meta1);
   }
   if (t < body) {  // odd count of body tiles: one more from buffer 0, last tile lands in buffer 1
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-    ld.issue(a, bh, t + 1, lds1, lds1 + KB, meta1);
+    ld.issue(t + 1, lds1, lds1 + KB, meta1);
     w.template tile<false>(a, t, lds0, lds0 + KB, meta0);
     ++t;
   }
@@ -362,6 +378,25 @@ __global__ __launch_bounds__(kThreadsPerBlock, 2) void attn_kernel(AttnArgs a) {
     }
   }
 }
+
+// Explicit instantiation of every launch variant: hipcc's host pass otherwise
+// emitted the kernel handle of only the first variant named in each ternary.
+template __global__ void attn_kernel<64, false, false, 0>(AttnArgs);
+template __global__ void attn_kernel<64, false, false, 1>(AttnArgs);
+template __global__ void attn_kernel<64, false, true, 0>(AttnArgs);
+template __global__ void attn_kernel<64, false, true, 1>(AttnArgs);
+template __global__ void attn_kernel<64, true, false, 0>(AttnArgs);
+template __global__ void attn_kernel<64, true, false, 1>(AttnArgs);
+template __global__ void attn_kernel<64, true, true, 0>(AttnArgs);
+template __global__ void attn_kernel<64, true, true, 1>(AttnArgs);
+template __global__ void attn_kernel<128, false, false, 0>(AttnArgs);
+template __global__ void attn_kernel<128, false, false, 1>(AttnArgs);
+template __global__ void attn_kernel<128, false, true, 0>(AttnArgs);
+template __global__ void attn_kernel<128, false, true, 1>(AttnArgs);
+template __global__ void attn_kernel<128, true, false, 0>(AttnArgs);
+template __global__ void attn_kernel<128, true, false, 1>(AttnArgs);
+template __global__ void attn_kernel<128, true, true, 0>(AttnArgs);
+template __global__ void attn_kernel<128, true, true, 1>(AttnArgs);
 
 template <int D, bool SMOOTH, bool DUMP, int OUT>
 int launch(const AttnArgs& a, int64_t nblocks, hipStream_t st) {

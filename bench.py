@@ -26,6 +26,12 @@ sys.path.insert(0, str(ROOT))
 PEAK_TOPS = 5000.0      # MI355X dense INT8 / FP8 MFMA, TOPS (published)
 PEAK_HBM_GBS = 8000.0   # MI355X HBM3E, GB/s (published)
 
+# HBM bytes per fused-kernel launch, measured with rocprofv3 --pmc FETCH_SIZE (scaled by
+# 2.0, the factor a plain 1 GiB copy reads) plus WRITE_SIZE (factor 1.0); the run and its
+# commands are in profiles/attn_kernel_main_hbm_bytes.txt. Counters cannot be read from
+# inside this process, so the figure is keyed by configuration and null where unmeasured.
+MEASURED_TRAFFIC_BYTES = {"main": 3.917e9}
+
 CONFIGS = {
     # name: (B, H, N, D, kind, v_smooth, description)
     "main": (1, 28, 37741, 128, "normal", False,
@@ -109,7 +115,7 @@ def main():
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="main", choices=sorted(CONFIGS))
-    ap.add_argument("--cpu-rows", type=int, default=1024, help="query rows per head for the CPU baseline")
+    ap.add_argument("--cpu-rows", type=int, default=3072, help="query rows per head for the CPU baseline")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--mode", default="full", choices=("full", "kernel", "copy"),
                     help="full: the benchmark; kernel: prepare once, then only the fused kernel "
@@ -208,7 +214,8 @@ def main():
         "step_tops": round(ops / (wall_ms * 1e-3) / 1e12, 2),
         "frac_of_mfma_peak": round(tops / PEAK_TOPS, 4),
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_TOPS, "unit": "TFLOP/s",
-                     "frac": round(achieved / PEAK_TOPS, 4), "traffic": None,
+                     "frac": round(achieved / PEAK_TOPS, 4),
+                     "traffic": MEASURED_TRAFFIC_BYTES.get(args.config),
                      "kernel": "attn_kernel (fused QK/ExpCast/PV)", "ops_per_launch": ops},
         "roofline_prep": {"bound": "hbm", "achieved": round(prep_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                           "frac": round(prep_gbs / PEAK_HBM_GBS, 4), "algorithmic_bytes": prep_bytes},

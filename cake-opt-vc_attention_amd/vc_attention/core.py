@@ -11,9 +11,11 @@ Backends of this build:
   ``qk_format="int8"`` and the sageattn_vc block geometry (q_block=64,
   k_quant_block=128, kv_block=128, k_smooth=True, qk_hadamard=False,
   mean_dtype="float16", expcast=True, quantize=True).
-* ``"reference"``: accepted by ``Config`` for compatibility; ``attention``
-  raises NotImplementedError for it (the reference's eager FP8-QK prototype is
-  a different numerical contract that this build does not carry).
+* ``"reference"``, ``"npu_fp8"``, ``"cuda_fp8"``: validated by ``Config``
+  exactly as in the reference (core.py:36-65) so existing configurations keep
+  constructing; ``attention`` raises NotImplementedError for them (the eager
+  FP8-QK prototype and the Ascend/Hopper kernels are a different numerical
+  contract that this build does not carry).
 """
 import math
 from dataclasses import dataclass
@@ -37,10 +39,17 @@ class Config:
     backend: str = "reference"
     k_smooth: bool = True
     qk_hadamard: bool = True
+    cuda_schedule: str = "batched"
+    cuda_fused_pipeline: bool = True
+    cuda_fused_specialize: bool = True
+    cuda_fused_interleave: bool = True
     qk_format: str = "fp8_block"
 
     def __post_init__(self):
-        for name in ("expcast", "v_smooth", "quantize", "k_smooth", "qk_hadamard"):
+        if self.cuda_schedule not in ("serial", "batched", "fused"):
+            raise ValueError("cuda_schedule must be serial, batched, or fused")
+        for name in ("expcast", "v_smooth", "quantize", "k_smooth", "qk_hadamard", "cuda_fused_pipeline",
+                     "cuda_fused_specialize", "cuda_fused_interleave"):
             if not isinstance(getattr(self, name), bool):
                 raise ValueError(f"{name} must be a bool")
         for name in ("q_block", "k_quant_block", "kv_block", "clusters", "iterations", "refresh_interval"):
@@ -51,10 +60,21 @@ class Config:
             raise ValueError("active_fraction must be in [0, 1]")
         if self.mean_dtype not in ("float16", "bfloat16", "float32"):
             raise ValueError("Unsupported mean_dtype")
-        if self.backend not in ("reference", "hip"):
-            raise ValueError("backend must be reference or hip")
+        if self.backend not in ("reference", "npu_fp8", "cuda_fp8", "hip"):
+            raise ValueError("backend must be reference, npu_fp8, cuda_fp8, or hip")
         if self.qk_format not in ("fp8_block", "int8"):
             raise ValueError("qk_format must be fp8_block or int8")
+        if self.backend in ("npu_fp8", "cuda_fp8") and not self.quantize:
+            raise ValueError(f"{self.backend} requires quantize=True")
+        if self.backend in ("npu_fp8", "cuda_fp8") and self.k_quant_block % self.kv_block:
+            raise ValueError(f"{self.backend} requires kv_block to divide k_quant_block")
+        if self.backend == "cuda_fp8":
+            if self.cuda_schedule == "fused" and self.kv_block != 128:
+                raise ValueError("fused CUDA requires kv_block=128")
+            if any(x < 32 or x > 256 or x % 32 for x in (self.q_block, self.kv_block)):
+                raise ValueError("cuda_fp8 q_block/kv_block must be multiples of 32 in [32, 256]")
+            if self.k_quant_block > 4096:
+                raise ValueError("cuda_fp8 k_quant_block must be <= 4096")
         if self.backend == "hip":
             required = dict(qk_format="int8", quantize=True, expcast=True, q_block=64, k_quant_block=128,
                             kv_block=128, k_smooth=True, qk_hadamard=False, mean_dtype="float16")
@@ -148,6 +168,9 @@ def attention(q, k, v, config=None, *, cache=None, step=0, total_steps=1, reques
     scale = q.shape[-1] ** -0.5 if scale is None else scale
     if not math.isfinite(scale) or scale <= 0:
         raise ValueError("scale must be positive and finite")
+    if cfg.backend in ("npu_fp8", "cuda_fp8"):
+        raise NotImplementedError(f"backend {cfg.backend!r} targets Ascend/Hopper kernels; on MI355X use "
+                                  "Config(backend='hip', qk_format='int8', ...)")
     if cfg.backend != "hip":
         raise NotImplementedError("the eager FP8-QK reference backend is not part of this build; "
                                   "use Config(backend='hip', qk_format='int8', ...)")

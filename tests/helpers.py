@@ -77,3 +77,31 @@ def output_bound(actual, expected):
     scale = np.abs(e).max(axis=-1, keepdims=True)
     bound = 2.0 ** -7 * np.abs(e) + 2e-3 * scale + 1e-6
     return np.abs(a - e), bound
+
+
+# Scales and dot products for which the last tile's rounding order
+# RN(RN(float(acc)*RN(qs*ks))*sm) and the other tiles' RN(float(acc)*RN(sm*RN(qs*ks)))
+# give different ExpCast bytes for key 1 (sm = RN(128^-0.5)); found by search.
+ORDER_QS = float.fromhex("0x1.b2c8f2p-2")
+ORDER_KS = float.fromhex("0x1.3a883p-1")
+ORDER_ACC = (15989, 15902)
+ORDER_CODE_LAST, ORDER_CODE_OTHER = 96, 97
+
+
+def rounding_order_payload(nk):
+    """Payload state (D=128, one query row of ones) whose keys 0 and 1 have dot products
+    ORDER_ACC; every other key is zero. With nk <= 128 the pair sits in the last tile,
+    with nk > 128 in a tile before the last."""
+    dim, tiles = 128, (nk + 127) // 128
+    q = np.ones((1, 1, 1, dim), np.int8)
+    k = np.zeros((1, 1, nk, dim), np.int8)
+    for key, acc in enumerate(ORDER_ACC):
+        k[0, 0, key, :125] = 127
+        k[0, 0, key, 125] = acc - 125 * 127
+    qs = np.ones((1, 1, 32), np.float32)
+    qs[0, 0, 0] = ORDER_QS
+    ks = np.ones((1, 1, tiles * 4), np.float32)
+    ks[0, 0, 0] = ORDER_KS
+    return {"q": q, "k": k, "v": np.zeros((1, 1, dim, tiles * 128), np.uint8), "qs": qs, "ks": ks,
+            "vs": np.ones((1, 1, dim), np.float32), "means": None, "expcast": True, "block_values": False,
+            "scale": float(np.float32(dim ** -0.5)), "output_type": 1}

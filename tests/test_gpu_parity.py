@@ -309,3 +309,56 @@ def test_full_length_prep_exact_and_sampled_p_bytes():
     err, bound = output_bound(got, eout)
     assert np.all(err <= bound)
     assert cosine(got, eout) >= 0.9999
+
+
+@pytest.mark.parametrize("nk", [2, 129, 300])
+def test_last_tile_rounding_order_known_answer_on_gpu(nk):
+    # The fused kernel's P bytes on the rounding-order payload: byte 96 when the pair of
+    # keys is in the last tile, 97 when it is in an earlier tile (oracle known answer).
+    from helpers import ORDER_CODE_LAST, ORDER_CODE_OTHER, rounding_order_payload
+    _print_case("rounding order", nk)
+    st = rounding_order_payload(nk)
+    to = _to_dev
+    v8 = to(st["v"]).view(torch.float8_e4m3fn)
+    _, pd = vcx.forward(to(st["q"]), to(st["k"]), v8, to(st["qs"]), to(st["ks"]), to(st["vs"]), None,
+                        True, False, 1, st["scale"], p_rows=(0, 1))
+    codes = pd.cpu().numpy()
+    assert codes[0, 0, 0, 0] == 120
+    assert codes[0, 0, 0, 1] == (ORDER_CODE_LAST if nk <= 128 else ORDER_CODE_OTHER)
+    assert np.all(codes[0, 0, 0, 2:] == 0)
+
+
+FULL = [  # name, B, H (of the BASELINE shape's heads), N, D, kind, smooth
+    ("smooth", 1, 2, 37741, 128, "outlier", True),
+    ("d64", 1, 2, 32760, 64, "normal", True),
+    ("long", 1, 2, 75482, 128, "student", True),
+]
+
+
+@pytest.mark.parametrize("case", FULL, ids=lambda c: c[0])
+def test_full_length_baseline_configs(case):
+    # The BASELINE shapes with smoothing at their full sequence length (2 of their heads):
+    # grouping, every payload byte and scale, and the P bytes / output of sampled rows at
+    # the start, the middle and the ragged end of the sequence.
+    from sageattention_local import forward_prepared, prepare
+    name, B, H, N, D, kind, smooth = case
+    _print_case("full-length config", name, (B, H, N, D))
+    q, k, v = make_qkv(B, H, N, N, D, torch.bfloat16, seed=0, kind=kind)
+    qd, kd, vd = (x.to(DEV) for x in (q, k, v))
+    st = prepare(qd, kd, vd, v_smooth=smooth)
+    ost = _oracle_state(q, k, v, smooth, torch.bfloat16)
+    np.testing.assert_array_equal(st["permutation"].cpu().numpy(), ost["permutation"])
+    for key in ("q", "k", "qs", "ks", "vs"):
+        np.testing.assert_array_equal(st[key].cpu().numpy(), ost[key])
+    np.testing.assert_array_equal(storage_to_logical(st["v"], vcx.value_token()), ost["v"])
+    np.testing.assert_array_equal(st["means"].view(torch.int16).cpu().numpy().view(np.uint16), ost["means"])
+    out = forward_prepared(st)
+    for r0, r1 in ((0, 16), (N // 2 - 8, N // 2 + 8), (N - 21, N)):
+        _, pd = vcx.forward(st["q"], st["k"], st["v"], st["qs"], st["ks"], st["vs"], st["means"], True, True, 1,
+                            D ** -0.5, p_rows=(r0, r1))
+        eout, ecodes = o.reference(ost, query_indices=np.arange(r0, r1), return_codes=True)
+        np.testing.assert_array_equal(pd.cpu().numpy(), ecodes)
+        got = out[:, :, r0:r1].float().cpu().numpy()
+        err, bound = output_bound(got, eout)
+        assert np.all(err <= bound), (r0, float((err - bound).max()))
+        assert cosine(got, eout) >= 0.9999

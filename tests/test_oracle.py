@@ -427,3 +427,65 @@ def test_uniform_attention_equals_decoded_value_mean():
     expected = dec.mean(-1) * s["vs"][0, 0]
     np.testing.assert_allclose(o.reference(s)[0, 0], np.broadcast_to(expected, (65, 64)), rtol=1e-6, atol=1e-6)
     del rng
+
+
+def test_expcast_codes_multi_tile_running_max_and_scale_indices():
+    # The P-byte rule of sal/csrc/vc/vc_sm90.cu:288-289,417-418,450,465-482 and
+    # vc_math.cuh:268-384, restated here in vectorised float32 numpy (not the oracle's
+    # loop): the codes of tile t use the running max over tiles 0..t, tiles before the
+    # last round float(acc) * RN(sm * RN(qs*ks)), the last tile rounds (float(acc)*dq)*sm
+    # and masks keys >= Nk; qs index (row//16)*8 + row%8, ks index tile*4 + (key%8)//2.
+    # Later tiles carry larger logits so that using the global max or a wrong scale
+    # index changes many codes. At D=64 sm = 2^-3, so both rounding orders agree here;
+    # the last tile's order is pinned at D=128 by the known answer below.
+    rng = np.random.default_rng(21)
+    nq, nk, dim = 40, 300, 64
+    s = payload(nq, nk, False, dim=dim)
+    s["q"][...] = rng.integers(-9, 10, s["q"].shape)
+    k = rng.integers(-9, 10, s["k"].shape)
+    k[..., 128:256, :] = np.clip(k[..., 128:256, :] * 2, -127, 127)
+    k[..., 256:, :] = np.clip(k[..., 256:, :] * 3, -127, 127)
+    s["k"][...] = k
+    s["qs"][...] = rng.uniform(0.02, 0.05, s["qs"].shape).astype(np.float32)
+    s["ks"][...] = rng.uniform(0.02, 0.05, s["ks"].shape).astype(np.float32)
+    _, codes = o.reference(s, return_codes=True)
+
+    f32 = np.float32
+    sm = f32(dim ** -0.5)
+    acc = s["q"][0, 0].astype(np.int64) @ s["k"][0, 0].T.astype(np.int64)  # exact int
+    rows, keys = np.arange(nq), np.arange(nk)
+    qs = s["qs"][0, 0][(rows // 16) * 8 + rows % 8].astype(f32)[:, None]
+    ks = s["ks"][0, 0][(keys // 128) * 4 + (keys % 8) // 2].astype(f32)[None, :]
+    dq = (qs * ks).astype(f32)
+    accf = acc.astype(f32)
+    m = np.full((nq, 1), f32(-5e6), f32)
+    expected = np.zeros((nq, 384), np.uint8)
+    tiles = (nk + 127) // 128
+    for t in range(tiles):
+        cols = slice(128 * t, min(128 * (t + 1), nk))
+        if t < tiles - 1:
+            logit = (accf[:, cols] * (sm * dq[:, cols]).astype(f32)).astype(f32)
+        else:
+            logit = ((accf[:, cols] * dq[:, cols]).astype(f32) * sm).astype(f32)
+        m = np.maximum(m, logit.max(-1, keepdims=True))
+        u = (logit - m).astype(f32)
+        # fmaf(u, A, B): the fp64 product of two floats is exact; one rounding to fp32
+        # after the fp64 add (ties at fp32 half-ulps of the sum do not occur here).
+        v = (u.astype(np.float64) * np.float64(11.541560173034668) + np.float64(119.6500015258789)).astype(f32)
+        expected[:, cols] = np.clip(np.rint(v), 0, 120).astype(np.uint8)
+    np.testing.assert_array_equal(codes[0, 0], expected)
+    # the running max matters: codes relative to the global max differ in tile 0
+    gmax = (accf * (sm * dq).astype(f32)).astype(f32).max(-1, keepdims=True)
+    assert np.any(expected[:, :128] != np.clip(np.rint(8 * math.log2(math.e) * (
+        (accf[:, :128] * (sm * dq[:, :128]).astype(f32)) - gmax) + 119.65), 0, 120).astype(np.uint8))
+
+
+@pytest.mark.parametrize("nk", [2, 128, 129, 300])
+def test_last_tile_rounding_order_known_answer(nk):
+    # sal/csrc/vc/vc_sm90.cu:417-418 (last tile: (acc*dq)*sm) vs :288-289 (acc*(sm*dq)):
+    # the same two dot products give byte 96 in the last tile and 97 before it.
+    from helpers import ORDER_CODE_LAST, ORDER_CODE_OTHER, rounding_order_payload
+    _, codes = o.reference(rounding_order_payload(nk), return_codes=True)
+    assert codes[0, 0, 0, 0] == 120
+    assert codes[0, 0, 0, 1] == (ORDER_CODE_LAST if nk <= 128 else ORDER_CODE_OTHER)
+    assert np.all(codes[0, 0, 0, 2:] == 0)

@@ -21,8 +21,11 @@
 // Numerical contract (reference sal/csrc/vc/vc_sm90.cu:284-612, vc_math.cuh:268-474):
 //   tiles before the last: logit = RN(float(acc) * RN(sm * RN(qs*ks)))
 //   last tile:             logit = RN(RN(float(acc) * RN(qs*ks)) * sm), keys >= Nk -> -inf
-//   m' = max(m, rowmax), alpha = expf(m - m'), code = sat_u8(RNE(fmaf(RN(logit-m'), A, B)))
+//   m' = max(m, rowmax), code = sat_u8(RNE(fmaf(RN(logit-m'), A, B)))
+//   alpha = exp2((m - m') * log2(e)) (hardware exp2; alpha == 1 exactly when m' == m)
 //   O = alpha*O + PV (+ mass*mean), den = alpha*den + mass, out = O/den * vs.
+// The P bytes follow the contract exactly; alpha, O and den only feed the
+// bf16/fp16 output, whose tolerance covers the exp2 approximation.
 #include "vcx_common.hpp"
 
 namespace vcx {
@@ -162,24 +165,24 @@ struct Wave {
 
     // ---- S^T = K Q^T
     v4i S[2][8];
-    v4i kc[DS], kn[DS];
+    v4i kf[8][DS];
 #pragma unroll
-    for (int ds = 0; ds < DS; ++ds) kc[ds] = *reinterpret_cast<const v4i*>(lk + koff[ds]);
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int ds = 0; ds < DS; ++ds) kf[j][ds] = *reinterpret_cast<const v4i*>(lk + j * 16 * D + koff[ds]);
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      if (j + 1 < 8) {
+      if (j + 2 < 8) {
 #pragma unroll
-        for (int ds = 0; ds < DS; ++ds) kn[ds] = *reinterpret_cast<const v4i*>(lk + (j + 1) * 16 * D + koff[ds]);
+        for (int ds = 0; ds < DS; ++ds) kf[j + 2][ds] = *reinterpret_cast<const v4i*>(lk + (j + 2) * 16 * D + koff[ds]);
       }
 #pragma unroll
       for (int qg = 0; qg < 2; ++qg) {
         v4i acc = {0, 0, 0, 0};
 #pragma unroll
-        for (int ds = 0; ds < DS; ++ds) acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(kc[ds], qf[qg][ds], acc, 0, 0, 0);
+        for (int ds = 0; ds < DS; ++ds) acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(kf[j][ds], qf[qg][ds], acc, 0, 0, 0);
         S[qg][j] = acc;
       }
-#pragma unroll
-      for (int ds = 0; ds < DS; ++ds) kc[ds] = kn[ds];
       __builtin_amdgcn_sched_barrier(0);
     }
 
@@ -211,10 +214,16 @@ struct Wave {
             tmax = fmaxf(tmax, lg[j][r]);
           }
       }
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+      {
+        // Row maximum over the four lane groups: gfx950 permlane swaps give each
+        // lane the values of lanes l^16 and l^32 without an LDS round trip.
+        const auto x16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(tmax), __float_as_uint(tmax), false, false);
+        tmax = fmaxf(__uint_as_float(x16[0]), __uint_as_float(x16[1]));
+        const auto x32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(tmax), __float_as_uint(tmax), false, false);
+        tmax = fmaxf(__uint_as_float(x32[0]), __uint_as_float(x32[1]));
+      }
       const float mn = fmaxf(m[qg], tmax);
-      alpha[qg] = expf(m[qg] - mn);
+      alpha[qg] = __builtin_amdgcn_exp2f((m[qg] - mn) * 1.44269504088896341f);
       m[qg] = mn;
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
@@ -249,31 +258,36 @@ struct Wave {
     }
 
     // ---- O^T += V^T P^T, mass = 1^T P^T
-    v8i vc = load_v(lv, 0), vn;
+    v8i vf[CB];
+    vf[0] = load_v(lv, 0);
+    if (CB > 1) vf[1] = load_v(lv, 1);
 #pragma unroll
     for (int cb = 0; cb < CB; ++cb) {
-      if (cb + 1 < CB) vn = load_v(lv, cb + 1);
+      if (cb + 2 < CB) vf[cb + 2] = load_v(lv, cb + 2);
 #pragma unroll
-      for (int qg = 0; qg < 2; ++qg) O[qg][cb] = mfma_fp8(vc, P[qg], O[qg][cb]);
-      vc = vn;
+      for (int qg = 0; qg < 2; ++qg) O[qg][cb] = mfma_fp8(vf[cb], P[qg], O[qg][cb]);
       __builtin_amdgcn_sched_barrier(0);
     }
     const v8i ones = {0x38383838, 0x38383838, 0x38383838, 0x38383838,
                       0x38383838, 0x38383838, 0x38383838, 0x38383838};
+    float mass[2];
 #pragma unroll
     for (int qg = 0; qg < 2; ++qg) {
       const v4f zero = {0.0f, 0.0f, 0.0f, 0.0f};
       const v4f ms = mfma_fp8(ones, P[qg], zero);
+      mass[qg] = ms[0];
       den[qg] = den[qg] * alpha[qg] + ms[0];
-      if constexpr (SMOOTH) {
+    }
+    if constexpr (SMOOTH) {
 #pragma unroll
-        for (int cb = 0; cb < CB; ++cb) {
-          const uint2 hm = *reinterpret_cast<const uint2*>(lm + 32 * cb + 8 * G);
-          const float mean[4] = {f16_bits_to_f32(hm.x & 0xffffu), f16_bits_to_f32(hm.x >> 16),
-                                 f16_bits_to_f32(hm.y & 0xffffu), f16_bits_to_f32(hm.y >> 16)};
+      for (int cb = 0; cb < CB; ++cb) {
+        const uint2 hm = *reinterpret_cast<const uint2*>(lm + 32 * cb + 8 * G);
+        const float mean[4] = {f16_bits_to_f32(hm.x & 0xffffu), f16_bits_to_f32(hm.x >> 16),
+                               f16_bits_to_f32(hm.y & 0xffffu), f16_bits_to_f32(hm.y >> 16)};
 #pragma unroll
-          for (int r = 0; r < 4; ++r) O[qg][cb][r] = __builtin_fmaf(ms[0], mean[r], O[qg][cb][r]);
-        }
+        for (int qg = 0; qg < 2; ++qg)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) O[qg][cb][r] = __builtin_fmaf(mass[qg], mean[r], O[qg][cb][r]);
       }
     }
   }
@@ -429,6 +443,7 @@ extern "C" int vcx_attention_fwd(const int8_t* q8, const int8_t* k8, const uint8
   VCX_REQUIRE(D == 64 || D == 128, "D must be 64 or 128");
   VCX_REQUIRE(B * H <= 65535, "B*H exceeds 65535");
   VCX_REQUIRE(Nq < (int64_t(1) << 30) && Nk < (int64_t(1) << 30), "sequence too long");
+  VCX_REQUIRE(cdiv(Nk, kTile) * kTile * D < (int64_t(1) << 31), "K/V payload of one head must be below 2 GiB");
   if (expcast != 1) return fail(VCX_EUNSUPPORTED, "only the ExpCast probability encoding is implemented");
   if (block_values && !channel_scale)
     return fail(VCX_EUNSUPPORTED, "per-block V scales are not implemented in the fused kernel");

@@ -43,6 +43,30 @@ __device__ inline int64_t source_token(const int64_t* perm, int64_t bh, int64_t 
   return perm ? perm[bh * n + key] : key;
 }
 
+// Rows of the NR keys key0 + 16*i (i < NR) of one head, for channel chunk c.
+// All permutation lookups are issued first, then all row loads, so that their
+// latencies overlap; a key past n loads row 0 and reads as zero.
+template <int DT, int D, int NR>
+__device__ inline void load_key_rows(const uint16_t* base, int64_t sn, const int64_t* perm, int64_t bh, int64_t n,
+                                     int64_t key0, int c, float (&v)[NR][D / 16]) {
+  constexpr int CPT = D / 16;
+  int64_t src[NR];
+#pragma unroll
+  for (int i = 0; i < NR; ++i) {
+    const int64_t key = key0 + 16 * i;
+    src[i] = key < n ? source_token(perm, bh, n, key) : 0;
+  }
+  Row<D> r[NR];
+#pragma unroll
+  for (int i = 0; i < NR; ++i) load_row<D>(base, sn, src[i], c, r[i]);
+#pragma unroll
+  for (int i = 0; i < NR; ++i) {
+    const bool valid = key0 + 16 * i < n;
+#pragma unroll
+    for (int j = 0; j < CPT; ++j) v[i][j] = valid ? row_val<DT, D>(r[i], j) : 0.0f;
+  }
+}
+
 // Per-head base pointer of a strided [B,H,N,D] tensor.
 __device__ inline const uint16_t* head_base(const void* x, int64_t bh, int64_t H, int64_t sb, int64_t sh) {
   int64_t b = bh / H, h = bh % H;
@@ -88,19 +112,7 @@ __global__ __launch_bounds__(kThreads) void tile_stats_kernel(
   const int tid = threadIdx.x, kk = tid >> 4, c = tid & 15, lane = tid & 63, w = tid >> 6;
   const uint16_t* base = head_base(x, bh, H, sb, sh);
   float v[8][CPT];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    int64_t key = tile * kTile + kk + 16 * i;
-    if (key < n) {
-      Row<D> r;
-      load_row<D>(base, sn, source_token(perm, bh, n, key), c, r);
-#pragma unroll
-      for (int j = 0; j < CPT; ++j) v[i][j] = row_val<DT, D>(r, j);
-    } else {
-#pragma unroll
-      for (int j = 0; j < CPT; ++j) v[i][j] = 0.0f;
-    }
-  }
+  load_key_rows<DT, D, 8>(base, sn, perm, bh, n, tile * kTile + kk, c, v);
   const int64_t meta = (bh * tiles + tile) * D;
   if constexpr (MODE == kVAmax) {
     float m[CPT];
@@ -169,8 +181,20 @@ __global__ void k_mean_kernel(const double* sums, int64_t tiles, int64_t n, int 
                               uint16_t* km_out) {
   const int64_t bh = blockIdx.x;
   const int ch = threadIdx.x;
+  const double* col = sums + bh * tiles * D + ch;
+  // Sequential fp64 sum over tiles (the contract's order); the loads of a batch
+  // of tiles are issued together so that their latencies overlap.
+  constexpr int kBatch = 16;
   double s = 0.0;
-  for (int64_t t = 0; t < tiles; ++t) s = __dadd_rn(s, sums[(bh * tiles + t) * D + ch]);
+  int64_t t = 0;
+  for (; t + kBatch <= tiles; t += kBatch) {
+    double v[kBatch];
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i) v[i] = col[(t + i) * D];
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i) s = __dadd_rn(s, v[i]);
+  }
+  for (; t < tiles; ++t) s = __dadd_rn(s, col[t * D]);
   float mean = static_cast<float>(__ddiv_rn(s, static_cast<double>(n)));
   uint32_t bits = f32_to_in<DT>(mean);
   km_f32[bh * D + ch] = in_to_f32<DT>(bits);
@@ -183,16 +207,42 @@ __global__ void v_scale_kernel(const float* a0, const float* a1, int64_t tiles, 
                                float* vs, float* recip) {
   const int64_t bh = blockIdx.x;
   const int ch = threadIdx.x;
+  const float* c0 = a0 + bh * tiles * D + ch;
+  const float* c1 = smooth ? a1 + bh * tiles * D + ch : nullptr;
+  // Maxima are order-free; loads of a batch of tiles are issued together.
+  constexpr int kBatch = 16;
   if (!smooth) {
     float amax = 0.0f;
-    for (int64_t t = 0; t < tiles; ++t) amax = fmaxf(amax, a0[(bh * tiles + t) * D + ch]);
+    int64_t t = 0;
+    for (; t + kBatch <= tiles; t += kBatch) {
+      float v[kBatch];
+#pragma unroll
+      for (int i = 0; i < kBatch; ++i) v[i] = c0[(t + i) * D];
+#pragma unroll
+      for (int i = 0; i < kBatch; ++i) amax = fmaxf(amax, v[i]);
+    }
+    for (; t < tiles; ++t) amax = fmaxf(amax, c0[t * D]);
     vs[bh * D + ch] = amax > 0.0f ? __fdiv_rn(amax, 448.0f) : 0.0f;
     recip[bh * D + ch] = amax > 0.0f ? __fdiv_rn(448.0f, amax) : 0.0f;
   } else {
     float P = 0.0f, M = 0.0f;
-    for (int64_t t = 0; t < tiles; ++t) {
-      P = fmaxf(P, a1[(bh * tiles + t) * D + ch]);
-      M = fmaxf(M, fabsf(a0[(bh * tiles + t) * D + ch]));
+    int64_t t = 0;
+    for (; t + kBatch <= tiles; t += kBatch) {
+      float v0[kBatch], v1[kBatch];
+#pragma unroll
+      for (int i = 0; i < kBatch; ++i) {
+        v0[i] = c0[(t + i) * D];
+        v1[i] = c1[(t + i) * D];
+      }
+#pragma unroll
+      for (int i = 0; i < kBatch; ++i) {
+        P = fmaxf(P, v1[i]);
+        M = fmaxf(M, fabsf(v0[i]));
+      }
+    }
+    for (; t < tiles; ++t) {
+      P = fmaxf(P, c1[t * D]);
+      M = fmaxf(M, fabsf(c0[t * D]));
     }
     float s = P > 0.0f ? __fdiv_rn(P, 448.0f) : 1.0f;
     vs[bh * D + ch] = fmaxf(s, __fdiv_rn(M, 65504.0f));
@@ -212,21 +262,22 @@ __global__ __launch_bounds__(kThreads) void quant_q_kernel(const void* q, int64_
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, c = lane & 15, sel = (lane >> 4) & 1;
   const uint16_t* base = head_base(q, bh, H, sb, sh);
   const int64_t qs_len = (n + 63) / 64 * 32;
+  // The four rows of the thread are loaded together before any is used.
+  Row<D> rows[4];
+#pragma unroll
+  for (int pass = 0; pass < 4; ++pass) {
+    const int grp = pass * 8 + w * 2 + (lane >> 5);
+    const int64_t row = blk * 64 + 16 * (grp >> 3) + (grp & 7) + 8 * sel;
+    load_row<D>(base, sn, row < n ? row : 0, c, rows[pass]);
+  }
 #pragma unroll
   for (int pass = 0; pass < 4; ++pass) {
     const int grp = pass * 8 + w * 2 + (lane >> 5);  // 0..31 inside the 64-row block
     const int g = grp >> 3, t = grp & 7;
     const int64_t row = blk * 64 + 16 * g + t + 8 * sel;
     float x[CPT];
-    if (row < n) {
-      Row<D> r;
-      load_row<D>(base, sn, row, c, r);
 #pragma unroll
-      for (int j = 0; j < CPT; ++j) x[j] = row_val<DT, D>(r, j);
-    } else {
-#pragma unroll
-      for (int j = 0; j < CPT; ++j) x[j] = 0.0f;
-    }
+    for (int j = 0; j < CPT; ++j) x[j] = row < n ? row_val<DT, D>(rows[pass], j) : 0.0f;
     float amax = 0.0f;
 #pragma unroll
     for (int j = 0; j < CPT; ++j) amax = fmaxf(amax, fabsf(x[j]));
@@ -268,21 +319,15 @@ __global__ __launch_bounds__(kThreads) void quant_k_kernel(const void* k, int64_
 #pragma unroll
   for (int j = 0; j < CPT; ++j) mean[j] = km[bh * D + c * CPT + j];
   float v[8][CPT];
+  load_key_rows<DT, D, 8>(base, sn, perm, bh, n, tile * kTile + kk, c, v);
   float amax = 0.0f;
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    int64_t key = tile * kTile + kk + 16 * i;
-    if (key < n) {
-      Row<D> r;
-      load_row<D>(base, sn, source_token(perm, bh, n, key), c, r);
+    const bool valid = tile * kTile + kk + 16 * i < n;
 #pragma unroll
-      for (int j = 0; j < CPT; ++j) {
-        v[i][j] = round_in<DT>(__fsub_rn(row_val<DT, D>(r, j), mean[j]));
-        amax = fmaxf(amax, fabsf(v[i][j]));
-      }
-    } else {
-#pragma unroll
-      for (int j = 0; j < CPT; ++j) v[i][j] = 0.0f;
+    for (int j = 0; j < CPT; ++j) {
+      v[i][j] = valid ? round_in<DT>(__fsub_rn(v[i][j], mean[j])) : 0.0f;
+      amax = fmaxf(amax, fabsf(v[i][j]));
     }
   }
 #pragma unroll
@@ -329,6 +374,9 @@ __global__ __launch_bounds__(kThreads) void quant_v_kernel(
   const int64_t tile = blockIdx.x, bh = blockIdx.y, tiles = gridDim.x;
   const int tid = threadIdx.x, kk = tid >> 4, c = tid & 15;
   const uint16_t* base = head_base(vin, bh, H, sb, sh);
+  // Row loads first, so that they overlap the scale/mean stage below.
+  float xv[8][CPT];
+  load_key_rows<DT, D, 8>(base, sn, perm, bh, n, tile * kTile + kk, c, xv);
   if (tid < D) {
     const int64_t meta = (bh * tiles + tile) * D + tid;
     if constexpr (SMOOTH) {
@@ -355,12 +403,10 @@ __global__ __launch_bounds__(kThreads) void quant_v_kernel(
     const int64_t key = tile * kTile + kt;
     const int pos = value_position(kt);
     if (key < n) {
-      Row<D> r;
-      load_row<D>(base, sn, source_token(perm, bh, n, key), c, r);
 #pragma unroll
       for (int j = 0; j < CPT; ++j) {
         const int ch = c * CPT + j;
-        float x = row_val<DT, D>(r, j);
+        float x = xv[i][j];
         uint32_t byte;
         if constexpr (SMOOTH) {
           byte = e4m3_sat(__fdiv_rn(__fsub_rn(x, mu_sh[ch]), sc_sh[ch]));

@@ -360,6 +360,10 @@ __global__ __launch_bounds__(kThreads) void quant_k_kernel(const void* k, int64_
 
 // grid (tiles, B*H), 256 threads. Bytes are staged in LDS as [D][128] storage
 // positions, then written as 16-byte rows of the [D][tiles*128] payload.
+// Thread (m, cg) owns storage dword m (positions 4m..4m+3, i.e. the four tokens
+// 16(m%8) + 2(m/8) + {0, 1, 8, 9}) for the D/8 channels of group cg, so it
+// packs four bytes per channel into one LDS dword; 16-byte chunks of a staged
+// row are XOR-swizzled by the channel group to spread the stores over banks.
 //  SMOOTH = 0: byte = e4m3(RN(x * recip[ch])), zero channel -> 0.
 //  SMOOTH = 1: byte = e4m3(RN(RN(x - mean_t) / s)), with s the channel scale
 //              (CHANNEL) or the tile's block scale, written with the fp16 means.
@@ -368,15 +372,44 @@ __global__ __launch_bounds__(kThreads) void quant_v_kernel(
     const void* vin, int64_t H, int64_t n, int64_t sb, int64_t sh, int64_t sn, const int64_t* perm,
     const float* scale_or_recip, const float* tile_mean, const float* tile_peak, uint8_t* v8,
     float* vs_block, uint16_t* means) {
-  constexpr int CPT = D / 16;
-  __shared__ uint8_t stage[D * kTile];
+  constexpr int CPG = D / 8;  // channels per thread
+  __shared__ __attribute__((aligned(16))) uint8_t stage[D * kTile];
   __shared__ float sc_sh[D], mu_sh[D];
   const int64_t tile = blockIdx.x, bh = blockIdx.y, tiles = gridDim.x;
-  const int tid = threadIdx.x, kk = tid >> 4, c = tid & 15;
+  const int tid = threadIdx.x, m = tid >> 3, cg = tid & 7;
   const uint16_t* base = head_base(vin, bh, H, sb, sh);
   // Row loads first, so that they overlap the scale/mean stage below.
-  float xv[8][CPT];
-  load_key_rows<DT, D, 8>(base, sn, perm, bh, n, tile * kTile + kk, c, xv);
+  uint32_t w[4][CPG / 2];
+  bool valid[4];
+  {
+    int64_t src[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int64_t key = tile * kTile + 16 * (m & 7) + 2 * (m >> 3) + (q & 1) + 8 * (q >> 1);
+      valid[q] = key < n;
+      src[q] = valid[q] ? source_token(perm, bh, n, key) : 0;
+    }
+    // Two vector loads per row: 16 bytes each for D = 128, 8 bytes for D = 64
+    // (the alignment the input checks guarantee).
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const uint16_t* p = base + src[q] * sn + cg * CPG;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        if constexpr (D == 128) {
+          const uint4 v = *reinterpret_cast<const uint4*>(p + 8 * h);
+          w[q][4 * h] = v.x;
+          w[q][4 * h + 1] = v.y;
+          w[q][4 * h + 2] = v.z;
+          w[q][4 * h + 3] = v.w;
+        } else {
+          const uint2 v = *reinterpret_cast<const uint2*>(p + 4 * h);
+          w[q][2 * h] = v.x;
+          w[q][2 * h + 1] = v.y;
+        }
+      }
+    }
+  }
   if (tid < D) {
     const int64_t meta = (bh * tiles + tile) * D + tid;
     if constexpr (SMOOTH) {
@@ -397,35 +430,33 @@ __global__ __launch_bounds__(kThreads) void quant_v_kernel(
     }
   }
   __syncthreads();
+  const int chunk = ((m >> 2) ^ cg) * 16 + 4 * (m & 3);
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int kt = kk + 16 * i;
-    const int64_t key = tile * kTile + kt;
-    const int pos = value_position(kt);
-    if (key < n) {
+  for (int j = 0; j < CPG; ++j) {
+    const int ch = cg * CPG + j;
+    float y[4];
 #pragma unroll
-      for (int j = 0; j < CPT; ++j) {
-        const int ch = c * CPT + j;
-        float x = xv[i][j];
-        uint32_t byte;
-        if constexpr (SMOOTH) {
-          byte = e4m3_sat(__fdiv_rn(__fsub_rn(x, mu_sh[ch]), sc_sh[ch]));
-        } else {
-          float rc = sc_sh[ch];
-          byte = rc == 0.0f ? 0u : e4m3_sat(__fmul_rn(x, rc));
-        }
-        stage[ch * kTile + pos] = static_cast<uint8_t>(byte);
+    for (int q = 0; q < 4; ++q) {
+      const float x = in_to_f32<DT>((w[q][j >> 1] >> (16 * (j & 1))) & 0xffffu);
+      float t;
+      if constexpr (SMOOTH) {
+        t = __fdiv_rn(__fsub_rn(x, mu_sh[ch]), sc_sh[ch]);
+      } else {
+        const float rc = sc_sh[ch];
+        t = rc == 0.0f ? 0.0f : __fmul_rn(x, rc);  // a zero channel gives +0 bytes
       }
-    } else {
-#pragma unroll
-      for (int j = 0; j < CPT; ++j) stage[(c * CPT + j) * kTile + pos] = 0;
+      // padding tokens are +0; E4M3 saturates at +-448
+      y[q] = valid[q] ? fminf(448.0f, fmaxf(-448.0f, t)) : 0.0f;
     }
+    uint32_t packed = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(y[0], y[1], 0, false));
+    packed = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(y[2], y[3], static_cast<int>(packed), true));
+    *reinterpret_cast<uint32_t*>(&stage[ch * kTile + chunk]) = packed;
   }
   __syncthreads();
   const int64_t npad = tiles * kTile;
   for (int s = tid; s < D * 8; s += kThreads) {
     const int ch = s >> 3, part = s & 7;
-    uint4 val = *reinterpret_cast<const uint4*>(&stage[ch * kTile + part * 16]);
+    uint4 val = *reinterpret_cast<const uint4*>(&stage[ch * kTile + ((part ^ (ch / CPG)) * 16)]);
     *reinterpret_cast<uint4*>(v8 + (bh * D + ch) * npad + tile * kTile + part * 16) = val;
   }
 }

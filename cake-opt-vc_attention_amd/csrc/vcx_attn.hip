@@ -79,17 +79,25 @@ __device__ inline __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t by
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(bytes), 0x00020000);
 }
 
-template <int D, bool SMOOTH>
+// Value modes: VM 0 = no smoothing (per-channel V scale in the epilogue),
+// 1 = block-mean smoothing with per-channel scales, 2 = block-mean smoothing
+// with per-block scales (applied to every tile's contribution).
+template <int D, int VM>
 struct TileLoader {
+  static constexpr bool SMOOTH = VM >= 1, BSCALE = VM == 2;
   // Meta region of a buffer: SMOOTH ? fp16 means of the tile (2*D bytes) : nothing,
-  // followed by the tile's 4 K scales (16 bytes). Loaded by lanes 0..ML of wave 0.
+  // then BSCALE ? the tile's fp32 V scales (4*D bytes) : nothing, then the tile's
+  // 4 K scales (16 bytes). Means and K scales are loaded by wave 0, V scales by wave 1.
   static constexpr int ML = SMOOTH ? (2 * D) / 16 : 0;
-  static constexpr int KS_OFF = 16 * ML;
+  static constexpr int VL = BSCALE ? (4 * D) / 16 : 0;
+  static constexpr int VS_OFF = 16 * ML;
+  static constexpr int KS_OFF = 16 * (ML + VL);
+  static constexpr int META_BYTES = KS_OFF + 16;
   static constexpr int N = D / 32;  // instructions per wave per operand
   uint32_t koff[N];                 // lane byte offset inside the K tile (row*D + chunk*16)
   uint32_t voff[N];                 // lane byte offset inside the V^T tile columns
   uint32_t moff;                    // lane byte offset of the meta load (wave 0)
-  __amdgpu_buffer_rsrc_t rk, rv, rm, rs;
+  __amdgpu_buffer_rsrc_t rk, rv, rm, rs, rb;
   int wave;
 
   __device__ inline void init(const AttnArgs& a, int64_t bh) {
@@ -109,6 +117,7 @@ struct TileLoader {
     rv = make_rsrc(a.v8 + bh * D * npad, static_cast<uint32_t>(D * npad));
     rs = make_rsrc(a.ks + bh * a.tiles * 4, static_cast<uint32_t>(a.tiles * 16));
     if constexpr (SMOOTH) rm = make_rsrc(a.means + bh * a.tiles * D, static_cast<uint32_t>(a.tiles * D * 2));
+    if constexpr (BSCALE) rb = make_rsrc(a.vs + bh * a.tiles * D, static_cast<uint32_t>(a.tiles * D * 4));
     moff = static_cast<uint32_t>(lane * 16);
   }
 
@@ -123,6 +132,10 @@ struct TileLoader {
       }
       if (lane == 0)
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)(lm + KS_OFF), 16, 0, static_cast<int>(t * 16), 0, 0);
+    }
+    if constexpr (BSCALE) {
+      if (wave == 1 && lane < VL)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_void*)(lm + VS_OFF), 16, moff, static_cast<int>(t * D * 4), 0, 0);
     }
     const int kso = static_cast<int>(t * kTile * D);
 #pragma unroll
@@ -139,10 +152,12 @@ __device__ inline v4f mfma_fp8(const v8i& a, const v8i& b, const v4f& c) {
   return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
 }
 
-template <int D, bool SMOOTH, bool DUMP>
+template <int D, int VM, bool DUMP>
 struct Wave {
   static constexpr int DS = D / 64;  // 64-deep QK steps
   static constexpr int CB = D / 16;  // 16-channel output blocks
+  static constexpr bool SMOOTH = VM >= 1, BSCALE = VM == 2;
+  typedef TileLoader<D, VM> LD;
 
   v4i qf[2][DS];
   float qsv[2];
@@ -161,7 +176,7 @@ struct Wave {
 
   template <bool LAST>
   __device__ inline void tile(const AttnArgs& a, int64_t t, const uint8_t* lk, const uint8_t* lv, const uint8_t* lm) {
-    const float ksv = *reinterpret_cast<const float*>(lm + TileLoader<D, SMOOTH>::KS_OFF + 4 * G);
+    const float ksv = *reinterpret_cast<const float*>(lm + LD::KS_OFF + 4 * G);
 
     // ---- S^T = K Q^T
     v4i S[2][8];
@@ -258,6 +273,41 @@ struct Wave {
     }
 
     // ---- O^T += V^T P^T, mass = 1^T P^T
+    const v8i ones = {0x38383838, 0x38383838, 0x38383838, 0x38383838,
+                      0x38383838, 0x38383838, 0x38383838, 0x38383838};
+    const v4f zero = {0.0f, 0.0f, 0.0f, 0.0f};
+    float mass[2];
+    if constexpr (BSCALE) {
+      // Per-block V scales: O += (PV_t + mass * mean_t) * vs_t per channel. The row
+      // mass comes first; each channel block's PV lands in a temporary that is
+      // folded into O right away.
+#pragma unroll
+      for (int qg = 0; qg < 2; ++qg) {
+        const v4f ms = mfma_fp8(ones, P[qg], zero);
+        mass[qg] = ms[0];
+        den[qg] = den[qg] * alpha[qg] + ms[0];
+      }
+      v8i vc = load_v(lv, 0), vn;
+#pragma unroll
+      for (int cb = 0; cb < CB; ++cb) {
+        if (cb + 1 < CB) vn = load_v(lv, cb + 1);
+        const uint2 hm = *reinterpret_cast<const uint2*>(lm + 32 * cb + 8 * G);
+        const float4 vsb = *reinterpret_cast<const float4*>(lm + LD::VS_OFF + 4 * (16 * cb + 4 * G));
+        const float mean[4] = {f16_bits_to_f32(hm.x & 0xffffu), f16_bits_to_f32(hm.x >> 16),
+                               f16_bits_to_f32(hm.y & 0xffffu), f16_bits_to_f32(hm.y >> 16)};
+        const float sc[4] = {vsb.x, vsb.y, vsb.z, vsb.w};
+#pragma unroll
+        for (int qg = 0; qg < 2; ++qg) {
+          const v4f pv = mfma_fp8(vc, P[qg], zero);
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            O[qg][cb][r] = __builtin_fmaf(__builtin_fmaf(mass[qg], mean[r], pv[r]), sc[r], O[qg][cb][r]);
+        }
+        vc = vn;
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      return;
+    }
     v8i vf[CB];
     vf[0] = load_v(lv, 0);
     if (CB > 1) vf[1] = load_v(lv, 1);
@@ -268,12 +318,8 @@ struct Wave {
       for (int qg = 0; qg < 2; ++qg) O[qg][cb] = mfma_fp8(vf[cb], P[qg], O[qg][cb]);
       __builtin_amdgcn_sched_barrier(0);
     }
-    const v8i ones = {0x38383838, 0x38383838, 0x38383838, 0x38383838,
-                      0x38383838, 0x38383838, 0x38383838, 0x38383838};
-    float mass[2];
 #pragma unroll
     for (int qg = 0; qg < 2; ++qg) {
-      const v4f zero = {0.0f, 0.0f, 0.0f, 0.0f};
       const v4f ms = mfma_fp8(ones, P[qg], zero);
       mass[qg] = ms[0];
       den[qg] = den[qg] * alpha[qg] + ms[0];
@@ -293,13 +339,14 @@ struct Wave {
   }
 };
 
-template <int D, bool SMOOTH, bool DUMP, int OUT>
+template <int D, int VM, bool DUMP, int OUT>
 __global__ __launch_bounds__(kThreadsPerBlock, 2) void attn_kernel(AttnArgs a) {
+  typedef TileLoader<D, VM> LD;
   constexpr int KB = kTile * D, VB = D * kTile;
   __shared__ __attribute__((aligned(16))) uint8_t lds0[KB + VB];
   __shared__ __attribute__((aligned(16))) uint8_t lds1[KB + VB];
-  __shared__ __attribute__((aligned(16))) uint8_t meta0[512];
-  __shared__ __attribute__((aligned(16))) uint8_t meta1[512];
+  __shared__ __attribute__((aligned(16))) uint8_t meta0[LD::META_BYTES];
+  __shared__ __attribute__((aligned(16))) uint8_t meta1[LD::META_BYTES];
 
   // XCD-aware order: the hardware deals blocks round-robin over 8 XCDs; give
   // each XCD a contiguous range of (head, query block) so its L2 serves one head.
@@ -309,14 +356,14 @@ __global__ __launch_bounds__(kThreadsPerBlock, 2) void attn_kernel(AttnArgs a) {
   const int64_t bh = logical / a.qblocks, qb = logical % a.qblocks;
 
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  Wave<D, SMOOTH, DUMP> w;
+  Wave<D, VM, DUMP> w;
   w.G = lane >> 4;
   w.li = lane & 15;
   w.bh_ = bh;
   // Lane-constant LDS offsets.
   const int kr = 8 * ((w.li & 3) >> 1) + 2 * (w.li >> 2) + (w.li & 1);
 #pragma unroll
-  for (int ds = 0; ds < Wave<D, SMOOTH, DUMP>::DS; ++ds)
+  for (int ds = 0; ds < Wave<D, VM, DUMP>::DS; ++ds)
     w.koff[ds] = kr * D + ((((D == 128) ? 4 * ds : 0) + w.G) ^ swz_k<D>(kr)) * 16;
 #pragma unroll
   for (int h = 0; h < 2; ++h) w.voff[h] = w.li * kTile + (((2 * w.G + h) ^ swz_v(w.li)) * 16);
@@ -329,17 +376,17 @@ __global__ __launch_bounds__(kThreadsPerBlock, 2) void attn_kernel(AttnArgs a) {
     const int64_t si = (r / 16) * 8 + r % 8;
     w.qsv[qg] = si < a.qs_len ? a.qs[bh * a.qs_len + si] : 1.0f;
 #pragma unroll
-    for (int ds = 0; ds < Wave<D, SMOOTH, DUMP>::DS; ++ds) {
+    for (int ds = 0; ds < Wave<D, VM, DUMP>::DS; ++ds) {
       if (r < a.Nq) w.qf[qg][ds] = *reinterpret_cast<const v4i*>(a.q8 + (bh * a.Nq + r) * D + ds * 64 + w.G * 16);
       else w.qf[qg][ds] = v4i{0, 0, 0, 0};
     }
     w.m[qg] = -5000000.0f;
     w.den[qg] = 0.0f;
 #pragma unroll
-    for (int cb = 0; cb < Wave<D, SMOOTH, DUMP>::CB; ++cb) w.O[qg][cb] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int cb = 0; cb < Wave<D, VM, DUMP>::CB; ++cb) w.O[qg][cb] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
   }
 
-  TileLoader<D, SMOOTH> ld;
+  LD ld;
   ld.init(a, bh);
   ld.issue(0, lds0, lds0 + KB, meta0);
   // Tiles before the last, two per iteration so each buffer is a fixed LDS object.
@@ -375,9 +422,11 @@ __global__ __launch_bounds__(kThreadsPerBlock, 2) void attn_kernel(AttnArgs a) {
     const float inv = 1.0f / w.den[qg];
     uint16_t* out = static_cast<uint16_t*>(a.out) + b * a.osb + h * a.osh + w.row[qg] * a.osn;
 #pragma unroll
-    for (int cb = 0; cb < Wave<D, SMOOTH, DUMP>::CB; ++cb) {
+    for (int cb = 0; cb < Wave<D, VM, DUMP>::CB; ++cb) {
       const int ch = 16 * cb + 4 * w.G;
-      const float4 sc = *reinterpret_cast<const float4*>(a.vs + bh * D + ch);
+      // per-channel V scale (per-block scales were applied tile by tile)
+      const float4 sc = Wave<D, VM, DUMP>::BSCALE ? make_float4(1.0f, 1.0f, 1.0f, 1.0f)
+                                                  : *reinterpret_cast<const float4*>(a.vs + bh * D + ch);
       const float y0 = w.O[qg][cb][0] * inv * sc.x, y1 = w.O[qg][cb][1] * inv * sc.y;
       const float y2 = w.O[qg][cb][2] * inv * sc.z, y3 = w.O[qg][cb][3] * inv * sc.w;
       uint2 packed;
@@ -395,37 +444,45 @@ __global__ __launch_bounds__(kThreadsPerBlock, 2) void attn_kernel(AttnArgs a) {
 
 // Explicit instantiation of every launch variant: hipcc's host pass otherwise
 // emitted the kernel handle of only the first variant named in each ternary.
-template __global__ void attn_kernel<64, false, false, 0>(AttnArgs);
-template __global__ void attn_kernel<64, false, false, 1>(AttnArgs);
-template __global__ void attn_kernel<64, false, true, 0>(AttnArgs);
-template __global__ void attn_kernel<64, false, true, 1>(AttnArgs);
-template __global__ void attn_kernel<64, true, false, 0>(AttnArgs);
-template __global__ void attn_kernel<64, true, false, 1>(AttnArgs);
-template __global__ void attn_kernel<64, true, true, 0>(AttnArgs);
-template __global__ void attn_kernel<64, true, true, 1>(AttnArgs);
-template __global__ void attn_kernel<128, false, false, 0>(AttnArgs);
-template __global__ void attn_kernel<128, false, false, 1>(AttnArgs);
-template __global__ void attn_kernel<128, false, true, 0>(AttnArgs);
-template __global__ void attn_kernel<128, false, true, 1>(AttnArgs);
-template __global__ void attn_kernel<128, true, false, 0>(AttnArgs);
-template __global__ void attn_kernel<128, true, false, 1>(AttnArgs);
-template __global__ void attn_kernel<128, true, true, 0>(AttnArgs);
-template __global__ void attn_kernel<128, true, true, 1>(AttnArgs);
+template __global__ void attn_kernel<64, 0, false, 0>(AttnArgs);
+template __global__ void attn_kernel<64, 0, false, 1>(AttnArgs);
+template __global__ void attn_kernel<64, 0, true, 0>(AttnArgs);
+template __global__ void attn_kernel<64, 0, true, 1>(AttnArgs);
+template __global__ void attn_kernel<64, 1, false, 0>(AttnArgs);
+template __global__ void attn_kernel<64, 1, false, 1>(AttnArgs);
+template __global__ void attn_kernel<64, 1, true, 0>(AttnArgs);
+template __global__ void attn_kernel<64, 1, true, 1>(AttnArgs);
+template __global__ void attn_kernel<64, 2, false, 0>(AttnArgs);
+template __global__ void attn_kernel<64, 2, false, 1>(AttnArgs);
+template __global__ void attn_kernel<64, 2, true, 0>(AttnArgs);
+template __global__ void attn_kernel<64, 2, true, 1>(AttnArgs);
+template __global__ void attn_kernel<128, 0, false, 0>(AttnArgs);
+template __global__ void attn_kernel<128, 0, false, 1>(AttnArgs);
+template __global__ void attn_kernel<128, 0, true, 0>(AttnArgs);
+template __global__ void attn_kernel<128, 0, true, 1>(AttnArgs);
+template __global__ void attn_kernel<128, 1, false, 0>(AttnArgs);
+template __global__ void attn_kernel<128, 1, false, 1>(AttnArgs);
+template __global__ void attn_kernel<128, 1, true, 0>(AttnArgs);
+template __global__ void attn_kernel<128, 1, true, 1>(AttnArgs);
+template __global__ void attn_kernel<128, 2, false, 0>(AttnArgs);
+template __global__ void attn_kernel<128, 2, false, 1>(AttnArgs);
+template __global__ void attn_kernel<128, 2, true, 0>(AttnArgs);
+template __global__ void attn_kernel<128, 2, true, 1>(AttnArgs);
 
-template <int D, bool SMOOTH, bool DUMP, int OUT>
+template <int D, int VM, bool DUMP, int OUT>
 int launch(const AttnArgs& a, int64_t nblocks, hipStream_t st) {
-  attn_kernel<D, SMOOTH, DUMP, OUT><<<dim3(static_cast<unsigned>(nblocks)), kThreadsPerBlock, 0, st>>>(a);
+  attn_kernel<D, VM, DUMP, OUT><<<dim3(static_cast<unsigned>(nblocks)), kThreadsPerBlock, 0, st>>>(a);
   return check_launch("attn_kernel");
 }
 
-template <int D, bool SMOOTH>
+template <int D, int VM>
 int launch_out(const AttnArgs& a, int64_t nblocks, bool dump, int out_dtype, hipStream_t st) {
   if (dump) {
-    return out_dtype == VCX_BFLOAT16 ? launch<D, SMOOTH, true, VCX_BFLOAT16>(a, nblocks, st)
-                                     : launch<D, SMOOTH, true, VCX_FLOAT16>(a, nblocks, st);
+    return out_dtype == VCX_BFLOAT16 ? launch<D, VM, true, VCX_BFLOAT16>(a, nblocks, st)
+                                     : launch<D, VM, true, VCX_FLOAT16>(a, nblocks, st);
   }
-  return out_dtype == VCX_BFLOAT16 ? launch<D, SMOOTH, false, VCX_BFLOAT16>(a, nblocks, st)
-                                   : launch<D, SMOOTH, false, VCX_FLOAT16>(a, nblocks, st);
+  return out_dtype == VCX_BFLOAT16 ? launch<D, VM, false, VCX_BFLOAT16>(a, nblocks, st)
+                                   : launch<D, VM, false, VCX_FLOAT16>(a, nblocks, st);
 }
 
 }  // namespace
@@ -445,8 +502,7 @@ extern "C" int vcx_attention_fwd(const int8_t* q8, const int8_t* k8, const uint8
   VCX_REQUIRE(Nq < (int64_t(1) << 30) && Nk < (int64_t(1) << 30), "sequence too long");
   VCX_REQUIRE(cdiv(Nk, kTile) * kTile * D < (int64_t(1) << 31), "K/V payload of one head must be below 2 GiB");
   if (expcast != 1) return fail(VCX_EUNSUPPORTED, "only the ExpCast probability encoding is implemented");
-  if (block_values && !channel_scale)
-    return fail(VCX_EUNSUPPORTED, "per-block V scales are not implemented in the fused kernel");
+  VCX_REQUIRE(block_values || channel_scale, "per-block V scales require block values (smoothing)");
   VCX_REQUIRE(out_dtype == VCX_FLOAT16 || out_dtype == VCX_BFLOAT16, "out_dtype must be float16 or bfloat16");
   VCX_REQUIRE(std::isfinite(sm_scale) && sm_scale > 0.0f, "sm_scale must be positive and finite FP32");
   VCX_REQUIRE(q8 && k8 && v8 && qs && ks && vs && out, "null tensor pointer");
@@ -471,11 +527,13 @@ extern "C" int vcx_attention_fwd(const int8_t* q8, const int8_t* k8, const uint8
   hipStream_t st = static_cast<hipStream_t>(stream);
   const bool dump = p_dump != nullptr;
   if (D == 128) {
-    return block_values ? launch_out<128, true>(a, nblocks, dump, out_dtype, st)
-                        : launch_out<128, false>(a, nblocks, dump, out_dtype, st);
+    if (!block_values) return launch_out<128, 0>(a, nblocks, dump, out_dtype, st);
+    return channel_scale ? launch_out<128, 1>(a, nblocks, dump, out_dtype, st)
+                         : launch_out<128, 2>(a, nblocks, dump, out_dtype, st);
   }
-  return block_values ? launch_out<64, true>(a, nblocks, dump, out_dtype, st)
-                      : launch_out<64, false>(a, nblocks, dump, out_dtype, st);
+  if (!block_values) return launch_out<64, 0>(a, nblocks, dump, out_dtype, st);
+  return channel_scale ? launch_out<64, 1>(a, nblocks, dump, out_dtype, st)
+                       : launch_out<64, 2>(a, nblocks, dump, out_dtype, st);
 }
 
 extern "C" int vcx_kernel_resources(int64_t D, int block_values, int64_t* out) {
@@ -483,10 +541,10 @@ extern "C" int vcx_kernel_resources(int64_t D, int block_values, int64_t* out) {
   VCX_REQUIRE(D == 64 || D == 128, "D must be 64 or 128");
   hipFuncAttributes attr{};
   const void* fn;
-  if (D == 128) fn = block_values ? reinterpret_cast<const void*>(&attn_kernel<128, true, false, VCX_BFLOAT16>)
-                                  : reinterpret_cast<const void*>(&attn_kernel<128, false, false, VCX_BFLOAT16>);
-  else fn = block_values ? reinterpret_cast<const void*>(&attn_kernel<64, true, false, VCX_BFLOAT16>)
-                         : reinterpret_cast<const void*>(&attn_kernel<64, false, false, VCX_BFLOAT16>);
+  if (D == 128) fn = block_values ? reinterpret_cast<const void*>(&attn_kernel<128, 1, false, VCX_BFLOAT16>)
+                                  : reinterpret_cast<const void*>(&attn_kernel<128, 0, false, VCX_BFLOAT16>);
+  else fn = block_values ? reinterpret_cast<const void*>(&attn_kernel<64, 1, false, VCX_BFLOAT16>)
+                         : reinterpret_cast<const void*>(&attn_kernel<64, 0, false, VCX_BFLOAT16>);
   hipError_t e = hipFuncGetAttributes(&attr, fn);
   if (e != hipSuccess) return fail(VCX_EHIP, "hipFuncGetAttributes: %s", hipGetErrorString(e));
   out[0] = attr.numRegs;

@@ -16,8 +16,8 @@ Differences a caller can observe, all deliberate:
   names select Hopper WGMMA/TMA schedules that have no MI355X counterpart.
 * The prepared ``v`` payload is stored in the gfx950 tile order
   (``vcx.value_token``), not Sage's 16-token permutation.
-* ``expcast=False`` (the Sage FP8 control path) and ``v_scale_mode="block"``
-  in the fused kernel are rejected with ValueError by this build.
+* ``expcast=False`` (the Sage FP8 control path) is rejected with ValueError
+  by this build.
 """
 import math
 
@@ -148,8 +148,6 @@ def forward_prepared(state, *, kernel_mode="optimized", out=None):
         raise ValueError("vc31/vc32 require per-channel V scale")
     if not state["expcast"]:
         raise ValueError("this build implements the ExpCast probability contract only (expcast=True)")
-    if not channel:
-        raise ValueError("per-block V scales (v_scale_mode='block') are not implemented by the gfx950 kernel")
     return _extension().forward(state["q"], state["k"], state["v"], state["qs"], state["ks"], state["vs"],
                                 state["means"], state["expcast"], state["block_values"], state["output_type"],
                                 state["scale"], channel_scale=channel, out=out)
@@ -177,8 +175,6 @@ def sageattn_vc(q, k, v, tensor_layout="HND", is_causal=False, sm_scale=None, re
     _check_scale(sm_scale)
     if not expcast:
         raise ValueError("this build implements the ExpCast probability contract only (expcast=True)")
-    if v_smooth and v_scale_mode == "block":
-        raise ValueError("per-block V scales (v_scale_mode='block') are not implemented by the gfx950 kernel")
     with torch.cuda.device(q.device):
         if tensor_layout == "NHD":
             q, k, v = (x.transpose(1, 2) for x in (q, k, v))  # strided HND views, no copy

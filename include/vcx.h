@@ -111,8 +111,10 @@ int vcx_prepare_v_fp8(const void* v, int dtype, int64_t B, int64_t H, int64_t N,
 /* Fused attention forward: INT8 QK^T on MFMA, ExpCast E4M3 probabilities,
  * FP8 PV on MFMA, online max/sum, block-mean restore, epilogue.
  * expcast must be 1. block_values = 1 consumes means/vs as written by
- * vcx_prepare_v_fp8(smooth=1, channel_scale); block_values = 0 uses vs [B,H,D]
- * and ignores means. out: fp16/bf16 (out_dtype) with element strides.
+ * vcx_prepare_v_fp8(smooth=1, channel_scale): channel_scale = 1 applies vs
+ * [B,H,D] in the epilogue, channel_scale = 0 scales every tile's contribution
+ * by its vs [B,H,tiles,D]; block_values = 0 uses vs [B,H,D], ignores means and
+ * requires channel_scale = 1. out: fp16/bf16 (out_dtype) with element strides.
  * p_dump (nullable): diagnostic copy of the E4M3 P bytes for query rows
  * [p_row_begin, p_row_end) of every head, uint8 [B,H,rows,ceil(Nk/128)*128]
  * in logical key order (padding keys 0); slower kernel variant.

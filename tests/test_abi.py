@@ -67,8 +67,8 @@ def test_invalid_calls_rejected_before_launch():
     assert rc == 1 and "sm_scale" in msg
     rc, msg = _fwd()
     assert rc == 1 and "null" in msg
-    rc, msg = _fwd(block_values=1, channel_scale=0)
-    assert rc == 2 and "per-block" in msg
+    rc, msg = _fwd(block_values=0, channel_scale=0)
+    assert rc == 1 and "per-block" in msg
     L = vcx.lib()
     assert L.vcx_expcast_codes(None, None, -1, None) == 1
     assert L.vcx_group_values(None, 1, 1, 1, 10, 128, 0, 0, 128, 9, 2, None, None, None, None, 0, None) == 2

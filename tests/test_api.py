@@ -75,12 +75,19 @@ def test_forward_prepared_dispatches_state_to_the_single_kernel(monkeypatch, mod
     assert kwargs["channel_scale"] is True
 
 
+def test_forward_prepared_block_scales_dispatch_without_channel_scale(monkeypatch):
+    # reference vc.py:161, 180-190: per-block V scales ([B,H,tiles,D]) reach the kernel as block values
+    calls = []
+    monkeypatch.setattr(api, "_extension", lambda: SimpleNamespace(forward=lambda *a, **k: calls.append((a, k)) or "out"))
+    assert api.forward_prepared(payload(True, vs_ndim=4)) == "out"
+    (args, kwargs), = calls
+    assert args[7:9] == (True, True) and kwargs["channel_scale"] is False
+
+
 def test_forward_prepared_rejections(monkeypatch):
     monkeypatch.setattr(api, "_extension", lambda: SimpleNamespace(forward=lambda *a, **k: "out"))
     with pytest.raises(ValueError, match="expcast=True"):
         api.forward_prepared({**payload(False), "expcast": False})
-    with pytest.raises(ValueError, match="per-block"):
-        api.forward_prepared(payload(True, vs_ndim=4))
     with pytest.raises(ValueError, match="per-channel V scale"):
         api.forward_prepared(payload(True, vs_ndim=4), kernel_mode="vc31_unified")
     with pytest.raises(ValueError, match="v_smooth=False"):

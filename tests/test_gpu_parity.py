@@ -362,3 +362,49 @@ def test_full_length_baseline_configs(case):
         err, bound = output_bound(got, eout)
         assert np.all(err <= bound), (r0, float((err - bound).max()))
         assert cosine(got, eout) >= 0.9999
+
+
+BLOCK = [  # B, H, Nq, Nk, D, dtype
+    (1, 2, 300, 700, 128, torch.bfloat16),
+    (2, 1, 129, 257, 64, torch.float16),
+    (1, 1, 1, 1, 128, torch.bfloat16),
+]
+
+
+@pytest.mark.parametrize("case", BLOCK, ids=lambda c: _ids(c))
+def test_attention_block_scales_p_bytes_and_output(case):
+    # v_scale_mode="block" (reference vc.py:161; preprocess.cu:24-57): every tile's
+    # contribution (PV + mass * mean) is scaled by that tile's per-channel V scale.
+    B, H, Nq, Nk, D, dt = case
+    _print_case("attention block scales", case)
+    q, k, v = make_qkv(B, H, Nq, Nk, D, dt, seed=11, kind="outlier")
+    st = o.prepare(bits(q), bits(k), bits(v), v_smooth=True, v_scale_mode="block", dtype=dtype_name(dt))
+    assert st["vs"].ndim == 4
+    tok = vcx.value_token()
+    to = _to_dev
+    v8 = to(logical_to_storage(st["v"], tok)).view(torch.float8_e4m3fn)
+    out, pd = vcx.forward(to(st["q"]), to(st["k"]), v8, to(st["qs"]), to(st["ks"]), to(st["vs"]),
+                          to(st["means"]).view(torch.float16), True, True, st["output_type"], st["scale"],
+                          channel_scale=False, p_rows=(0, Nq))
+    eout, ecodes = o.reference(st, return_codes=True)
+    np.testing.assert_array_equal(pd.cpu().numpy(), ecodes)
+    got = out.float().cpu().numpy()
+    assert np.isfinite(got).all()
+    err, bound = output_bound(got, eout)
+    assert np.all(err <= bound), float((err - bound).max())
+    assert cosine(got, eout) >= 0.9999
+
+
+def test_sageattn_vc_block_scale_end_to_end():
+    from sageattention_local import sageattn_vc
+    q, k, v = make_qkv(1, 2, 257, 400, 128, torch.bfloat16, seed=5, kind="outlier")
+    _print_case("sageattn_vc block scales")
+    out = sageattn_vc(*(x.to(DEV) for x in (q, k, v)), v_smooth=True, v_scale_mode="block").float().cpu().numpy()
+    st = _oracle_state(q, k, v, True, torch.bfloat16)
+    stb = o.prepare(bits(q), bits(k), bits(v), v_smooth=True, v_scale_mode="block", dtype="bfloat16")
+    eout = o.reference(stb)
+    err, bound = output_bound(out, eout)
+    assert np.all(err <= bound)
+    assert cosine(out, eout) >= 0.9999
+    # the channel-scale output of the same inputs is close but not identical
+    assert not np.array_equal(eout, o.reference(st))

@@ -408,3 +408,34 @@ def test_sageattn_vc_block_scale_end_to_end():
     assert cosine(out, eout) >= 0.9999
     # the channel-scale output of the same inputs is close but not identical
     assert not np.array_equal(eout, o.reference(st))
+
+
+def test_main_config_all_heads_payloads_and_sampled_rows():
+    # The benchmark's main workload in full ([1,28,37741,128] bf16, smoothing off): every
+    # payload byte and scale of all 28 heads, and the P bytes / output of 8 query rows
+    # spread over every head (first, last and ragged-block rows included).
+    B, H, N, D = 1, 28, 37741, 128
+    _print_case("main config, all heads")
+    q, k, v = make_qkv(B, H, N, N, D, torch.bfloat16, seed=0)
+    qd, kd, vd = (x.to(DEV) for x in (q, k, v))
+    q8, qs, k8, ks, _ = vcx.prepare_qk(qd, kd)
+    v8, vs, _ = vcx.prepare_v(vd)
+    st = _oracle_state(q, k, v, False, torch.bfloat16)
+    np.testing.assert_array_equal(q8.cpu().numpy(), st["q"])
+    np.testing.assert_array_equal(k8.cpu().numpy(), st["k"])
+    np.testing.assert_array_equal(qs.cpu().numpy(), st["qs"])
+    np.testing.assert_array_equal(ks.cpu().numpy(), st["ks"])
+    np.testing.assert_array_equal(storage_to_logical(v8, vcx.value_token()), st["v"])
+    np.testing.assert_array_equal(vs.cpu().numpy(), st["vs"])
+    out = vcx.forward(q8, k8, v8, qs, ks, vs, None, True, False, 1, D ** -0.5)
+    rows = np.array([0, 1, 4711, 18870, 29999, 37631, 37700, 37740])
+    eout, ecodes = o.reference(st, query_indices=rows, return_codes=True)
+    for r0 in (0, 37700):  # the P-dump variant takes one contiguous row range per launch
+        r1 = r0 + 41 if r0 else 2
+        _, pd = vcx.forward(q8, k8, v8, qs, ks, vs, None, True, False, 1, D ** -0.5, p_rows=(r0, r1))
+        sel = [i for i, r in enumerate(rows) if r0 <= r < r1]
+        np.testing.assert_array_equal(pd.cpu().numpy()[:, :, rows[sel] - r0], ecodes[:, :, sel])
+    got = out[:, :, rows].float().cpu().numpy()
+    err, bound = output_bound(got, eout)
+    assert np.all(err <= bound), float((err - bound).max())
+    assert cosine(got, eout) >= 0.9999

@@ -26,6 +26,12 @@
 //   O = alpha*O + PV (+ mass*mean), den = alpha*den + mass, out = O/den * vs.
 // The P bytes follow the contract exactly; alpha, O and den only feed the
 // bf16/fp16 output, whose tolerance covers the exp2 approximation.
+//
+// EC = false is the Sage FP8 control path (expcast=False; vc_sm90.cu:177,
+// attn_utils.cuh:355-455): a.sm = RN(sm * RN(log2 e)), base/factor as above,
+// m' = max(m, max fmaf(base, factor, -8.807)), P = E4M3(exp2(fmaf(base, factor, -m'))),
+// den and the mean restore use the unrounded sum of P. exp2 is v_exp_f32, so a P
+// byte can differ by one code from an exactly rounded exp2 next to a midpoint.
 #include "vcx_common.hpp"
 
 namespace vcx {
@@ -152,7 +158,28 @@ __device__ inline v4f mfma_fp8(const v8i& a, const v8i& b, const v4f& c) {
   return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
 }
 
-template <int D, int VM, bool DUMP>
+// Row reductions over the four lane groups that hold one query row: gfx950
+// permlane swaps give each lane the values of lanes l^16 and l^32 without an LDS
+// round trip. Every lane of the row ends with the same value (the adds commute).
+__device__ inline float row_max(float x) {
+  const auto x16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = fmaxf(__uint_as_float(x16[0]), __uint_as_float(x16[1]));
+  const auto x32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(x32[0]), __uint_as_float(x32[1]));
+}
+
+__device__ inline float row_sum(float x) {
+  const auto x16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __uint_as_float(x16[0]) + __uint_as_float(x16[1]);
+  const auto x32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(x32[0]) + __uint_as_float(x32[1]);
+}
+
+// Sage's FP8 offset: the control path's row maximum is lowered by 8.807 so that the
+// largest probability is 2^8.807 ~ 448, the E4M3 maximum (sal/csrc/qattn/attn_utils.cuh:30).
+constexpr float kFp8Offset = 8.807f;
+
+template <int D, int VM, bool DUMP, bool EC>
 struct Wave {
   static constexpr int DS = D / 64;  // 64-deep QK steps
   static constexpr int CB = D / 16;  // 16-channel output blocks
@@ -201,54 +228,87 @@ struct Wave {
       __builtin_amdgcn_sched_barrier(0);
     }
 
-    // ---- logits, online max, ExpCast codes
+    // ---- logits, online max, P bytes (ExpCast codes, or E4M3 probabilities on the control path)
     v8i P[2];
-    float alpha[2];
+    float alpha[2], tmass[2];
 #pragma unroll
     for (int qg = 0; qg < 2; ++qg) {
-      float lg[8][4];
-      float tmax = -INFINITY;
-      const float dq = qsv[qg] * ksv;
-      if constexpr (!LAST) {
-        const float c = a.sm * dq;
+      if constexpr (EC) {
+        float lg[8][4];
+        float tmax = -INFINITY;
+        const float dq = qsv[qg] * ksv;
+        if constexpr (!LAST) {
+          const float c = a.sm * dq;
 #pragma unroll
-        for (int j = 0; j < 8; ++j)
+          for (int j = 0; j < 8; ++j)
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            lg[j][r] = static_cast<float>(S[qg][j][r]) * c;
-            tmax = fmaxf(tmax, lg[j][r]);
-          }
-      } else {
+            for (int r = 0; r < 4; ++r) {
+              lg[j][r] = static_cast<float>(S[qg][j][r]) * c;
+              tmax = fmaxf(tmax, lg[j][r]);
+            }
+        } else {
 #pragma unroll
-        for (int j = 0; j < 8; ++j)
+          for (int j = 0; j < 8; ++j)
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int64_t key = t * kTile + 16 * j + 8 * (r >> 1) + 2 * G + (r & 1);
-            float x = (static_cast<float>(S[qg][j][r]) * dq) * a.sm;
-            lg[j][r] = key < a.Nk ? x : -INFINITY;
-            tmax = fmaxf(tmax, lg[j][r]);
-          }
-      }
-      {
-        // Row maximum over the four lane groups: gfx950 permlane swaps give each
-        // lane the values of lanes l^16 and l^32 without an LDS round trip.
-        const auto x16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(tmax), __float_as_uint(tmax), false, false);
-        tmax = fmaxf(__uint_as_float(x16[0]), __uint_as_float(x16[1]));
-        const auto x32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(tmax), __float_as_uint(tmax), false, false);
-        tmax = fmaxf(__uint_as_float(x32[0]), __uint_as_float(x32[1]));
-      }
-      const float mn = fmaxf(m[qg], tmax);
-      alpha[qg] = __builtin_amdgcn_exp2f((m[qg] - mn) * 1.44269504088896341f);
-      m[qg] = mn;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        uint32_t w = 0;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float u = __builtin_fmaf(lg[j][r] - mn, kExpA, kExpB);
-          w = __builtin_amdgcn_cvt_pk_u8_f32(u, r, w);
+            for (int r = 0; r < 4; ++r) {
+              const int64_t key = t * kTile + 16 * j + 8 * (r >> 1) + 2 * G + (r & 1);
+              float x = (static_cast<float>(S[qg][j][r]) * dq) * a.sm;
+              lg[j][r] = key < a.Nk ? x : -INFINITY;
+              tmax = fmaxf(tmax, lg[j][r]);
+            }
         }
-        P[qg][j] = static_cast<int>(w);
+        tmax = row_max(tmax);
+        const float mn = fmaxf(m[qg], tmax);
+        alpha[qg] = __builtin_amdgcn_exp2f((m[qg] - mn) * 1.44269504088896341f);
+        m[qg] = mn;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          uint32_t w = 0;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const float u = __builtin_fmaf(lg[j][r] - mn, kExpA, kExpB);
+            w = __builtin_amdgcn_cvt_pk_u8_f32(u, r, w);
+          }
+          P[qg][j] = static_cast<int>(w);
+        }
+      } else {
+        // Sage FP8 control path: log2-domain logits (a.sm carries RN(sm * RN(log2 e))),
+        // running maximum with the upstream 8.807 offset, P = E4M3(exp2(.)) and an
+        // unrounded mass.
+        float bs[8][4];
+        float tmax = -INFINITY;
+        const float dq = qsv[qg] * ksv;
+        const float f = LAST ? a.sm : a.sm * dq;
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            float b = static_cast<float>(S[qg][j][r]);
+            if constexpr (LAST) {
+              const int64_t key = t * kTile + 16 * j + 8 * (r >> 1) + 2 * G + (r & 1);
+              b = key < a.Nk ? b * dq : -INFINITY;
+            }
+            bs[j][r] = b;
+            tmax = fmaxf(tmax, __builtin_fmaf(b, f, -kFp8Offset));
+          }
+        tmax = row_max(tmax);
+        const float mn = fmaxf(m[qg], tmax);
+        alpha[qg] = __builtin_amdgcn_exp2f(m[qg] - mn);
+        m[qg] = mn;
+        float ls = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          float pr[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            pr[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(bs[j][r], f, -mn));
+            ls += pr[r];
+          }
+          int w = __builtin_amdgcn_cvt_pk_fp8_f32(pr[0], pr[1], 0, false);
+          w = __builtin_amdgcn_cvt_pk_fp8_f32(pr[2], pr[3], w, true);
+          P[qg][j] = w;
+        }
+        tmass[qg] = row_sum(ls);
       }
       if constexpr (DUMP) {
         if (row[qg] >= a.prow0 && row[qg] < a.prow1 && row[qg] < a.Nq) {
@@ -283,9 +343,9 @@ struct Wave {
       // folded into O right away.
 #pragma unroll
       for (int qg = 0; qg < 2; ++qg) {
-        const v4f ms = mfma_fp8(ones, P[qg], zero);
-        mass[qg] = ms[0];
-        den[qg] = den[qg] * alpha[qg] + ms[0];
+        if constexpr (EC) mass[qg] = mfma_fp8(ones, P[qg], zero)[0];
+        else mass[qg] = tmass[qg];
+        den[qg] = den[qg] * alpha[qg] + mass[qg];
       }
       v8i vc = load_v(lv, 0), vn;
 #pragma unroll
@@ -320,9 +380,9 @@ struct Wave {
     }
 #pragma unroll
     for (int qg = 0; qg < 2; ++qg) {
-      const v4f ms = mfma_fp8(ones, P[qg], zero);
-      mass[qg] = ms[0];
-      den[qg] = den[qg] * alpha[qg] + ms[0];
+      if constexpr (EC) mass[qg] = mfma_fp8(ones, P[qg], zero)[0];
+      else mass[qg] = tmass[qg];
+      den[qg] = den[qg] * alpha[qg] + mass[qg];
     }
     if constexpr (SMOOTH) {
 #pragma unroll
@@ -339,7 +399,7 @@ struct Wave {
   }
 };
 
-template <int D, int VM, bool DUMP, int OUT>
+template <int D, int VM, bool DUMP, int OUT, bool EC>
 __global__ __launch_bounds__(kThreadsPerBlock, 2) void attn_kernel(AttnArgs a) {
   typedef TileLoader<D, VM> LD;
   constexpr int KB = kTile * D, VB = D * kTile;
@@ -356,14 +416,14 @@ __global__ __launch_bounds__(kThreadsPerBlock, 2) void attn_kernel(AttnArgs a) {
   const int64_t bh = logical / a.qblocks, qb = logical % a.qblocks;
 
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  Wave<D, VM, DUMP> w;
+  Wave<D, VM, DUMP, EC> w;
   w.G = lane >> 4;
   w.li = lane & 15;
   w.bh_ = bh;
   // Lane-constant LDS offsets.
   const int kr = 8 * ((w.li & 3) >> 1) + 2 * (w.li >> 2) + (w.li & 1);
 #pragma unroll
-  for (int ds = 0; ds < Wave<D, VM, DUMP>::DS; ++ds)
+  for (int ds = 0; ds < Wave<D, VM, DUMP, EC>::DS; ++ds)
     w.koff[ds] = kr * D + ((((D == 128) ? 4 * ds : 0) + w.G) ^ swz_k<D>(kr)) * 16;
 #pragma unroll
   for (int h = 0; h < 2; ++h) w.voff[h] = w.li * kTile + (((2 * w.G + h) ^ swz_v(w.li)) * 16);
@@ -376,14 +436,14 @@ __global__ __launch_bounds__(kThreadsPerBlock, 2) void attn_kernel(AttnArgs a) {
     const int64_t si = (r / 16) * 8 + r % 8;
     w.qsv[qg] = si < a.qs_len ? a.qs[bh * a.qs_len + si] : 1.0f;
 #pragma unroll
-    for (int ds = 0; ds < Wave<D, VM, DUMP>::DS; ++ds) {
+    for (int ds = 0; ds < Wave<D, VM, DUMP, EC>::DS; ++ds) {
       if (r < a.Nq) w.qf[qg][ds] = *reinterpret_cast<const v4i*>(a.q8 + (bh * a.Nq + r) * D + ds * 64 + w.G * 16);
       else w.qf[qg][ds] = v4i{0, 0, 0, 0};
     }
     w.m[qg] = -5000000.0f;
     w.den[qg] = 0.0f;
 #pragma unroll
-    for (int cb = 0; cb < Wave<D, VM, DUMP>::CB; ++cb) w.O[qg][cb] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int cb = 0; cb < Wave<D, VM, DUMP, EC>::CB; ++cb) w.O[qg][cb] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
   }
 
   LD ld;
@@ -422,10 +482,10 @@ __global__ __launch_bounds__(kThreadsPerBlock, 2) void attn_kernel(AttnArgs a) {
     const float inv = 1.0f / w.den[qg];
     uint16_t* out = static_cast<uint16_t*>(a.out) + b * a.osb + h * a.osh + w.row[qg] * a.osn;
 #pragma unroll
-    for (int cb = 0; cb < Wave<D, VM, DUMP>::CB; ++cb) {
+    for (int cb = 0; cb < Wave<D, VM, DUMP, EC>::CB; ++cb) {
       const int ch = 16 * cb + 4 * w.G;
       // per-channel V scale (per-block scales were applied tile by tile)
-      const float4 sc = Wave<D, VM, DUMP>::BSCALE ? make_float4(1.0f, 1.0f, 1.0f, 1.0f)
+      const float4 sc = Wave<D, VM, DUMP, EC>::BSCALE ? make_float4(1.0f, 1.0f, 1.0f, 1.0f)
                                                   : *reinterpret_cast<const float4*>(a.vs + bh * D + ch);
       const float y0 = w.O[qg][cb][0] * inv * sc.x, y1 = w.O[qg][cb][1] * inv * sc.y;
       const float y2 = w.O[qg][cb][2] * inv * sc.z, y3 = w.O[qg][cb][3] * inv * sc.w;
@@ -444,45 +504,75 @@ __global__ __launch_bounds__(kThreadsPerBlock, 2) void attn_kernel(AttnArgs a) {
 
 // Explicit instantiation of every launch variant: hipcc's host pass otherwise
 // emitted the kernel handle of only the first variant named in each ternary.
-template __global__ void attn_kernel<64, 0, false, 0>(AttnArgs);
-template __global__ void attn_kernel<64, 0, false, 1>(AttnArgs);
-template __global__ void attn_kernel<64, 0, true, 0>(AttnArgs);
-template __global__ void attn_kernel<64, 0, true, 1>(AttnArgs);
-template __global__ void attn_kernel<64, 1, false, 0>(AttnArgs);
-template __global__ void attn_kernel<64, 1, false, 1>(AttnArgs);
-template __global__ void attn_kernel<64, 1, true, 0>(AttnArgs);
-template __global__ void attn_kernel<64, 1, true, 1>(AttnArgs);
-template __global__ void attn_kernel<64, 2, false, 0>(AttnArgs);
-template __global__ void attn_kernel<64, 2, false, 1>(AttnArgs);
-template __global__ void attn_kernel<64, 2, true, 0>(AttnArgs);
-template __global__ void attn_kernel<64, 2, true, 1>(AttnArgs);
-template __global__ void attn_kernel<128, 0, false, 0>(AttnArgs);
-template __global__ void attn_kernel<128, 0, false, 1>(AttnArgs);
-template __global__ void attn_kernel<128, 0, true, 0>(AttnArgs);
-template __global__ void attn_kernel<128, 0, true, 1>(AttnArgs);
-template __global__ void attn_kernel<128, 1, false, 0>(AttnArgs);
-template __global__ void attn_kernel<128, 1, false, 1>(AttnArgs);
-template __global__ void attn_kernel<128, 1, true, 0>(AttnArgs);
-template __global__ void attn_kernel<128, 1, true, 1>(AttnArgs);
-template __global__ void attn_kernel<128, 2, false, 0>(AttnArgs);
-template __global__ void attn_kernel<128, 2, false, 1>(AttnArgs);
-template __global__ void attn_kernel<128, 2, true, 0>(AttnArgs);
-template __global__ void attn_kernel<128, 2, true, 1>(AttnArgs);
+template __global__ void attn_kernel<64, 0, false, 0, true>(AttnArgs);
+template __global__ void attn_kernel<64, 0, false, 1, true>(AttnArgs);
+template __global__ void attn_kernel<64, 0, true, 0, true>(AttnArgs);
+template __global__ void attn_kernel<64, 0, true, 1, true>(AttnArgs);
+template __global__ void attn_kernel<64, 1, false, 0, true>(AttnArgs);
+template __global__ void attn_kernel<64, 1, false, 1, true>(AttnArgs);
+template __global__ void attn_kernel<64, 1, true, 0, true>(AttnArgs);
+template __global__ void attn_kernel<64, 1, true, 1, true>(AttnArgs);
+template __global__ void attn_kernel<64, 2, false, 0, true>(AttnArgs);
+template __global__ void attn_kernel<64, 2, false, 1, true>(AttnArgs);
+template __global__ void attn_kernel<64, 2, true, 0, true>(AttnArgs);
+template __global__ void attn_kernel<64, 2, true, 1, true>(AttnArgs);
+template __global__ void attn_kernel<128, 0, false, 0, true>(AttnArgs);
+template __global__ void attn_kernel<128, 0, false, 1, true>(AttnArgs);
+template __global__ void attn_kernel<128, 0, true, 0, true>(AttnArgs);
+template __global__ void attn_kernel<128, 0, true, 1, true>(AttnArgs);
+template __global__ void attn_kernel<128, 1, false, 0, true>(AttnArgs);
+template __global__ void attn_kernel<128, 1, false, 1, true>(AttnArgs);
+template __global__ void attn_kernel<128, 1, true, 0, true>(AttnArgs);
+template __global__ void attn_kernel<128, 1, true, 1, true>(AttnArgs);
+template __global__ void attn_kernel<128, 2, false, 0, true>(AttnArgs);
+template __global__ void attn_kernel<128, 2, false, 1, true>(AttnArgs);
+template __global__ void attn_kernel<128, 2, true, 0, true>(AttnArgs);
+template __global__ void attn_kernel<128, 2, true, 1, true>(AttnArgs);
+template __global__ void attn_kernel<64, 0, false, 0, false>(AttnArgs);
+template __global__ void attn_kernel<64, 0, false, 1, false>(AttnArgs);
+template __global__ void attn_kernel<64, 0, true, 0, false>(AttnArgs);
+template __global__ void attn_kernel<64, 0, true, 1, false>(AttnArgs);
+template __global__ void attn_kernel<64, 1, false, 0, false>(AttnArgs);
+template __global__ void attn_kernel<64, 1, false, 1, false>(AttnArgs);
+template __global__ void attn_kernel<64, 1, true, 0, false>(AttnArgs);
+template __global__ void attn_kernel<64, 1, true, 1, false>(AttnArgs);
+template __global__ void attn_kernel<64, 2, false, 0, false>(AttnArgs);
+template __global__ void attn_kernel<64, 2, false, 1, false>(AttnArgs);
+template __global__ void attn_kernel<64, 2, true, 0, false>(AttnArgs);
+template __global__ void attn_kernel<64, 2, true, 1, false>(AttnArgs);
+template __global__ void attn_kernel<128, 0, false, 0, false>(AttnArgs);
+template __global__ void attn_kernel<128, 0, false, 1, false>(AttnArgs);
+template __global__ void attn_kernel<128, 0, true, 0, false>(AttnArgs);
+template __global__ void attn_kernel<128, 0, true, 1, false>(AttnArgs);
+template __global__ void attn_kernel<128, 1, false, 0, false>(AttnArgs);
+template __global__ void attn_kernel<128, 1, false, 1, false>(AttnArgs);
+template __global__ void attn_kernel<128, 1, true, 0, false>(AttnArgs);
+template __global__ void attn_kernel<128, 1, true, 1, false>(AttnArgs);
+template __global__ void attn_kernel<128, 2, false, 0, false>(AttnArgs);
+template __global__ void attn_kernel<128, 2, false, 1, false>(AttnArgs);
+template __global__ void attn_kernel<128, 2, true, 0, false>(AttnArgs);
+template __global__ void attn_kernel<128, 2, true, 1, false>(AttnArgs);
 
-template <int D, int VM, bool DUMP, int OUT>
+template <int D, int VM, bool DUMP, int OUT, bool EC>
 int launch(const AttnArgs& a, int64_t nblocks, hipStream_t st) {
-  attn_kernel<D, VM, DUMP, OUT><<<dim3(static_cast<unsigned>(nblocks)), kThreadsPerBlock, 0, st>>>(a);
+  attn_kernel<D, VM, DUMP, OUT, EC><<<dim3(static_cast<unsigned>(nblocks)), kThreadsPerBlock, 0, st>>>(a);
   return check_launch("attn_kernel");
 }
 
-template <int D, int VM>
+template <int D, int VM, bool EC>
 int launch_out(const AttnArgs& a, int64_t nblocks, bool dump, int out_dtype, hipStream_t st) {
   if (dump) {
-    return out_dtype == VCX_BFLOAT16 ? launch<D, VM, true, VCX_BFLOAT16>(a, nblocks, st)
-                                     : launch<D, VM, true, VCX_FLOAT16>(a, nblocks, st);
+    return out_dtype == VCX_BFLOAT16 ? launch<D, VM, true, VCX_BFLOAT16, EC>(a, nblocks, st)
+                                     : launch<D, VM, true, VCX_FLOAT16, EC>(a, nblocks, st);
   }
-  return out_dtype == VCX_BFLOAT16 ? launch<D, VM, false, VCX_BFLOAT16>(a, nblocks, st)
-                                   : launch<D, VM, false, VCX_FLOAT16>(a, nblocks, st);
+  return out_dtype == VCX_BFLOAT16 ? launch<D, VM, false, VCX_BFLOAT16, EC>(a, nblocks, st)
+                                   : launch<D, VM, false, VCX_FLOAT16, EC>(a, nblocks, st);
+}
+
+template <int D, int VM>
+int launch_mode(const AttnArgs& a, int64_t nblocks, bool dump, int out_dtype, bool expcast, hipStream_t st) {
+  return expcast ? launch_out<D, VM, true>(a, nblocks, dump, out_dtype, st)
+                 : launch_out<D, VM, false>(a, nblocks, dump, out_dtype, st);
 }
 
 }  // namespace
@@ -501,7 +591,7 @@ extern "C" int vcx_attention_fwd(const int8_t* q8, const int8_t* k8, const uint8
   VCX_REQUIRE(B * H <= 65535, "B*H exceeds 65535");
   VCX_REQUIRE(Nq < (int64_t(1) << 30) && Nk < (int64_t(1) << 30), "sequence too long");
   VCX_REQUIRE(cdiv(Nk, kTile) * kTile * D < (int64_t(1) << 31), "K/V payload of one head must be below 2 GiB");
-  if (expcast != 1) return fail(VCX_EUNSUPPORTED, "only the ExpCast probability encoding is implemented");
+  VCX_REQUIRE(expcast == 0 || expcast == 1, "expcast must be 0 or 1");
   VCX_REQUIRE(block_values || channel_scale, "per-block V scales require block values (smoothing)");
   VCX_REQUIRE(out_dtype == VCX_FLOAT16 || out_dtype == VCX_BFLOAT16, "out_dtype must be float16 or bfloat16");
   VCX_REQUIRE(std::isfinite(sm_scale) && sm_scale > 0.0f, "sm_scale must be positive and finite FP32");
@@ -520,20 +610,23 @@ extern "C" int vcx_attention_fwd(const int8_t* q8, const int8_t* k8, const uint8
   a.q8 = q8; a.k8 = k8; a.v8 = v8; a.qs = qs; a.ks = ks; a.vs = vs; a.means = means; a.out = out;
   a.osb = o_sb; a.osh = o_sh; a.osn = o_sn;
   a.H = H; a.Nq = Nq; a.Nk = Nk; a.tiles = cdiv(Nk, kTile); a.qblocks = cdiv(Nq, kRowsPerBlock);
-  a.qs_len = cdiv(Nq, 64) * 32; a.sm = sm_scale;
+  a.qs_len = cdiv(Nq, 64) * 32;
+  // The control path works in the log2 domain: RN(sm * RN(log2 e)) (sal/csrc/vc/vc_sm90.cu:177).
+  a.sm = expcast ? sm_scale : sm_scale * 1.4426950408889634f;
   a.pdump = p_dump; a.prow0 = p_row_begin; a.prow1 = p_row_end;
   const int64_t nblocks = B * H * a.qblocks;
   VCX_REQUIRE(nblocks < (int64_t(1) << 31), "too many blocks");
   hipStream_t st = static_cast<hipStream_t>(stream);
   const bool dump = p_dump != nullptr;
+  const bool ec = expcast == 1;
   if (D == 128) {
-    if (!block_values) return launch_out<128, 0>(a, nblocks, dump, out_dtype, st);
-    return channel_scale ? launch_out<128, 1>(a, nblocks, dump, out_dtype, st)
-                         : launch_out<128, 2>(a, nblocks, dump, out_dtype, st);
+    if (!block_values) return launch_mode<128, 0>(a, nblocks, dump, out_dtype, ec, st);
+    return channel_scale ? launch_mode<128, 1>(a, nblocks, dump, out_dtype, ec, st)
+                         : launch_mode<128, 2>(a, nblocks, dump, out_dtype, ec, st);
   }
-  if (!block_values) return launch_out<64, 0>(a, nblocks, dump, out_dtype, st);
-  return channel_scale ? launch_out<64, 1>(a, nblocks, dump, out_dtype, st)
-                       : launch_out<64, 2>(a, nblocks, dump, out_dtype, st);
+  if (!block_values) return launch_mode<64, 0>(a, nblocks, dump, out_dtype, ec, st);
+  return channel_scale ? launch_mode<64, 1>(a, nblocks, dump, out_dtype, ec, st)
+                       : launch_mode<64, 2>(a, nblocks, dump, out_dtype, ec, st);
 }
 
 extern "C" int vcx_kernel_resources(int64_t D, int block_values, int64_t* out) {
@@ -541,10 +634,10 @@ extern "C" int vcx_kernel_resources(int64_t D, int block_values, int64_t* out) {
   VCX_REQUIRE(D == 64 || D == 128, "D must be 64 or 128");
   hipFuncAttributes attr{};
   const void* fn;
-  if (D == 128) fn = block_values ? reinterpret_cast<const void*>(&attn_kernel<128, 1, false, VCX_BFLOAT16>)
-                                  : reinterpret_cast<const void*>(&attn_kernel<128, 0, false, VCX_BFLOAT16>);
-  else fn = block_values ? reinterpret_cast<const void*>(&attn_kernel<64, 1, false, VCX_BFLOAT16>)
-                         : reinterpret_cast<const void*>(&attn_kernel<64, 0, false, VCX_BFLOAT16>);
+  if (D == 128) fn = block_values ? reinterpret_cast<const void*>(&attn_kernel<128, 1, false, VCX_BFLOAT16, true>)
+                                  : reinterpret_cast<const void*>(&attn_kernel<128, 0, false, VCX_BFLOAT16, true>);
+  else fn = block_values ? reinterpret_cast<const void*>(&attn_kernel<64, 1, false, VCX_BFLOAT16, true>)
+                         : reinterpret_cast<const void*>(&attn_kernel<64, 0, false, VCX_BFLOAT16, true>);
   hipError_t e = hipFuncGetAttributes(&attr, fn);
   if (e != hipSuccess) return fail(VCX_EHIP, "hipFuncGetAttributes: %s", hipGetErrorString(e));
   out[0] = attr.numRegs;

@@ -16,8 +16,9 @@ Differences a caller can observe, all deliberate:
   names select Hopper WGMMA/TMA schedules that have no MI355X counterpart.
 * The prepared ``v`` payload is stored in the gfx950 tile order
   (``vcx.value_token``), not Sage's 16-token permutation.
-* ``expcast=False`` (the Sage FP8 control path) is rejected with ValueError
-  by this build.
+* ``expcast=False`` runs the Sage FP8 control path (E4M3 probabilities from
+  the hardware exp2, unrounded exp2 mass); its P bytes can differ from an
+  exactly rounded exp2 next to an E4M3 rounding midpoint.
 """
 import math
 
@@ -127,8 +128,6 @@ def prepare(q, k, v, *, expcast=True, v_smooth=True, clusters=8, iterations=2, s
         raise ValueError("v_scale_mode must be 'channel' or 'block'")
     if grouping_mode not in ("fused", "legacy"):
         raise ValueError("grouping_mode must be 'fused' or 'legacy'")
-    if not expcast:
-        raise ValueError("this build implements the ExpCast probability contract only (expcast=True)")
     ext = _extension()
     permutation = ext.group_values(v, clusters, iterations) if v_smooth else None
     q8, qs, k8, ks, km = ext.prepare_qk(q, k, permutation)
@@ -146,8 +145,6 @@ def forward_prepared(state, *, kernel_mode="optimized", out=None):
                 expcast=state["expcast"], dim=state["q"].shape[-1], v_scale_mode="channel" if channel else "block")
     if kernel_mode in UNIFIED_MODES and state["vs"].ndim != 3:
         raise ValueError("vc31/vc32 require per-channel V scale")
-    if not state["expcast"]:
-        raise ValueError("this build implements the ExpCast probability contract only (expcast=True)")
     return _extension().forward(state["q"], state["k"], state["v"], state["qs"], state["ks"], state["vs"],
                                 state["means"], state["expcast"], state["block_values"], state["output_type"],
                                 state["scale"], channel_scale=channel, out=out)
@@ -173,8 +170,6 @@ def sageattn_vc(q, k, v, tensor_layout="HND", is_causal=False, sm_scale=None, re
     validate_inputs(q, k, v, tensor_layout, is_causal, return_lse, expcast, v_smooth, clusters, iterations)
     _require_gfx950(q.device)
     _check_scale(sm_scale)
-    if not expcast:
-        raise ValueError("this build implements the ExpCast probability contract only (expcast=True)")
     with torch.cuda.device(q.device):
         if tensor_layout == "NHD":
             q, k, v = (x.transpose(1, 2) for x in (q, k, v))  # strided HND views, no copy
@@ -203,6 +198,7 @@ def sage_vc_build_info():
             "qk_hadamard": False, "v_block": 128, "mean_dtype": "float16",
             "clustering": "<=8 clusters, Lloyd with fp64 distances, stable counting sort; fresh every call",
             "expcast_probability": "exact FP32 RN multiply/subtract + single-rounding FMA + saturating RNE byte",
+            "control_probability": "log2-domain FMA with the 8.807 offset, hardware exp2, RNE E4M3; unrounded mass",
             "mass": "FP8 MFMA row sum with an all-ones operand (same accumulation as PV)",
             "v_layout": "gfx950_tile128", "kernel_modes": list(BASE_MODES) + list(SAGE_LAYOUT_MODES),
             "default_kernel_mode": "optimized"}

@@ -6,11 +6,12 @@ denoising-step schedule (core.py:181-226) and ``attention(...) -> (out,
 counters)`` with backend dispatch (core.py:263-371).
 
 Backends of this build:
-* ``"hip"``: the gfx950 sageattn_vc path (Sage per-thread INT8 QK, ExpCast,
-  FP8 PV, optional V grouping + block smoothing) through libvcx. It requires
-  ``qk_format="int8"`` and the sageattn_vc block geometry (q_block=64,
-  k_quant_block=128, kv_block=128, k_smooth=True, qk_hadamard=False,
-  mean_dtype="float16", expcast=True, quantize=True).
+* ``"hip"``: the gfx950 sageattn_vc path (Sage per-thread INT8 QK, ExpCast or
+  the Sage FP8 control probabilities (``expcast=False``), FP8 PV, optional V
+  grouping + block smoothing) through libvcx. It requires ``qk_format="int8"``
+  and the sageattn_vc block geometry (q_block=64, k_quant_block=128,
+  kv_block=128, k_smooth=True, qk_hadamard=False, mean_dtype="float16",
+  quantize=True).
 * ``"reference"``, ``"npu_fp8"``, ``"cuda_fp8"``: validated by ``Config``
   exactly as in the reference (core.py:36-65) so existing configurations keep
   constructing; ``attention`` raises NotImplementedError for them (the eager
@@ -76,7 +77,7 @@ class Config:
             if self.k_quant_block > 4096:
                 raise ValueError("cuda_fp8 k_quant_block must be <= 4096")
         if self.backend == "hip":
-            required = dict(qk_format="int8", quantize=True, expcast=True, q_block=64, k_quant_block=128,
+            required = dict(qk_format="int8", quantize=True, q_block=64, k_quant_block=128,
                             kv_block=128, k_smooth=True, qk_hadamard=False, mean_dtype="float16")
             bad = [f"{k}={v!r}" for k, v in required.items() if getattr(self, k) != v]
             if bad:
@@ -192,12 +193,13 @@ def attention(q, k, v, config=None, *, cache=None, step=0, total_steps=1, reques
 
     q8, qs, k8, ks, km = vcx.prepare_qk(q, k, pi)
     v8, vs, means = vcx.prepare_v(v, pi, smooth=active, channel_scale=True)
-    out = vcx.forward(q8, k8, v8, qs, ks, vs, means, True, active, 0 if q.dtype == torch.float16 else 1, scale)
+    out = vcx.forward(q8, k8, v8, qs, ks, vs, means, cfg.expcast, active, 0 if q.dtype == torch.float16 else 1,
+                      scale)
     return out, {
         "backend": "hip",
         "smoothing_active": active,
         "layout_refreshed": refreshed,
-        "expcast": True,
+        "expcast": cfg.expcast,
         "k_smooth": True,
         "qk_hadamard": False,
         "qk_format": "int8",

@@ -514,21 +514,34 @@ VCO_EXPORT void vco_quant_v_smooth(const uint16_t* v, int dtype, int64_t BH, int
  * :414-549 (last tile, masking), :551-612 (epilogue); probability contract
  * sal/csrc/vc/vc_math.cuh:268-384; mean restore :410-474; decoded-payload
  * oracle sal/sageattention_local/vc_reference.py:20-91.
+ *
+ * expcast = 0 is the upstream Sage FP8 control path instead
+ * (sal/sageattention_local/vc_reference.py:31-32,58-66; sal/csrc/vc/vc_sm90.cu:177,284-296;
+ * sal/csrc/qattn/attn_utils.cuh:30, update_mdo :355-455 with exp_offset; sal/csrc/vc/vc_math.cuh:358-362):
+ *   s2 = RN(sm * RN(log2 e)); base/factor as above with s2 in place of sm
+ *   (tiles before the last: base = float(acc), factor = RN(s2 * dq); last tile:
+ *   base = RN(float(acc) * dq), factor = s2);
+ *   m' = max(m, max_k fmaf(base, factor, -8.807f)); alpha = exp2(m - m')
+ *   p = exp2(fmaf(base, factor, -m')) (binary32, unrounded); P byte = E4M3(p), RN-even
+ *   mass = sum p (unrounded, also in the mean restore); PV uses the decoded P byte.
+ * exp2 is libm's exp2f here; the kernel's hardware exp2 may differ from it by an ulp,
+ * which moves a P byte only when p sits next to an E4M3 rounding midpoint.
  * q8 [BH][nq][D]; k8 [BH][nk][D]; v8 LOGICAL [BH][D][tiles*128];
  * qs [BH][ceil(nq/64)*32]; ks [BH][tiles*4];
  * vs: NULL (no scale), [BH][D] (channel) or [BH][tiles][D] (block_scale=1);
  * means: NULL or [BH][tiles][D] binary16 bits;
  * rows [nrows] query indices; out [BH][nrows][D] float;
  * pcodes (nullable) [BH][nrows][tiles*128]. */
-VCO_EXPORT void vco_attention(const int8_t* q8, const int8_t* k8, const uint8_t* v8,
-                              const float* qs, const float* ks, const float* vs,
-                              const uint16_t* means, int block_scale, int64_t BH, int64_t nq,
-                              int64_t nk, int D, float sm, const int64_t* rows, int64_t nrows,
-                              float* out, uint8_t* pcodes) {
+static void attention_rows(const int8_t* q8, const int8_t* k8, const uint8_t* v8,
+                           const float* qs, const float* ks, const float* vs,
+                           const uint16_t* means, int block_scale, int64_t BH, int64_t nq,
+                           int64_t nk, int D, float sm, const int64_t* rows, int64_t nrows,
+                           float* out, uint8_t* pcodes, int expcast) {
   int64_t tiles = (nk + 127) / 128, npad = tiles * 128;
   int64_t qsn = (nq + 63) / 64 * 32;
   float* vdec = (float*)malloc(sizeof(float) * 256);  /* decode table */
   for (int c = 0; c < 256; ++c) vdec[c] = vco_e4m3_decode((uint8_t)c);
+  const float s = expcast ? sm : sm * 1.4426950408889634f;
 #pragma omp parallel for schedule(dynamic) collapse(2)
   for (int64_t h = 0; h < BH; ++h) {
     for (int64_t ri = 0; ri < nrows; ++ri) {
@@ -538,7 +551,7 @@ VCO_EXPORT void vco_attention(const int8_t* q8, const int8_t* k8, const uint8_t*
       float m = -5000000.0f;
       double den = 0.0;
       double o[128];
-      float logit[128];
+      float logit[128], factor[128];
       uint8_t code[128];
       for (int d = 0; d < D; ++d) o[d] = 0.0;
       for (int64_t t = 0; t < tiles; ++t) {
@@ -546,29 +559,44 @@ VCO_EXPORT void vco_attention(const int8_t* q8, const int8_t* k8, const uint8_t*
         float tmax = -INFINITY;
         for (int i = 0; i < 128; ++i) {
           int64_t key = t * 128 + i;
-          if (key >= nk) { logit[i] = -INFINITY; continue; }
+          if (key >= nk) { logit[i] = -INFINITY; factor[i] = 1.0f; continue; }
           const int8_t* krow = k8 + (h * nk + key) * D;
           int32_t acc = 0;
           for (int d = 0; d < D; ++d) acc += (int32_t)qrow[d] * (int32_t)krow[d];
           float dq = qscale * ks[h * tiles * 4 + t * 4 + (i % 8) / 2];
           float f = (float)acc;
-          float lg;
-          if (!last) { float c = sm * dq; lg = f * c; }
-          else { float a = f * dq; lg = a * sm; }
-          logit[i] = lg;
-          tmax = fmaxf(tmax, lg);
+          float base, fac;
+          if (!last) { base = f; fac = s * dq; }
+          else { base = f * dq; fac = s; }
+          if (expcast) {
+            float lg = base * fac;
+            logit[i] = lg;
+            tmax = fmaxf(tmax, lg);
+          } else {
+            logit[i] = base;  /* the control path keeps base and factor apart */
+            factor[i] = fac;
+            tmax = fmaxf(tmax, fmaf(base, fac, -8.807f));
+          }
         }
         float mnew = fmaxf(m, tmax);
-        float alpha = expf(m - mnew);
+        float alpha = expcast ? expf(m - mnew) : exp2f(m - mnew);
         m = mnew;
         double mass = 0.0;
         double prod[128];
         for (int d = 0; d < D; ++d) prod[d] = 0.0;
         for (int i = 0; i < 128; ++i) {
-          float shifted = logit[i] - mnew;
-          code[i] = vco_expcast_code(shifted);
-          double p = (double)vdec[code[i]];
-          mass += p;
+          double p;
+          if (expcast) {
+            float shifted = logit[i] - mnew;
+            code[i] = vco_expcast_code(shifted);
+            p = (double)vdec[code[i]];
+            mass += p;
+          } else {
+            float e = exp2f(fmaf(logit[i], factor[i], -mnew));
+            code[i] = vco_e4m3_encode(e);
+            p = (double)vdec[code[i]];
+            mass += (double)e;
+          }
           if (p != 0.0)
             for (int d = 0; d < D; ++d)
               prod[d] += p * (double)vdec[v8[(h * D + d) * npad + t * 128 + i]];
@@ -592,4 +620,24 @@ VCO_EXPORT void vco_attention(const int8_t* q8, const int8_t* k8, const uint8_t*
     }
   }
   free(vdec);
+}
+
+VCO_EXPORT void vco_attention(const int8_t* q8, const int8_t* k8, const uint8_t* v8,
+                              const float* qs, const float* ks, const float* vs,
+                              const uint16_t* means, int block_scale, int64_t BH, int64_t nq,
+                              int64_t nk, int D, float sm, const int64_t* rows, int64_t nrows,
+                              float* out, uint8_t* pcodes) {
+  attention_rows(q8, k8, v8, qs, ks, vs, means, block_scale, BH, nq, nk, D, sm, rows, nrows,
+                 out, pcodes, 1);
+}
+
+/* The Sage FP8 control path (expcast=False); pcodes receives the E4M3 bytes of P. */
+VCO_EXPORT void vco_attention_control(const int8_t* q8, const int8_t* k8, const uint8_t* v8,
+                                      const float* qs, const float* ks, const float* vs,
+                                      const uint16_t* means, int block_scale, int64_t BH,
+                                      int64_t nq, int64_t nk, int D, float sm,
+                                      const int64_t* rows, int64_t nrows, float* out,
+                                      uint8_t* pcodes) {
+  attention_rows(q8, k8, v8, qs, ks, vs, means, block_scale, BH, nq, nk, D, sm, rows, nrows,
+                 out, pcodes, 0);
 }

@@ -79,6 +79,7 @@ def _declare(L):
     L.vco_quant_v_channel.argtypes = [P, i32, i64, i64, i32, P, P, P]
     L.vco_quant_v_smooth.argtypes = [P, i32, i64, i64, i32, P, i32, P, P, P]
     L.vco_attention.argtypes = [P, P, P, P, P, P, P, i32, i64, i64, i64, i32, f32, P, i64, P, P]
+    L.vco_attention_control.argtypes = L.vco_attention.argtypes
 
 
 def _ptr(a):
@@ -225,9 +226,10 @@ def prepare_values(v, perm=None, channel_scale: bool = True, dtype: str = "bfloa
 
 def prepare(q, k, v, *, expcast=True, v_smooth=True, clusters=8, iterations=2, sm_scale=None,
             v_scale_mode="channel", dtype="bfloat16"):
-    """State dict of the sageattn_vc contract (reference vc.py:141-170); v is LOGICAL."""
-    if not expcast:
-        raise ValueError("the oracle restates the ExpCast contract only")
+    """State dict of the sageattn_vc contract (reference vc.py:141-170); v is LOGICAL.
+
+    expcast only selects the probability path of ``reference``; the payloads are the same.
+    """
     perm = None
     if v_smooth:
         perm, _, _ = group_values(v, clusters, iterations, dtype)
@@ -241,13 +243,15 @@ def prepare(q, k, v, *, expcast=True, v_smooth=True, clusters=8, iterations=2, s
         means = None
     D = np.asarray(q).shape[-1]
     return {"q": q8, "k": k8, "v": v8, "qs": qs, "ks": ks, "vs": vs, "means": means, "km": km,
-            "expcast": True, "block_values": v_smooth, "output_type": 1 if dtype == "bfloat16" else 0,
+            "expcast": bool(expcast), "block_values": v_smooth, "output_type": 1 if dtype == "bfloat16" else 0,
             "scale": D ** -0.5 if sm_scale is None else sm_scale, "permutation": perm}
 
 
 def reference(state, query_indices=None, return_codes=False):
-    """Decoded-payload oracle (vc_reference.py:20-91) with the exact ExpCast P codes.
+    """Decoded-payload oracle (vc_reference.py:20-91) with the exact P bytes.
 
+    state["expcast"] False selects the Sage FP8 control path (vc_reference.py:58-66):
+    the bytes are then E4M3(exp2(...)) and the mass is the unrounded exp2 sum.
     Returns float32 [B,H,len(ids),D] (and uint8 codes [B,H,len(ids),tiles*128]).
     """
     q8, k8, v8 = state["q"], state["k"], state["v"]
@@ -262,12 +266,13 @@ def reference(state, query_indices=None, return_codes=False):
     block_scale = int(means is not None and vs is not None and vs.ndim == 4)
     out = np.empty((B, H, ids.size, D), np.float32)
     codes = np.empty((B, H, ids.size, tiles * 128), np.uint8) if return_codes else None
-    lib().vco_attention(_ptr(_c(q8, np.int8)), _ptr(_c(k8, np.int8)), _ptr(_c(v8, np.uint8)),
-                        _ptr(_c(state["qs"], np.float32)), _ptr(_c(state["ks"], np.float32)),
-                        _ptr(None if vs is None else _c(vs, np.float32)),
-                        _ptr(None if means is None else _c(means, np.uint16)), block_scale,
-                        B * H, Nq, Nk, D, float(np.float32(state["scale"])), _ptr(ids), ids.size,
-                        _ptr(out), _ptr(codes))
+    fn = lib().vco_attention if state.get("expcast", True) else lib().vco_attention_control
+    fn(_ptr(_c(q8, np.int8)), _ptr(_c(k8, np.int8)), _ptr(_c(v8, np.uint8)),
+       _ptr(_c(state["qs"], np.float32)), _ptr(_c(state["ks"], np.float32)),
+       _ptr(None if vs is None else _c(vs, np.float32)),
+       _ptr(None if means is None else _c(means, np.uint16)), block_scale,
+       B * H, Nq, Nk, D, float(np.float32(state["scale"])), _ptr(ids), ids.size,
+       _ptr(out), _ptr(codes))
     return (out, codes) if return_codes else out
 
 

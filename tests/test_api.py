@@ -84,10 +84,17 @@ def test_forward_prepared_block_scales_dispatch_without_channel_scale(monkeypatc
     assert args[7:9] == (True, True) and kwargs["channel_scale"] is False
 
 
+def test_forward_prepared_control_path_dispatches_expcast_false(monkeypatch):
+    # reference vc.py:173-197: expcast=False selects the Sage FP8 control probabilities
+    calls = []
+    monkeypatch.setattr(api, "_extension", lambda: SimpleNamespace(forward=lambda *a, **k: calls.append((a, k)) or "out"))
+    assert api.forward_prepared({**payload(False), "expcast": False}) == "out"
+    (args, _), = calls
+    assert args[7] is False
+
+
 def test_forward_prepared_rejections(monkeypatch):
     monkeypatch.setattr(api, "_extension", lambda: SimpleNamespace(forward=lambda *a, **k: "out"))
-    with pytest.raises(ValueError, match="expcast=True"):
-        api.forward_prepared({**payload(False), "expcast": False})
     with pytest.raises(ValueError, match="per-channel V scale"):
         api.forward_prepared(payload(True, vs_ndim=4), kernel_mode="vc31_unified")
     with pytest.raises(ValueError, match="v_smooth=False"):

@@ -439,3 +439,69 @@ def test_main_config_all_heads_payloads_and_sampled_rows():
     err, bound = output_bound(got, eout)
     assert np.all(err <= bound), float((err - bound).max())
     assert cosine(got, eout) >= 0.9999
+
+
+CONTROL = [  # B, H, Nq, Nk, D, dtype, V mode
+    (1, 2, 2048, 2048, 128, torch.bfloat16, "none"),
+    (1, 1, 1, 1, 128, torch.bfloat16, "none"),
+    (2, 3, 65, 129, 64, torch.float16, "channel"),
+    (1, 1, 129, 513, 64, torch.bfloat16, "channel"),
+    (1, 2, 257, 385, 128, torch.float16, "channel"),
+    (1, 2, 300, 700, 128, torch.bfloat16, "block"),
+]
+
+
+@pytest.mark.parametrize("case", CONTROL, ids=lambda c: _ids(c[:6]) + "_" + c[6])
+def test_control_path_p_bytes_and_output(case):
+    # expcast=False, the Sage FP8 control path (vc_reference.py:58-66, attn_utils.cuh:355-455):
+    # P = E4M3(exp2(fmaf(base, factor, -m'))) with the hardware exp2, so a byte may move by
+    # one code where p sits next to an E4M3 rounding midpoint (expected a few per 10^6).
+    B, H, Nq, Nk, D, dt, vmode = case
+    _print_case("control path", case)
+    smooth = vmode != "none"
+    q, k, v = make_qkv(B, H, Nq, Nk, D, dt, seed=13, kind="outlier" if smooth else "normal")
+    st = o.prepare(bits(q), bits(k), bits(v), expcast=False, v_smooth=smooth,
+                   v_scale_mode="block" if vmode == "block" else "channel", dtype=dtype_name(dt))
+    assert st["expcast"] is False
+    to = _to_dev
+    v8 = to(logical_to_storage(st["v"], vcx.value_token())).view(torch.float8_e4m3fn)
+    means = to(st["means"]).view(torch.float16) if smooth else None
+    out, pd = vcx.forward(to(st["q"]), to(st["k"]), v8, to(st["qs"]), to(st["ks"]), to(st["vs"]), means,
+                          False, smooth, st["output_type"], st["scale"], channel_scale=vmode != "block",
+                          p_rows=(0, Nq))
+    eout, ecodes = o.reference(st, return_codes=True)
+    diff = np.abs(pd.cpu().numpy().astype(np.int32) - ecodes.astype(np.int32))
+    assert diff.max() <= 1 and np.count_nonzero(diff) <= max(4, diff.size // 100000), np.count_nonzero(diff)
+    got = out.float().cpu().numpy()
+    assert np.isfinite(got).all()
+    err, bound = output_bound(got, eout)
+    assert np.all(err <= bound), float((err - bound).max())
+    assert cosine(got, eout) >= 0.9999
+    out2 = vcx.forward(to(st["q"]), to(st["k"]), v8, to(st["qs"]), to(st["ks"]), to(st["vs"]), means,
+                       False, smooth, st["output_type"], st["scale"], channel_scale=vmode != "block")
+    assert torch.equal(out2, out)
+
+
+def test_control_path_uniform_attention_known_answer_and_end_to_end():
+    # scripts/validate_sage_vc.py:161-182: q = k = 0 gives every key p = 2^8.807 (byte 0x7E),
+    # so the output is the decoded V mean times 448 / 2^8.807f.
+    from sageattention_local import sageattn_vc
+    q = torch.zeros(1, 1, 65, 128, device=DEV, dtype=torch.bfloat16)
+    k = torch.zeros(1, 1, 513, 128, device=DEV, dtype=torch.bfloat16)
+    v = ((torch.arange(513, device=DEV).view(1, 1, 513, 1) / 128 - 2)
+         * torch.linspace(.5, 1.5, 128, device=DEV) + torch.arange(128, device=DEV).remainder(11) * .125)
+    v = v.to(torch.bfloat16).contiguous()
+    _print_case("control path uniform")
+    v8, vs, _ = vcx.prepare_v(v)
+    dec = torch.from_numpy(o.e4m3_decode(storage_to_logical(v8, vcx.value_token())[..., :513]))
+    weight = 448.0 / 2.0 ** float(np.float32(8.807))
+    expected = (dec.double().mean(-1) * vs.cpu().double() * weight).unsqueeze(2).expand(1, 1, 65, 128)
+    out = sageattn_vc(q, k, v, expcast=False, v_smooth=False)
+    torch.testing.assert_close(out.double().cpu(), expected, rtol=0.004, atol=0.004)
+    # random inputs through the public entry against the oracle
+    q, k, v = make_qkv(1, 2, 300, 500, 128, torch.bfloat16, seed=21, kind="outlier")
+    got = sageattn_vc(*(x.to(DEV) for x in (q, k, v)), expcast=False, v_smooth=True).float().cpu().numpy()
+    eout = o.reference(o.prepare(bits(q), bits(k), bits(v), expcast=False, v_smooth=True, dtype="bfloat16"))
+    err, bound = output_bound(got, eout)
+    assert np.all(err <= bound)
+    assert cosine(got, eout) >= 0.9999

@@ -322,24 +322,31 @@ def test_linspace_ids_match_torch():
 
 # ------------------------------------------------------------------ attention oracle known answers
 
-def payload(nq, nk, block_values, dim=64):
-    """The reference's fixed payload (tests/test_sage_vc.py:31-39), ExpCast only."""
+def payload(nq, nk, block_values, dim=64, expcast=True):
+    """The reference's fixed payload (tests/test_sage_vc.py:31-39)."""
     tiles = (nk + 127) // 128
     return {"q": np.zeros((1, 1, nq, dim), np.int8), "k": np.zeros((1, 1, nk, dim), np.int8),
             "v": np.zeros((1, 1, dim, tiles * 128), np.uint8),
             "qs": np.ones((1, 1, ((nq + 63) // 64) * 32), np.float32), "ks": np.ones((1, 1, tiles * 4), np.float32),
             "vs": np.ones((1, 1, tiles, dim), np.float32) if block_values else np.ones((1, 1, dim), np.float32),
             "means": np.zeros((1, 1, tiles, dim), np.uint16) if block_values else None,
-            "expcast": True, "block_values": block_values, "scale": dim ** -0.5}
+            "expcast": expcast, "block_values": block_values, "scale": dim ** -0.5}
 
 
 def f16bits(values):
     return np.asarray(values, np.float16).view(np.uint16)
 
 
-def test_block_mean_restoration_and_tail_weight_known_answer():
-    # tests/test_sage_vc.py:42-49 (expcast=True arm).
-    s = payload(65, 257, True)
+# The Sage FP8 control path (expcast=False) divides FP8(P) by the unrounded exp2 mass, so
+# a single or uniform key carries the weight 448 / 2^8.807f (tests/test_sage_vc.py:62-63,
+# scripts/validate_sage_vc.py:174-178).
+CONTROL_WEIGHT = 448.0 / 2.0 ** float(np.float32(8.807))
+
+
+@pytest.mark.parametrize("expcast", [False, True])
+def test_block_mean_restoration_and_tail_weight_known_answer(expcast):
+    # tests/test_sage_vc.py:42-49
+    s = payload(65, 257, True, expcast=expcast)
     s["means"][0, 0] = f16bits(np.array([1., -2., 6.])[:, None] * np.ones((1, 64)))
     s["vs"][0, 0] = np.array([2., 3., 4.])[:, None]
     out = o.reference(s)
@@ -347,16 +354,18 @@ def test_block_mean_restoration_and_tail_weight_known_answer():
 
 
 @pytest.mark.parametrize("block_values", [False, True])
-def test_single_key_preserves_nonzero_value(block_values):
-    # tests/test_sage_vc.py:52-65 (expcast=True arm: weight 1).
-    s = payload(17, 1, block_values)
+@pytest.mark.parametrize("expcast", [False, True])
+def test_single_key_preserves_nonzero_value(block_values, expcast):
+    # tests/test_sage_vc.py:52-65: weight 1 (ExpCast) or 448 / 2^8.807f (control).
+    s = payload(17, 1, block_values, expcast=expcast)
     data = (np.arange(64) % 9 - 4).astype(np.float32)
     s["v"][0, 0, :, 0] = o.e4m3_encode(data)
     s["vs"][...] = 0.125
     if block_values:
         s["means"][...] = f16bits(2.0)
     out = o.reference(s)
-    expected = (data + (2 if block_values else 0)) * 0.125
+    weight = 1.0 if expcast else CONTROL_WEIGHT
+    expected = (data * weight + (2 if block_values else 0)) * 0.125
     np.testing.assert_allclose(out, np.broadcast_to(expected, out.shape), rtol=1e-6, atol=1e-6)
 
 
@@ -376,10 +385,11 @@ def test_query_sampling_keeps_original_scale_indices():
     np.testing.assert_array_equal(codes, all_codes[:, :, ids])
 
 
-def test_channel_scale_epilogue_matches_expanded_per_tile_scales():
+@pytest.mark.parametrize("expcast", [False, True])
+def test_channel_scale_epilogue_matches_expanded_per_tile_scales(expcast):
     # tests/test_sage_vc.py:82-95
     rng = np.random.default_rng(918)
-    s = payload(65, 257, True)
+    s = payload(65, 257, True, expcast=expcast)
     s["q"][...] = rng.integers(-4, 5, s["q"].shape)
     s["k"][...] = rng.integers(-4, 5, s["k"].shape)
     s["qs"][...] = .1
@@ -392,9 +402,10 @@ def test_channel_scale_epilogue_matches_expanded_per_tile_scales():
     np.testing.assert_allclose(o.reference(channel), o.reference(old), rtol=5e-5, atol=1e-6)
 
 
-def test_shared_scale_nonzero_mean_known_answer():
+@pytest.mark.parametrize("expcast", [False, True])
+def test_shared_scale_nonzero_mean_known_answer(expcast):
     # tests/test_sage_vc.py:98-105
-    s = payload(65, 257, True)
+    s = payload(65, 257, True, expcast=expcast)
     s["vs"] = np.full((1, 1, 64), .25, np.float32)
     s["means"][0, 0] = f16bits(np.array([8., -24., 96.])[:, None] * np.ones((1, 64)))
     out = o.reference(s)
@@ -417,16 +428,72 @@ def test_expcast_codes_agree_with_dense_numpy_formula_one_tile():
     assert np.all(codes[0, 0, :, 35:] == 0)
 
 
-def test_uniform_attention_equals_decoded_value_mean():
-    # scripts/validate_sage_vc.py:161-182 (ExpCast weight 1): q = k = 0.
+@pytest.mark.parametrize("expcast", [False, True])
+def test_uniform_attention_equals_decoded_value_mean(expcast):
+    # scripts/validate_sage_vc.py:161-182: q = k = 0; weight 1 (ExpCast) or 448 / 2^8.807f.
     rng = np.random.default_rng(4)
-    s = payload(65, 513, False)
+    s = payload(65, 513, False, expcast=expcast)
     s["v"][..., :513] = o.e4m3_encode((np.arange(513) / 128 - 2).astype(np.float32))[None, None, None, :]
     s["vs"][...] = np.linspace(0.5, 1.5, 64)
     dec = o.e4m3_decode(s["v"][0, 0, :, :513]).astype(np.float64)
-    expected = dec.mean(-1) * s["vs"][0, 0]
-    np.testing.assert_allclose(o.reference(s)[0, 0], np.broadcast_to(expected, (65, 64)), rtol=1e-6, atol=1e-6)
+    expected = dec.mean(-1) * s["vs"][0, 0] * (1.0 if expcast else CONTROL_WEIGHT)
+    out, codes = o.reference(s, return_codes=True)
+    np.testing.assert_allclose(out[0, 0], np.broadcast_to(expected, (65, 64)), rtol=1e-6, atol=1e-6)
+    # every valid key gets the largest byte of its path, padding keys get 0
+    assert np.all(codes[..., :513] == (120 if expcast else 0x7E)) and np.all(codes[..., 513:] == 0)
     del rng
+
+
+def _control_case(seed, nq=24, nk=300, dim=64):
+    rng = np.random.default_rng(seed)
+    s = payload(nq, nk, False, dim=dim, expcast=False)
+    s["q"][...] = rng.integers(-60, 61, s["q"].shape)
+    s["k"][...] = rng.integers(-60, 61, s["k"].shape)
+    s["qs"][...] = rng.uniform(0.04, 0.09, s["qs"].shape)
+    s["ks"][...] = rng.uniform(0.04, 0.09, s["ks"].shape)
+    s["v"][..., :nk] = o.e4m3_encode(rng.standard_normal((1, 1, dim, nk)).astype(np.float32))
+    s["vs"][...] = rng.uniform(0.5, 2.0, s["vs"].shape)
+    # exact log2-domain logits of the payload: acc * qs[row] * ks[tile, (key%8)//2] * sm * log2 e
+    rows, keys = np.arange(nq), np.arange(nk)
+    acc = s["q"][0, 0].astype(np.float64) @ s["k"][0, 0].T.astype(np.float64)
+    qsc = s["qs"][0, 0][(rows // 16) * 8 + rows % 8].astype(np.float64)
+    ksc = s["ks"][0, 0][(keys // 128) * 4 + (keys % 8) // 2].astype(np.float64)
+    lg2 = acc * qsc[:, None] * ksc[None, :] * (dim ** -0.5) * math.log2(math.e)
+    return s, lg2
+
+
+def test_control_bytes_are_e4m3_of_exp2_with_the_fp8_offset():
+    # attn_utils.cuh:30,378-386,436-452: the running maximum (over the tiles so far) carries
+    # the 8.807 offset, so the largest P of a row is 2^8.807 ~ 448 (byte 0x7E) and
+    # P = E4M3(2^(l - running max l + 8.807)). Checked against float64 logits and torch's
+    # E4M3 cast; the oracle's fp32 FMAs may differ only next to a rounding midpoint.
+    s, lg2 = _control_case(11)
+    _, codes = o.reference(s, return_codes=True)
+    nk = lg2.shape[1]
+    tile_max = np.stack([lg2[:, t:t + 128].max(-1) for t in range(0, nk, 128)], -1)
+    running = np.maximum.accumulate(tile_max, axis=-1)
+    shifted = lg2 - (running[:, np.arange(nk) // 128] - 8.807)
+    want = torch.from_numpy(np.exp2(shifted).astype(np.float32)).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    got = codes[0, 0, :, :lg2.shape[1]]
+    assert np.mean(got == want) > 0.995 and np.abs(got.astype(int) - want).max() <= 1
+    assert np.all(got.max(-1) == 0x7E) and np.all(codes[0, 0, :, lg2.shape[1]:] == 0)
+
+
+def test_control_output_is_a_base_e_softmax_within_the_fp8_bound():
+    # vc_sm90.cu:177 scales by log2 e, so the control path is softmax(logits) @ V with only
+    # the E4M3 rounding of P in the numerator: |E4M3(p) - p| <= 2^-4 p + 2^-10 for P in the
+    # units of the offset maximum (p <= 448; 2^-10 is half the subnormal quantum).
+    s, lg2 = _control_case(12)
+    out = o.reference(s)[0, 0].astype(np.float64)
+    w = np.exp2(lg2 - lg2.max(-1, keepdims=True) + 8.807)
+    dec = o.e4m3_decode(s["v"][0, 0, :, :lg2.shape[1]]).astype(np.float64) * s["vs"][0, 0, :, None]
+    exact = (w @ dec.T) / w.sum(-1, keepdims=True)
+    bound = ((2.0 ** -4 * w + 2.0 ** -10) @ np.abs(dec.T)) / w.sum(-1, keepdims=True)
+    assert np.all(np.abs(out - exact) <= bound + 1e-6)
+    # and a base-2 softmax (no log2 e) is far outside that bound
+    w2 = np.exp2((lg2 - lg2.max(-1, keepdims=True)) / math.log2(math.e))
+    wrong = (w2 @ dec.T) / w2.sum(-1, keepdims=True)
+    assert np.mean(np.abs(wrong - exact) > bound) > 0.3
 
 
 def test_expcast_codes_multi_tile_running_max_and_scale_indices():

@@ -179,8 +179,9 @@ __device__ inline float row_sum(float x) {
 // largest probability is 2^8.807 ~ 448, the E4M3 maximum (sal/csrc/qattn/attn_utils.cuh:30).
 constexpr float kFp8Offset = 8.807f;
 
-template <int D, int VM, bool DUMP, bool EC>
+template <int D, int VM, bool DUMP, int PM>
 struct Wave {
+  static constexpr bool EC = PM != 0;  // ExpCast bytes (1 unfused, 2 folded) or the control path (0)
   static constexpr int DS = D / 64;  // 64-deep QK steps
   static constexpr int CB = D / 16;  // 16-channel output blocks
   static constexpr bool SMOOTH = VM >= 1, BSCALE = VM == 2;
@@ -233,7 +234,67 @@ struct Wave {
     float alpha[2], tmass[2];
 #pragma unroll
     for (int qg = 0; qg < 2; ++qg) {
-      if constexpr (EC) {
+      if constexpr (PM == 2) {
+        // Folded ExpCast encode (the reference's default kernel modes without block
+        // values, sal/csrc/vc/vc_math.cuh:16-111): code = RNE(fmaf(base, gain, bias)) with
+        // gain = RN(scale * A) and bias = fmaf(-m', A, B), unless some row of this 16-row
+        // group has |m'| > 128 or a lane's scale underflows or its gain overflows; then the
+        // whole group takes the unfused code RNE(fmaf(RN(RN(base * scale) - m'), A, B)).
+        float bs[8][4];
+        const float dq = qsv[qg] * ksv;
+        const float scale = LAST ? a.sm : a.sm * dq;
+        float tmax;
+        if constexpr (!LAST) {
+          // float(acc) is exact and monotone: the row maximum is taken on the integers
+          int im = S[qg][0][0];
+#pragma unroll
+          for (int j = 0; j < 8; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              im = im > S[qg][j][r] ? im : S[qg][j][r];
+              bs[j][r] = static_cast<float>(S[qg][j][r]);
+            }
+          tmax = static_cast<float>(im) * scale;
+        } else {
+          float bm = -INFINITY;
+#pragma unroll
+          for (int j = 0; j < 8; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const int64_t key = t * kTile + 16 * j + 8 * (r >> 1) + 2 * G + (r & 1);
+              bs[j][r] = key < a.Nk ? static_cast<float>(S[qg][j][r]) * dq : -INFINITY;
+              bm = fmaxf(bm, bs[j][r]);
+            }
+          tmax = bm * scale;
+        }
+        tmax = row_max(tmax);
+        const float mn = fmaxf(m[qg], tmax);
+        alpha[qg] = __builtin_amdgcn_exp2f((m[qg] - mn) * 1.44269504088896341f);
+        m[qg] = mn;
+        const float gain = scale * kExpA;
+        const bool safe = scale >= 1.1754943508222875e-38f && __builtin_isfinite(gain) && fabsf(mn) <= 128.0f;
+        if (__all(safe)) {
+          const float bias = __builtin_fmaf(-mn, kExpA, kExpB);
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            uint32_t w = 0;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) w = __builtin_amdgcn_cvt_pk_u8_f32(__builtin_fmaf(bs[j][r], gain, bias), r, w);
+            P[qg][j] = static_cast<int>(w);
+          }
+        } else {
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            uint32_t w = 0;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const float lgt = bs[j][r] * scale;
+              w = __builtin_amdgcn_cvt_pk_u8_f32(__builtin_fmaf(lgt - mn, kExpA, kExpB), r, w);
+            }
+            P[qg][j] = static_cast<int>(w);
+          }
+        }
+      } else if constexpr (PM == 1) {
         float lg[8][4];
         float tmax = -INFINITY;
         const float dq = qsv[qg] * ksv;
@@ -399,7 +460,7 @@ struct Wave {
   }
 };
 
-template <int D, int VM, bool DUMP, int OUT, bool EC>
+template <int D, int VM, bool DUMP, int OUT, int PM>
 __global__ __launch_bounds__(kThreadsPerBlock, 2) void attn_kernel(AttnArgs a) {
   typedef TileLoader<D, VM> LD;
   constexpr int KB = kTile * D, VB = D * kTile;
@@ -416,14 +477,14 @@ __global__ __launch_bounds__(kThreadsPerBlock, 2) void attn_kernel(AttnArgs a) {
   const int64_t bh = logical / a.qblocks, qb = logical % a.qblocks;
 
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  Wave<D, VM, DUMP, EC> w;
+  Wave<D, VM, DUMP, PM> w;
   w.G = lane >> 4;
   w.li = lane & 15;
   w.bh_ = bh;
   // Lane-constant LDS offsets.
   const int kr = 8 * ((w.li & 3) >> 1) + 2 * (w.li >> 2) + (w.li & 1);
 #pragma unroll
-  for (int ds = 0; ds < Wave<D, VM, DUMP, EC>::DS; ++ds)
+  for (int ds = 0; ds < Wave<D, VM, DUMP, PM>::DS; ++ds)
     w.koff[ds] = kr * D + ((((D == 128) ? 4 * ds : 0) + w.G) ^ swz_k<D>(kr)) * 16;
 #pragma unroll
   for (int h = 0; h < 2; ++h) w.voff[h] = w.li * kTile + (((2 * w.G + h) ^ swz_v(w.li)) * 16);
@@ -436,14 +497,14 @@ __global__ __launch_bounds__(kThreadsPerBlock, 2) void attn_kernel(AttnArgs a) {
     const int64_t si = (r / 16) * 8 + r % 8;
     w.qsv[qg] = si < a.qs_len ? a.qs[bh * a.qs_len + si] : 1.0f;
 #pragma unroll
-    for (int ds = 0; ds < Wave<D, VM, DUMP, EC>::DS; ++ds) {
+    for (int ds = 0; ds < Wave<D, VM, DUMP, PM>::DS; ++ds) {
       if (r < a.Nq) w.qf[qg][ds] = *reinterpret_cast<const v4i*>(a.q8 + (bh * a.Nq + r) * D + ds * 64 + w.G * 16);
       else w.qf[qg][ds] = v4i{0, 0, 0, 0};
     }
     w.m[qg] = -5000000.0f;
     w.den[qg] = 0.0f;
 #pragma unroll
-    for (int cb = 0; cb < Wave<D, VM, DUMP, EC>::CB; ++cb) w.O[qg][cb] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int cb = 0; cb < Wave<D, VM, DUMP, PM>::CB; ++cb) w.O[qg][cb] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
   }
 
   LD ld;
@@ -482,10 +543,10 @@ __global__ __launch_bounds__(kThreadsPerBlock, 2) void attn_kernel(AttnArgs a) {
     const float inv = 1.0f / w.den[qg];
     uint16_t* out = static_cast<uint16_t*>(a.out) + b * a.osb + h * a.osh + w.row[qg] * a.osn;
 #pragma unroll
-    for (int cb = 0; cb < Wave<D, VM, DUMP, EC>::CB; ++cb) {
+    for (int cb = 0; cb < Wave<D, VM, DUMP, PM>::CB; ++cb) {
       const int ch = 16 * cb + 4 * w.G;
       // per-channel V scale (per-block scales were applied tile by tile)
-      const float4 sc = Wave<D, VM, DUMP, EC>::BSCALE ? make_float4(1.0f, 1.0f, 1.0f, 1.0f)
+      const float4 sc = Wave<D, VM, DUMP, PM>::BSCALE ? make_float4(1.0f, 1.0f, 1.0f, 1.0f)
                                                   : *reinterpret_cast<const float4*>(a.vs + bh * D + ch);
       const float y0 = w.O[qg][cb][0] * inv * sc.x, y1 = w.O[qg][cb][1] * inv * sc.y;
       const float y2 = w.O[qg][cb][2] * inv * sc.z, y3 = w.O[qg][cb][3] * inv * sc.w;
@@ -504,75 +565,86 @@ __global__ __launch_bounds__(kThreadsPerBlock, 2) void attn_kernel(AttnArgs a) {
 
 // Explicit instantiation of every launch variant: hipcc's host pass otherwise
 // emitted the kernel handle of only the first variant named in each ternary.
-template __global__ void attn_kernel<64, 0, false, 0, true>(AttnArgs);
-template __global__ void attn_kernel<64, 0, false, 1, true>(AttnArgs);
-template __global__ void attn_kernel<64, 0, true, 0, true>(AttnArgs);
-template __global__ void attn_kernel<64, 0, true, 1, true>(AttnArgs);
-template __global__ void attn_kernel<64, 1, false, 0, true>(AttnArgs);
-template __global__ void attn_kernel<64, 1, false, 1, true>(AttnArgs);
-template __global__ void attn_kernel<64, 1, true, 0, true>(AttnArgs);
-template __global__ void attn_kernel<64, 1, true, 1, true>(AttnArgs);
-template __global__ void attn_kernel<64, 2, false, 0, true>(AttnArgs);
-template __global__ void attn_kernel<64, 2, false, 1, true>(AttnArgs);
-template __global__ void attn_kernel<64, 2, true, 0, true>(AttnArgs);
-template __global__ void attn_kernel<64, 2, true, 1, true>(AttnArgs);
-template __global__ void attn_kernel<128, 0, false, 0, true>(AttnArgs);
-template __global__ void attn_kernel<128, 0, false, 1, true>(AttnArgs);
-template __global__ void attn_kernel<128, 0, true, 0, true>(AttnArgs);
-template __global__ void attn_kernel<128, 0, true, 1, true>(AttnArgs);
-template __global__ void attn_kernel<128, 1, false, 0, true>(AttnArgs);
-template __global__ void attn_kernel<128, 1, false, 1, true>(AttnArgs);
-template __global__ void attn_kernel<128, 1, true, 0, true>(AttnArgs);
-template __global__ void attn_kernel<128, 1, true, 1, true>(AttnArgs);
-template __global__ void attn_kernel<128, 2, false, 0, true>(AttnArgs);
-template __global__ void attn_kernel<128, 2, false, 1, true>(AttnArgs);
-template __global__ void attn_kernel<128, 2, true, 0, true>(AttnArgs);
-template __global__ void attn_kernel<128, 2, true, 1, true>(AttnArgs);
-template __global__ void attn_kernel<64, 0, false, 0, false>(AttnArgs);
-template __global__ void attn_kernel<64, 0, false, 1, false>(AttnArgs);
-template __global__ void attn_kernel<64, 0, true, 0, false>(AttnArgs);
-template __global__ void attn_kernel<64, 0, true, 1, false>(AttnArgs);
-template __global__ void attn_kernel<64, 1, false, 0, false>(AttnArgs);
-template __global__ void attn_kernel<64, 1, false, 1, false>(AttnArgs);
-template __global__ void attn_kernel<64, 1, true, 0, false>(AttnArgs);
-template __global__ void attn_kernel<64, 1, true, 1, false>(AttnArgs);
-template __global__ void attn_kernel<64, 2, false, 0, false>(AttnArgs);
-template __global__ void attn_kernel<64, 2, false, 1, false>(AttnArgs);
-template __global__ void attn_kernel<64, 2, true, 0, false>(AttnArgs);
-template __global__ void attn_kernel<64, 2, true, 1, false>(AttnArgs);
-template __global__ void attn_kernel<128, 0, false, 0, false>(AttnArgs);
-template __global__ void attn_kernel<128, 0, false, 1, false>(AttnArgs);
-template __global__ void attn_kernel<128, 0, true, 0, false>(AttnArgs);
-template __global__ void attn_kernel<128, 0, true, 1, false>(AttnArgs);
-template __global__ void attn_kernel<128, 1, false, 0, false>(AttnArgs);
-template __global__ void attn_kernel<128, 1, false, 1, false>(AttnArgs);
-template __global__ void attn_kernel<128, 1, true, 0, false>(AttnArgs);
-template __global__ void attn_kernel<128, 1, true, 1, false>(AttnArgs);
-template __global__ void attn_kernel<128, 2, false, 0, false>(AttnArgs);
-template __global__ void attn_kernel<128, 2, false, 1, false>(AttnArgs);
-template __global__ void attn_kernel<128, 2, true, 0, false>(AttnArgs);
-template __global__ void attn_kernel<128, 2, true, 1, false>(AttnArgs);
+template __global__ void attn_kernel<64, 0, false, 0, 2>(AttnArgs);
+template __global__ void attn_kernel<64, 0, false, 1, 2>(AttnArgs);
+template __global__ void attn_kernel<64, 0, true, 0, 2>(AttnArgs);
+template __global__ void attn_kernel<64, 0, true, 1, 2>(AttnArgs);
+template __global__ void attn_kernel<128, 0, false, 0, 2>(AttnArgs);
+template __global__ void attn_kernel<128, 0, false, 1, 2>(AttnArgs);
+template __global__ void attn_kernel<128, 0, true, 0, 2>(AttnArgs);
+template __global__ void attn_kernel<128, 0, true, 1, 2>(AttnArgs);
+template __global__ void attn_kernel<64, 0, false, 0, 1>(AttnArgs);
+template __global__ void attn_kernel<64, 0, false, 1, 1>(AttnArgs);
+template __global__ void attn_kernel<64, 0, true, 0, 1>(AttnArgs);
+template __global__ void attn_kernel<64, 0, true, 1, 1>(AttnArgs);
+template __global__ void attn_kernel<64, 1, false, 0, 1>(AttnArgs);
+template __global__ void attn_kernel<64, 1, false, 1, 1>(AttnArgs);
+template __global__ void attn_kernel<64, 1, true, 0, 1>(AttnArgs);
+template __global__ void attn_kernel<64, 1, true, 1, 1>(AttnArgs);
+template __global__ void attn_kernel<64, 2, false, 0, 1>(AttnArgs);
+template __global__ void attn_kernel<64, 2, false, 1, 1>(AttnArgs);
+template __global__ void attn_kernel<64, 2, true, 0, 1>(AttnArgs);
+template __global__ void attn_kernel<64, 2, true, 1, 1>(AttnArgs);
+template __global__ void attn_kernel<128, 0, false, 0, 1>(AttnArgs);
+template __global__ void attn_kernel<128, 0, false, 1, 1>(AttnArgs);
+template __global__ void attn_kernel<128, 0, true, 0, 1>(AttnArgs);
+template __global__ void attn_kernel<128, 0, true, 1, 1>(AttnArgs);
+template __global__ void attn_kernel<128, 1, false, 0, 1>(AttnArgs);
+template __global__ void attn_kernel<128, 1, false, 1, 1>(AttnArgs);
+template __global__ void attn_kernel<128, 1, true, 0, 1>(AttnArgs);
+template __global__ void attn_kernel<128, 1, true, 1, 1>(AttnArgs);
+template __global__ void attn_kernel<128, 2, false, 0, 1>(AttnArgs);
+template __global__ void attn_kernel<128, 2, false, 1, 1>(AttnArgs);
+template __global__ void attn_kernel<128, 2, true, 0, 1>(AttnArgs);
+template __global__ void attn_kernel<128, 2, true, 1, 1>(AttnArgs);
+template __global__ void attn_kernel<64, 0, false, 0, 0>(AttnArgs);
+template __global__ void attn_kernel<64, 0, false, 1, 0>(AttnArgs);
+template __global__ void attn_kernel<64, 0, true, 0, 0>(AttnArgs);
+template __global__ void attn_kernel<64, 0, true, 1, 0>(AttnArgs);
+template __global__ void attn_kernel<64, 1, false, 0, 0>(AttnArgs);
+template __global__ void attn_kernel<64, 1, false, 1, 0>(AttnArgs);
+template __global__ void attn_kernel<64, 1, true, 0, 0>(AttnArgs);
+template __global__ void attn_kernel<64, 1, true, 1, 0>(AttnArgs);
+template __global__ void attn_kernel<64, 2, false, 0, 0>(AttnArgs);
+template __global__ void attn_kernel<64, 2, false, 1, 0>(AttnArgs);
+template __global__ void attn_kernel<64, 2, true, 0, 0>(AttnArgs);
+template __global__ void attn_kernel<64, 2, true, 1, 0>(AttnArgs);
+template __global__ void attn_kernel<128, 0, false, 0, 0>(AttnArgs);
+template __global__ void attn_kernel<128, 0, false, 1, 0>(AttnArgs);
+template __global__ void attn_kernel<128, 0, true, 0, 0>(AttnArgs);
+template __global__ void attn_kernel<128, 0, true, 1, 0>(AttnArgs);
+template __global__ void attn_kernel<128, 1, false, 0, 0>(AttnArgs);
+template __global__ void attn_kernel<128, 1, false, 1, 0>(AttnArgs);
+template __global__ void attn_kernel<128, 1, true, 0, 0>(AttnArgs);
+template __global__ void attn_kernel<128, 1, true, 1, 0>(AttnArgs);
+template __global__ void attn_kernel<128, 2, false, 0, 0>(AttnArgs);
+template __global__ void attn_kernel<128, 2, false, 1, 0>(AttnArgs);
+template __global__ void attn_kernel<128, 2, true, 0, 0>(AttnArgs);
+template __global__ void attn_kernel<128, 2, true, 1, 0>(AttnArgs);
 
-template <int D, int VM, bool DUMP, int OUT, bool EC>
+template <int D, int VM, bool DUMP, int OUT, int PM>
 int launch(const AttnArgs& a, int64_t nblocks, hipStream_t st) {
-  attn_kernel<D, VM, DUMP, OUT, EC><<<dim3(static_cast<unsigned>(nblocks)), kThreadsPerBlock, 0, st>>>(a);
+  attn_kernel<D, VM, DUMP, OUT, PM><<<dim3(static_cast<unsigned>(nblocks)), kThreadsPerBlock, 0, st>>>(a);
   return check_launch("attn_kernel");
 }
 
-template <int D, int VM, bool EC>
+template <int D, int VM, int PM>
 int launch_out(const AttnArgs& a, int64_t nblocks, bool dump, int out_dtype, hipStream_t st) {
   if (dump) {
-    return out_dtype == VCX_BFLOAT16 ? launch<D, VM, true, VCX_BFLOAT16, EC>(a, nblocks, st)
-                                     : launch<D, VM, true, VCX_FLOAT16, EC>(a, nblocks, st);
+    return out_dtype == VCX_BFLOAT16 ? launch<D, VM, true, VCX_BFLOAT16, PM>(a, nblocks, st)
+                                     : launch<D, VM, true, VCX_FLOAT16, PM>(a, nblocks, st);
   }
-  return out_dtype == VCX_BFLOAT16 ? launch<D, VM, false, VCX_BFLOAT16, EC>(a, nblocks, st)
-                                   : launch<D, VM, false, VCX_FLOAT16, EC>(a, nblocks, st);
+  return out_dtype == VCX_BFLOAT16 ? launch<D, VM, false, VCX_BFLOAT16, PM>(a, nblocks, st)
+                                   : launch<D, VM, false, VCX_FLOAT16, PM>(a, nblocks, st);
 }
 
 template <int D, int VM>
-int launch_mode(const AttnArgs& a, int64_t nblocks, bool dump, int out_dtype, bool expcast, hipStream_t st) {
-  return expcast ? launch_out<D, VM, true>(a, nblocks, dump, out_dtype, st)
-                 : launch_out<D, VM, false>(a, nblocks, dump, out_dtype, st);
+int launch_mode(const AttnArgs& a, int64_t nblocks, bool dump, int out_dtype, int mode, hipStream_t st) {
+  if constexpr (VM == 0) {
+    if (mode == 2) return launch_out<D, VM, 2>(a, nblocks, dump, out_dtype, st);
+  }
+  return mode == 1 ? launch_out<D, VM, 1>(a, nblocks, dump, out_dtype, st)
+                   : launch_out<D, VM, 0>(a, nblocks, dump, out_dtype, st);
 }
 
 }  // namespace
@@ -591,7 +663,8 @@ extern "C" int vcx_attention_fwd(const int8_t* q8, const int8_t* k8, const uint8
   VCX_REQUIRE(B * H <= 65535, "B*H exceeds 65535");
   VCX_REQUIRE(Nq < (int64_t(1) << 30) && Nk < (int64_t(1) << 30), "sequence too long");
   VCX_REQUIRE(cdiv(Nk, kTile) * kTile * D < (int64_t(1) << 31), "K/V payload of one head must be below 2 GiB");
-  VCX_REQUIRE(expcast == 0 || expcast == 1, "expcast must be 0 or 1");
+  VCX_REQUIRE(expcast >= 0 && expcast <= 2, "expcast must be 0, 1 or 2");
+  VCX_REQUIRE(expcast != 2 || !block_values, "the folded ExpCast encode (expcast = 2) is defined without block values");
   VCX_REQUIRE(block_values || channel_scale, "per-block V scales require block values (smoothing)");
   VCX_REQUIRE(out_dtype == VCX_FLOAT16 || out_dtype == VCX_BFLOAT16, "out_dtype must be float16 or bfloat16");
   VCX_REQUIRE(std::isfinite(sm_scale) && sm_scale > 0.0f, "sm_scale must be positive and finite FP32");
@@ -612,21 +685,20 @@ extern "C" int vcx_attention_fwd(const int8_t* q8, const int8_t* k8, const uint8
   a.H = H; a.Nq = Nq; a.Nk = Nk; a.tiles = cdiv(Nk, kTile); a.qblocks = cdiv(Nq, kRowsPerBlock);
   a.qs_len = cdiv(Nq, 64) * 32;
   // The control path works in the log2 domain: RN(sm * RN(log2 e)) (sal/csrc/vc/vc_sm90.cu:177).
-  a.sm = expcast ? sm_scale : sm_scale * 1.4426950408889634f;
+  a.sm = expcast != 0 ? sm_scale : sm_scale * 1.4426950408889634f;
   a.pdump = p_dump; a.prow0 = p_row_begin; a.prow1 = p_row_end;
   const int64_t nblocks = B * H * a.qblocks;
   VCX_REQUIRE(nblocks < (int64_t(1) << 31), "too many blocks");
   hipStream_t st = static_cast<hipStream_t>(stream);
   const bool dump = p_dump != nullptr;
-  const bool ec = expcast == 1;
   if (D == 128) {
-    if (!block_values) return launch_mode<128, 0>(a, nblocks, dump, out_dtype, ec, st);
-    return channel_scale ? launch_mode<128, 1>(a, nblocks, dump, out_dtype, ec, st)
-                         : launch_mode<128, 2>(a, nblocks, dump, out_dtype, ec, st);
+    if (!block_values) return launch_mode<128, 0>(a, nblocks, dump, out_dtype, expcast, st);
+    return channel_scale ? launch_mode<128, 1>(a, nblocks, dump, out_dtype, expcast, st)
+                         : launch_mode<128, 2>(a, nblocks, dump, out_dtype, expcast, st);
   }
-  if (!block_values) return launch_mode<64, 0>(a, nblocks, dump, out_dtype, ec, st);
-  return channel_scale ? launch_mode<64, 1>(a, nblocks, dump, out_dtype, ec, st)
-                       : launch_mode<64, 2>(a, nblocks, dump, out_dtype, ec, st);
+  if (!block_values) return launch_mode<64, 0>(a, nblocks, dump, out_dtype, expcast, st);
+  return channel_scale ? launch_mode<64, 1>(a, nblocks, dump, out_dtype, expcast, st)
+                       : launch_mode<64, 2>(a, nblocks, dump, out_dtype, expcast, st);
 }
 
 extern "C" int vcx_kernel_resources(int64_t D, int block_values, int64_t* out) {
@@ -634,10 +706,10 @@ extern "C" int vcx_kernel_resources(int64_t D, int block_values, int64_t* out) {
   VCX_REQUIRE(D == 64 || D == 128, "D must be 64 or 128");
   hipFuncAttributes attr{};
   const void* fn;
-  if (D == 128) fn = block_values ? reinterpret_cast<const void*>(&attn_kernel<128, 1, false, VCX_BFLOAT16, true>)
-                                  : reinterpret_cast<const void*>(&attn_kernel<128, 0, false, VCX_BFLOAT16, true>);
-  else fn = block_values ? reinterpret_cast<const void*>(&attn_kernel<64, 1, false, VCX_BFLOAT16, true>)
-                         : reinterpret_cast<const void*>(&attn_kernel<64, 0, false, VCX_BFLOAT16, true>);
+  if (D == 128) fn = block_values ? reinterpret_cast<const void*>(&attn_kernel<128, 1, false, VCX_BFLOAT16, 1>)
+                                  : reinterpret_cast<const void*>(&attn_kernel<128, 0, false, VCX_BFLOAT16, 2>);
+  else fn = block_values ? reinterpret_cast<const void*>(&attn_kernel<64, 1, false, VCX_BFLOAT16, 1>)
+                         : reinterpret_cast<const void*>(&attn_kernel<64, 0, false, VCX_BFLOAT16, 2>);
   hipError_t e = hipFuncGetAttributes(&attr, fn);
   if (e != hipSuccess) return fail(VCX_EHIP, "hipFuncGetAttributes: %s", hipGetErrorString(e));
   out[0] = attr.numRegs;

@@ -12,8 +12,11 @@ Differences a caller can observe, all deliberate:
 * Any current HIP stream is accepted (the reference required the default
   stream because an upstream kernel used it); all work is enqueued on it.
 * ``kernel_mode`` accepts the reference's documented mode names with the same
-  compatibility rules, but every mode runs the single gfx950 kernel: the
-  names select Hopper WGMMA/TMA schedules that have no MI355X counterpart.
+  compatibility rules. Every mode runs the single gfx950 kernel (the names
+  select Hopper WGMMA/TMA schedules that have no MI355X counterpart); the
+  numerics follow the mode as in the reference: without block values the
+  default and vc12..vc15 modes use the folded ExpCast encode, vc4..vc11 the
+  unfused one (``AFFINE_MODES``).
 * The prepared ``v`` payload is stored in the gfx950 tile order
   (``vcx.value_token``), not Sage's 16-token permutation.
 * ``expcast=False`` runs the Sage FP8 control path (E4M3 probabilities from
@@ -138,6 +141,12 @@ def prepare(q, k, v, *, expcast=True, v_smooth=True, clusters=8, iterations=2, s
             "v_layout": "gfx950_tile128"}
 
 
+# Modes whose reference kernels fold RN(score*scale), the subtraction and the ExpCast map
+# into one FMA (affine_probability, reference vc.py:187-189; FoldAffine, vc_sm90.cu:1009).
+# The reference uses the folded encode only for ExpCast without block values.
+AFFINE_MODES = ("optimized", "vc15", "vc14", "vc13_overlap", "vc13_serial", "vc12")
+
+
 def forward_prepared(state, *, kernel_mode="optimized", out=None):
     """Fused kernel on a prepared state (reference vc.py:173-197)."""
     channel = not (state["block_values"] and state["vs"].ndim == 4)
@@ -145,9 +154,11 @@ def forward_prepared(state, *, kernel_mode="optimized", out=None):
                 expcast=state["expcast"], dim=state["q"].shape[-1], v_scale_mode="channel" if channel else "block")
     if kernel_mode in UNIFIED_MODES and state["vs"].ndim != 3:
         raise ValueError("vc31/vc32 require per-channel V scale")
+    mode = "vc15" if kernel_mode in SAGE_LAYOUT_MODES else kernel_mode
+    affine = bool(state["expcast"]) and not state["block_values"] and mode in AFFINE_MODES
     return _extension().forward(state["q"], state["k"], state["v"], state["qs"], state["ks"], state["vs"],
                                 state["means"], state["expcast"], state["block_values"], state["output_type"],
-                                state["scale"], channel_scale=channel, out=out)
+                                state["scale"], channel_scale=channel, affine=affine, out=out)
 
 
 @torch.no_grad()
@@ -197,7 +208,9 @@ def sage_vc_build_info():
             "algorithm": "Sage per-thread INT8 QK + VC block V residual/mean + ExpCast",
             "qk_hadamard": False, "v_block": 128, "mean_dtype": "float16",
             "clustering": "<=8 clusters, Lloyd with fp64 distances, stable counting sort; fresh every call",
-            "expcast_probability": "exact FP32 RN multiply/subtract + single-rounding FMA + saturating RNE byte",
+            "expcast_probability": "without block values (default modes): folded encode RNE(fmaf(score, RN(scale*A), "
+                                   "fmaf(-m, A, B))) with the 16-row |m| <= 128 fallback; otherwise exact FP32 RN "
+                                   "multiply/subtract + single-rounding FMA + saturating RNE byte",
             "control_probability": "log2-domain FMA with the 8.807 offset, hardware exp2, RNE E4M3; unrounded mass",
             "mass": "FP8 MFMA row sum with an all-ones operand (same accumulation as PV)",
             "v_layout": "gfx950_tile128", "kernel_modes": list(BASE_MODES) + list(SAGE_LAYOUT_MODES),

@@ -193,8 +193,9 @@ def attention(q, k, v, config=None, *, cache=None, step=0, total_steps=1, reques
 
     q8, qs, k8, ks, km = vcx.prepare_qk(q, k, pi)
     v8, vs, means = vcx.prepare_v(v, pi, smooth=active, channel_scale=True)
+    # The ExpCast encode of the reference's default kernel mode: folded without block values.
     out = vcx.forward(q8, k8, v8, qs, ks, vs, means, cfg.expcast, active, 0 if q.dtype == torch.float16 else 1,
-                      scale)
+                      scale, affine=cfg.expcast and not active)
     return out, {
         "backend": "hip",
         "smoothing_active": active,

@@ -213,12 +213,18 @@ def prepare_v(v, perm=None, smooth: bool = False, channel_scale: bool = True):
 
 @torch.no_grad()
 def forward(q8, k8, v8, qs, ks, vs, means, expcast: bool, block_values: bool, output_type: int, scale: float,
-            *, channel_scale: bool = True, out=None, p_rows=None):
+            *, channel_scale: bool = True, affine: bool = False, out=None, p_rows=None):
     """Fused attention on prepared payloads -> out [B,H,Nq,D] (fp16 if output_type == 0 else bf16).
 
+    expcast=False runs the Sage FP8 control probabilities. affine=True (ExpCast without
+    block values only) selects the folded encode of the reference's default kernel modes
+    (vc12..vc15, "optimized"); affine=False the unfused encode (vc4..vc11 and every
+    block-value launch).
     p_rows=(begin, end) additionally returns the E4M3 P bytes of those query rows
     (uint8 [B,H,end-begin,tiles*128], logical key order) from the diagnostic variant.
     """
+    if affine and (not expcast or block_values):
+        raise VcxError("the folded ExpCast encode applies to ExpCast without block values")
     dev = _require_device(q8, k8, v8, qs, ks, vs)
     B, H, Nq, D = q8.shape
     Nk = k8.shape[2]
@@ -250,7 +256,8 @@ def forward(q8, k8, v8, qs, ks, vs, means, expcast: bool, block_values: bool, ou
         r0, r1 = int(p_rows[0]), int(p_rows[1])
         pd = torch.zeros((B, H, max(r1 - r0, 0), tiles * 128), dtype=torch.uint8, device=dev)
     _check(lib().vcx_attention_fwd(_ptr(q8), _ptr(k8), _ptr(v8), _ptr(qs), _ptr(ks), _ptr(vs),
-                                   _ptr(means) if block_values else None, B, H, Nq, Nk, D, int(expcast),
+                                   _ptr(means) if block_values else None, B, H, Nq, Nk, D,
+                                   (2 if affine else 1) if expcast else 0,
                                    int(block_values), int(channel_scale), float(scale), 1 if output_type else 0,
                                    _ptr(out), osb, osh, osn, _ptr(pd), r0, r1, _stream(dev)),
            "vcx_attention_fwd")

@@ -502,6 +502,73 @@ VCO_EXPORT void vco_quant_v_smooth(const uint16_t* v, int dtype, int64_t BH, int
 /* Attention: P bytes (exact) and decoded-payload output (fp64 accumulate) */
 /* ------------------------------------------------------------------ */
 
+/* RN-even to an unsigned byte with saturation to [0, 255] (NaN -> 0): the byte
+ * conversion of the folded ExpCast encode (sal/csrc/vc/expcast.cuh:37-48,58-66). */
+static inline uint8_t cvt_u8_rne(float u) {
+  if (u != u) return 0;
+  u = fmaxf(0.0f, fminf(255.0f, u));
+  return (uint8_t)rintf(u);
+}
+
+/* Folded ExpCast encode of the reference's default kernel modes (vc12..vc15, "optimized")
+ * without block values: sal/csrc/vc/vc_math.cuh:16-111, vc_probability_prepare with
+ * FoldAffine. Per 16-row group and tile (one Hopper warp: 16 rows x 4 key groups),
+ *   safe = every thread's scale >= FLT_MIN, gain = RN(scale * 8 log2 e) finite and
+ *          |m'| <= 128 for every row of the group (m' after this tile's update);
+ * a safe group encodes code = sat_u8(RNE(fmaf(base, gain, fmaf(-m', A, B)))), an unsafe
+ * one falls back to the unfused code of every row. Rows past nq (zero Q rows in the
+ * reference's tile) take part with acc = 0. Returns safe[BH][ceil(nq/16)][tiles] for the
+ * groups that hold a requested row (others are left 0). */
+static uint8_t* affine_safe_flags(const int8_t* q8, const int8_t* k8, const float* qs,
+                                  const float* ks, int64_t BH, int64_t nq, int64_t nk, int D,
+                                  float sm, const int64_t* rows, int64_t nrows) {
+  const int64_t tiles = (nk + 127) / 128, groups = (nq + 15) / 16, qsn = (nq + 63) / 64 * 32;
+  uint8_t* flags = (uint8_t*)calloc((size_t)(BH * groups * tiles), 1);
+  uint8_t* wanted = (uint8_t*)calloc((size_t)groups, 1);
+  for (int64_t i = 0; i < nrows; ++i) wanted[rows[i] / 16] = 1;
+#pragma omp parallel for schedule(dynamic) collapse(2)
+  for (int64_t h = 0; h < BH; ++h) {
+    for (int64_t g = 0; g < groups; ++g) {
+      if (!wanted[g]) continue;
+      float m[16];
+      for (int r = 0; r < 16; ++r) m[r] = -5000000.0f;
+      for (int64_t t = 0; t < tiles; ++t) {
+        const int last = t == tiles - 1;
+        int ok = 1;
+        for (int rr = 0; rr < 16; ++rr) {
+          const int64_t r = g * 16 + rr;
+          const float qscale = qs[h * qsn + (r / 16) * 8 + r % 8];
+          float tmax = -INFINITY;
+          for (int gk = 0; gk < 4; ++gk) {
+            const float scale = last ? sm : sm * (qscale * ks[h * tiles * 4 + t * 4 + gk]);
+            const float gain = scale * kExpA;
+            if (!(scale >= 1.1754943508222875e-38f) || !isfinite(gain)) ok = 0;
+          }
+          for (int i = 0; i < 128; ++i) {
+            const int64_t key = t * 128 + i;
+            if (key >= nk) continue;
+            int32_t acc = 0;
+            if (r < nq) {
+              const int8_t* qrow = q8 + (h * nq + r) * D;
+              const int8_t* krow = k8 + (h * nk + key) * D;
+              for (int d = 0; d < D; ++d) acc += (int32_t)qrow[d] * (int32_t)krow[d];
+            }
+            const float dq = qscale * ks[h * tiles * 4 + t * 4 + (i % 8) / 2];
+            const float f = (float)acc;
+            const float lg = last ? (f * dq) * sm : f * (sm * dq);
+            tmax = fmaxf(tmax, lg);
+          }
+          m[rr] = fmaxf(m[rr], tmax);
+          if (!(fabsf(m[rr]) <= 128.0f)) ok = 0;
+        }
+        flags[(h * groups + g) * tiles + t] = (uint8_t)ok;
+      }
+    }
+  }
+  free(wanted);
+  return flags;
+}
+
 /* For each selected query row, stream the 128-key tiles in order:
  *   dq = RN(qs_row * ks_group)
  *   tiles before the last: logit = RN(float(acc) * RN(sm * dq))
@@ -536,12 +603,14 @@ static void attention_rows(const int8_t* q8, const int8_t* k8, const uint8_t* v8
                            const float* qs, const float* ks, const float* vs,
                            const uint16_t* means, int block_scale, int64_t BH, int64_t nq,
                            int64_t nk, int D, float sm, const int64_t* rows, int64_t nrows,
-                           float* out, uint8_t* pcodes, int expcast) {
+                           float* out, uint8_t* pcodes, int mode) {
+  const int expcast = mode != 0, affine = mode == 2;
   int64_t tiles = (nk + 127) / 128, npad = tiles * 128;
   int64_t qsn = (nq + 63) / 64 * 32;
   float* vdec = (float*)malloc(sizeof(float) * 256);  /* decode table */
   for (int c = 0; c < 256; ++c) vdec[c] = vco_e4m3_decode((uint8_t)c);
   const float s = expcast ? sm : sm * 1.4426950408889634f;
+  uint8_t* safe = affine ? affine_safe_flags(q8, k8, qs, ks, BH, nq, nk, D, sm, rows, nrows) : NULL;
 #pragma omp parallel for schedule(dynamic) collapse(2)
   for (int64_t h = 0; h < BH; ++h) {
     for (int64_t ri = 0; ri < nrows; ++ri) {
@@ -551,7 +620,7 @@ static void attention_rows(const int8_t* q8, const int8_t* k8, const uint8_t* v8
       float m = -5000000.0f;
       double den = 0.0;
       double o[128];
-      float logit[128], factor[128];
+      float logit[128], factor[128], abase[128];
       uint8_t code[128];
       for (int d = 0; d < D; ++d) o[d] = 0.0;
       for (int64_t t = 0; t < tiles; ++t) {
@@ -559,7 +628,7 @@ static void attention_rows(const int8_t* q8, const int8_t* k8, const uint8_t* v8
         float tmax = -INFINITY;
         for (int i = 0; i < 128; ++i) {
           int64_t key = t * 128 + i;
-          if (key >= nk) { logit[i] = -INFINITY; factor[i] = 1.0f; continue; }
+          if (key >= nk) { logit[i] = -INFINITY; abase[i] = -INFINITY; factor[i] = 1.0f; continue; }
           const int8_t* krow = k8 + (h * nk + key) * D;
           int32_t acc = 0;
           for (int d = 0; d < D; ++d) acc += (int32_t)qrow[d] * (int32_t)krow[d];
@@ -571,6 +640,8 @@ static void attention_rows(const int8_t* q8, const int8_t* k8, const uint8_t* v8
           if (expcast) {
             float lg = base * fac;
             logit[i] = lg;
+            abase[i] = base;
+            factor[i] = fac;
             tmax = fmaxf(tmax, lg);
           } else {
             logit[i] = base;  /* the control path keeps base and factor apart */
@@ -587,8 +658,14 @@ static void attention_rows(const int8_t* q8, const int8_t* k8, const uint8_t* v8
         for (int i = 0; i < 128; ++i) {
           double p;
           if (expcast) {
-            float shifted = logit[i] - mnew;
-            code[i] = vco_expcast_code(shifted);
+            if (affine && safe[(h * ((nq + 15) / 16) + r / 16) * tiles + t]) {
+              const float gain = factor[i] * kExpA;
+              const float bias = fmaf(-mnew, kExpA, kExpB);
+              code[i] = cvt_u8_rne(fmaf(abase[i], gain, bias));
+            } else {
+              float shifted = logit[i] - mnew;
+              code[i] = vco_expcast_code(shifted);
+            }
             p = (double)vdec[code[i]];
             mass += p;
           } else {
@@ -620,6 +697,7 @@ static void attention_rows(const int8_t* q8, const int8_t* k8, const uint8_t* v8
     }
   }
   free(vdec);
+  free(safe);
 }
 
 VCO_EXPORT void vco_attention(const int8_t* q8, const int8_t* k8, const uint8_t* v8,
@@ -629,6 +707,17 @@ VCO_EXPORT void vco_attention(const int8_t* q8, const int8_t* k8, const uint8_t*
                               float* out, uint8_t* pcodes) {
   attention_rows(q8, k8, v8, qs, ks, vs, means, block_scale, BH, nq, nk, D, sm, rows, nrows,
                  out, pcodes, 1);
+}
+
+/* The folded ExpCast encode of the reference's default modes without block values. */
+VCO_EXPORT void vco_attention_affine(const int8_t* q8, const int8_t* k8, const uint8_t* v8,
+                                     const float* qs, const float* ks, const float* vs,
+                                     const uint16_t* means, int block_scale, int64_t BH,
+                                     int64_t nq, int64_t nk, int D, float sm,
+                                     const int64_t* rows, int64_t nrows, float* out,
+                                     uint8_t* pcodes) {
+  attention_rows(q8, k8, v8, qs, ks, vs, means, block_scale, BH, nq, nk, D, sm, rows, nrows,
+                 out, pcodes, 2);
 }
 
 /* The Sage FP8 control path (expcast=False); pcodes receives the E4M3 bytes of P. */

@@ -80,6 +80,7 @@ def _declare(L):
     L.vco_quant_v_smooth.argtypes = [P, i32, i64, i64, i32, P, i32, P, P, P]
     L.vco_attention.argtypes = [P, P, P, P, P, P, P, i32, i64, i64, i64, i32, f32, P, i64, P, P]
     L.vco_attention_control.argtypes = L.vco_attention.argtypes
+    L.vco_attention_affine.argtypes = L.vco_attention.argtypes
 
 
 def _ptr(a):
@@ -247,11 +248,14 @@ def prepare(q, k, v, *, expcast=True, v_smooth=True, clusters=8, iterations=2, s
             "scale": D ** -0.5 if sm_scale is None else sm_scale, "permutation": perm}
 
 
-def reference(state, query_indices=None, return_codes=False):
+def reference(state, query_indices=None, return_codes=False, affine=False):
     """Decoded-payload oracle (vc_reference.py:20-91) with the exact P bytes.
 
     state["expcast"] False selects the Sage FP8 control path (vc_reference.py:58-66):
     the bytes are then E4M3(exp2(...)) and the mass is the unrounded exp2 sum.
+    affine=True selects the folded ExpCast encode of the reference's default kernel modes
+    (vc12..vc15, "optimized"; sal/csrc/vc/vc_math.cuh:16-111), which the reference only
+    uses without block values.
     Returns float32 [B,H,len(ids),D] (and uint8 codes [B,H,len(ids),tiles*128]).
     """
     q8, k8, v8 = state["q"], state["k"], state["v"]
@@ -266,7 +270,10 @@ def reference(state, query_indices=None, return_codes=False):
     block_scale = int(means is not None and vs is not None and vs.ndim == 4)
     out = np.empty((B, H, ids.size, D), np.float32)
     codes = np.empty((B, H, ids.size, tiles * 128), np.uint8) if return_codes else None
-    fn = lib().vco_attention if state.get("expcast", True) else lib().vco_attention_control
+    if affine and (not state.get("expcast", True) or means is not None):
+        raise ValueError("the folded ExpCast encode applies to ExpCast without block values")
+    fn = (lib().vco_attention_control if not state.get("expcast", True)
+          else lib().vco_attention_affine if affine else lib().vco_attention)
     fn(_ptr(_c(q8, np.int8)), _ptr(_c(k8, np.int8)), _ptr(_c(v8, np.uint8)),
        _ptr(_c(state["qs"], np.float32)), _ptr(_c(state["ks"], np.float32)),
        _ptr(None if vs is None else _c(vs, np.float32)),

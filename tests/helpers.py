@@ -105,3 +105,36 @@ def rounding_order_payload(nk):
     return {"q": q, "k": k, "v": np.zeros((1, 1, dim, tiles * 128), np.uint8), "qs": qs, "ks": ks,
             "vs": np.ones((1, 1, dim), np.float32), "means": None, "expcast": True, "block_values": False,
             "scale": float(np.float32(dim ** -0.5)), "output_type": 1}
+
+
+# A one-row payload (D=64, two tiles) where the folded ExpCast encode of the reference's
+# default kernel modes (sal/csrc/vc/vc_math.cuh:76-111) and the unfused encode give
+# different bytes for key 96 of the first tile (found by search): key 45 holds the row
+# maximum (byte 120); key 96 is 116 unfused and 115 folded.
+FOLD_Q = (-115, -105, 3, -123)
+FOLD_K = {45: (25, -117, 79, -112), 96: (-56, 8, -96, -119)}
+FOLD_QS = float.fromhex("0x1.6f324p-7")
+FOLD_KS = tuple(float.fromhex(x) for x in ("0x1.55ded6p-7", "0x1.90b75ap-7", "0x1.4523e2p-6", "0x1.12c5fep-6",
+                                              "0x1.0756f6p-6", "0x1.2fd4d6p-6", "0x1.078d94p-6", "0x1.6e4c06p-8"))
+FOLD_CODE_UNFUSED, FOLD_CODE_FOLDED = 116, 115
+
+
+def folded_encode_payload(extreme_rows=(), nq=32):
+    """FOLD_* on query row 0 of an nq-row payload; every row in `extreme_rows` gets a
+    row maximum far above 128 (the folded encode's safety bound), which makes its whole
+    16-row group fall back to the unfused encode."""
+    dim, nk = 64, 200
+    q = np.zeros((1, 1, nq, dim), np.int8)
+    k = np.zeros((1, 1, nk, dim), np.int8)
+    q[0, 0, 0, :4] = FOLD_Q
+    for key, row in FOLD_K.items():
+        k[0, 0, key, :4] = row
+    qs = np.ones((1, 1, ((nq + 63) // 64) * 32), np.float32)
+    qs[0, 0, 0] = FOLD_QS
+    for r in extreme_rows:
+        q[0, 0, r, 0] = 127
+        qs[0, 0, (r // 16) * 8 + r % 8] = 100.0
+    ks = np.asarray(FOLD_KS, np.float32).reshape(1, 1, 8)
+    return {"q": q, "k": k, "v": np.zeros((1, 1, dim, 256), np.uint8), "qs": qs, "ks": ks,
+            "vs": np.ones((1, 1, dim), np.float32), "means": None, "expcast": True, "block_values": False,
+            "scale": float(np.float32(dim ** -0.5)), "output_type": 1}

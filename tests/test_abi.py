@@ -61,8 +61,10 @@ def _fwd(**kw):
 
 def test_invalid_calls_rejected_before_launch():
     assert _fwd(D=96) == (1, "D must be 64 or 128")
-    rc, msg = _fwd(expcast=2)
+    rc, msg = _fwd(expcast=3)
     assert rc == 1 and "expcast" in msg
+    rc, msg = _fwd(expcast=2, block_values=1)
+    assert rc == 1 and "folded" in msg
     rc, msg = _fwd(expcast=0)  # the control path is accepted; the null pointers fail next
     assert rc == 1 and "null" in msg
     rc, msg = _fwd(sm=float("inf"))

@@ -73,6 +73,17 @@ def test_forward_prepared_dispatches_state_to_the_single_kernel(monkeypatch, mod
     assert args[:7] == tuple(state[x] for x in ("q", "k", "v", "qs", "ks", "vs", "means"))
     assert args[7:] == (True, False, 1, 0.125)
     assert kwargs["channel_scale"] is True
+    # reference vc.py:187-189: the default and vc12..vc15 modes fold the ExpCast encode
+    assert kwargs["affine"] is (mode in ("optimized", "vc15", "vc22_both", "vc28_stream_i2f"))
+
+
+def test_folded_encode_never_with_block_values_or_control(monkeypatch):
+    calls = []
+    monkeypatch.setattr(api, "_extension", lambda: SimpleNamespace(forward=lambda *a, **k: calls.append(k) or "out"))
+    api.forward_prepared(payload(True))
+    api.forward_prepared({**payload(False), "expcast": False})
+    api.forward_prepared(payload(False), kernel_mode="vc11")
+    assert [k["affine"] for k in calls] == [False, False, False]
 
 
 def test_forward_prepared_block_scales_dispatch_without_channel_scale(monkeypatch):

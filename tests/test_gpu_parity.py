@@ -11,7 +11,8 @@ import pytest
 import torch
 
 import vcx
-from helpers import bits, cosine, dtype_name, logical_to_storage, make_qkv, output_bound, storage_to_logical
+from helpers import (FOLD_CODE_FOLDED, FOLD_CODE_UNFUSED, bits, cosine, dtype_name, folded_encode_payload,
+                     logical_to_storage, make_qkv, output_bound, storage_to_logical)
 from oracle import vc_oracle as o
 
 pytestmark = pytest.mark.gpu
@@ -267,7 +268,8 @@ def test_sageattn_vc_end_to_end_config1_payloads_and_output():
             np.testing.assert_array_equal(st["permutation"].cpu().numpy(), ost["permutation"])
             np.testing.assert_array_equal(st["means"].view(torch.int16).cpu().numpy().view(np.uint16), ost["means"])
         out = forward_prepared(st).float().cpu().numpy()
-        eout = o.reference(ost)
+        # the default kernel mode folds the ExpCast encode when there are no block values
+        eout = o.reference(ost, affine=not smooth)
         err, bound = output_bound(out, eout)
         assert np.all(err <= bound)
         assert cosine(out, eout) >= 0.9999
@@ -427,18 +429,22 @@ def test_main_config_all_heads_payloads_and_sampled_rows():
     np.testing.assert_array_equal(ks.cpu().numpy(), st["ks"])
     np.testing.assert_array_equal(storage_to_logical(v8, vcx.value_token()), st["v"])
     np.testing.assert_array_equal(vs.cpu().numpy(), st["vs"])
-    out = vcx.forward(q8, k8, v8, qs, ks, vs, None, True, False, 1, D ** -0.5)
     rows = np.array([0, 1, 4711, 18870, 29999, 37631, 37700, 37740])
-    eout, ecodes = o.reference(st, query_indices=rows, return_codes=True)
-    for r0 in (0, 37700):  # the P-dump variant takes one contiguous row range per launch
-        r1 = r0 + 41 if r0 else 2
-        _, pd = vcx.forward(q8, k8, v8, qs, ks, vs, None, True, False, 1, D ** -0.5, p_rows=(r0, r1))
-        sel = [i for i, r in enumerate(rows) if r0 <= r < r1]
-        np.testing.assert_array_equal(pd.cpu().numpy()[:, :, rows[sel] - r0], ecodes[:, :, sel])
-    got = out[:, :, rows].float().cpu().numpy()
-    err, bound = output_bound(got, eout)
-    assert np.all(err <= bound), float((err - bound).max())
-    assert cosine(got, eout) >= 0.9999
+    # both ExpCast encodes: unfused, and folded (the reference's default mode, which the
+    # benchmark times)
+    for affine in (False, True):
+        out = vcx.forward(q8, k8, v8, qs, ks, vs, None, True, False, 1, D ** -0.5, affine=affine)
+        eout, ecodes = o.reference(st, query_indices=rows, return_codes=True, affine=affine)
+        for r0 in (0, 37700):  # the P-dump variant takes one contiguous row range per launch
+            r1 = r0 + 41 if r0 else 2
+            _, pd = vcx.forward(q8, k8, v8, qs, ks, vs, None, True, False, 1, D ** -0.5, affine=affine,
+                                p_rows=(r0, r1))
+            sel = [i for i, r in enumerate(rows) if r0 <= r < r1]
+            np.testing.assert_array_equal(pd.cpu().numpy()[:, :, rows[sel] - r0], ecodes[:, :, sel])
+        got = out[:, :, rows].float().cpu().numpy()
+        err, bound = output_bound(got, eout)
+        assert np.all(err <= bound), float((err - bound).max())
+        assert cosine(got, eout) >= 0.9999
 
 
 CONTROL = [  # B, H, Nq, Nk, D, dtype, V mode
@@ -505,3 +511,54 @@ def test_control_path_uniform_attention_known_answer_and_end_to_end():
     err, bound = output_bound(got, eout)
     assert np.all(err <= bound)
     assert cosine(got, eout) >= 0.9999
+
+
+FOLDED = [  # B, H, Nq, Nk, D, dtype, q/k magnitude (large values push |m'| past 128: group fallback)
+    (1, 2, 2048, 2048, 128, torch.bfloat16, 1.0),
+    (1, 2, 257, 385, 128, torch.float16, 1.0),
+    (1, 1, 63, 127, 64, torch.bfloat16, 1.0),
+    (1, 1, 1, 1, 128, torch.bfloat16, 1.0),
+    (1, 2, 300, 700, 64, torch.bfloat16, 6.0),
+]
+
+
+@pytest.mark.parametrize("case", FOLDED, ids=lambda c: _ids(c[:6]) + f"_x{c[6]:g}")
+def test_folded_encode_p_bytes_bit_exact_and_output(case):
+    # The reference's default ExpCast kernel without block values (vc_math.cuh:16-111,
+    # FoldAffine): bytes RNE(fmaf(base, RN(scale*A), fmaf(-m', A, B))), with the unfused
+    # bytes for every 16-row group and tile in which some |m'| > 128.
+    B, H, Nq, Nk, D, dt, mag = case
+    _print_case("folded encode", case)
+    q, k, v = make_qkv(B, H, Nq, Nk, D, dt, seed=17)
+    q, k = (x.float().mul(mag).to(dt) for x in (q, k))
+    st = _oracle_state(q, k, v, False, dt)
+    to = _to_dev
+    v8 = to(logical_to_storage(st["v"], vcx.value_token())).view(torch.float8_e4m3fn)
+    out, pd = vcx.forward(to(st["q"]), to(st["k"]), v8, to(st["qs"]), to(st["ks"]), to(st["vs"]), None,
+                          True, False, st["output_type"], st["scale"], affine=True, p_rows=(0, Nq))
+    eout, ecodes = o.reference(st, return_codes=True, affine=True)
+    np.testing.assert_array_equal(pd.cpu().numpy(), ecodes)
+    got = out.float().cpu().numpy()
+    err, bound = output_bound(got, eout)
+    assert np.all(err <= bound), float((err - bound).max())
+    assert cosine(got, eout) >= 0.9999
+    out2 = vcx.forward(to(st["q"]), to(st["k"]), v8, to(st["qs"]), to(st["ks"]), to(st["vs"]), None,
+                       True, False, st["output_type"], st["scale"], affine=True)
+    assert torch.equal(out2, out)
+
+
+@pytest.mark.parametrize("extreme, code", [((), FOLD_CODE_FOLDED), ((3,), FOLD_CODE_UNFUSED), ((19,), FOLD_CODE_FOLDED)])
+def test_folded_encode_known_answer_and_group_fallback_on_gpu(extreme, code):
+    # helpers.folded_encode_payload: key 96 of row 0 is 115 folded / 116 unfused; an extreme
+    # row in the same 16-row group (row 3) forces the unfused byte, one in the next group
+    # (row 19) does not.
+    s = folded_encode_payload(extreme_rows=extreme)
+    _print_case("folded encode KA", extreme)
+    to = _to_dev
+    v8 = to(logical_to_storage(s["v"], vcx.value_token())).view(torch.float8_e4m3fn)
+    _, pd = vcx.forward(to(s["q"]), to(s["k"]), v8, to(s["qs"]), to(s["ks"]), to(s["vs"]), None,
+                        True, False, 1, s["scale"], affine=True, p_rows=(0, 32))
+    got = pd.cpu().numpy()
+    assert got[0, 0, 0, 96] == code and got[0, 0, 0, 45] == 120
+    _, ecodes = o.reference(s, return_codes=True, affine=True)
+    np.testing.assert_array_equal(got, ecodes)

@@ -13,7 +13,8 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import bits, make_qkv
+from helpers import (FOLD_CODE_FOLDED, FOLD_CODE_UNFUSED, FOLD_K, FOLD_KS, FOLD_Q, FOLD_QS, bits,
+                     folded_encode_payload, make_qkv)
 from oracle import vc_oracle as o
 
 GOLDEN = Path(__file__).resolve().parent / "golden" / "int8_per_thread.npz"
@@ -556,3 +557,62 @@ def test_last_tile_rounding_order_known_answer(nk):
     assert codes[0, 0, 0, 0] == 120
     assert codes[0, 0, 0, 1] == (ORDER_CODE_LAST if nk <= 128 else ORDER_CODE_OTHER)
     assert np.all(codes[0, 0, 0, 2:] == 0)
+
+
+# ------------------------------------------------------------------ folded ExpCast encode
+
+def _rn32(x):
+    """Exact rational -> nearest binary32 (ties to even), as a Fraction."""
+    f = np.float32(float(x))
+    cands = [f, np.nextafter(f, np.float32(np.inf)), np.nextafter(f, np.float32(-np.inf))]
+    best = min(cands, key=lambda c: (abs(Fraction(float(c)) - x), int(np.float32(c).view(np.uint32)) & 1))
+    return Fraction(float(best))
+
+
+def test_folded_encode_known_answer_against_exact_arithmetic():
+    # sal/csrc/vc/vc_math.cuh:76-111 (FoldAffine, the reference's default "optimized"/vc15
+    # kernel without block values): gain = RN(scale * A), bias = fmaf(-m', A, B),
+    # code = sat_u8(RNE(fmaf(float(acc), gain, bias))) with scale = RN(sm * RN(qs * ks)).
+    # The unfused code is RNE(fmaf(RN(RN(float(acc) * scale) - m'), A, B)). Both are
+    # recomputed here in exact rational arithmetic with one rounding per IEEE step.
+    s = folded_encode_payload()
+    _, plain = o.reference(s, return_codes=True)
+    _, fold = o.reference(s, return_codes=True, affine=True)
+    assert plain[0, 0, 0, 96] == FOLD_CODE_UNFUSED and fold[0, 0, 0, 96] == FOLD_CODE_FOLDED
+    assert plain[0, 0, 0, 45] == fold[0, 0, 0, 45] == 120
+    A, B = Fraction(float(np.float32(11.541560173034668))), Fraction(float(np.float32(119.6500015258789)))
+    sm = np.float32(64 ** -0.5)
+    acc = {key: int(np.dot(np.int64(FOLD_Q), np.int64(row))) for key, row in FOLD_K.items()}
+    scale = {key: np.float32(sm * np.float32(np.float32(FOLD_QS) * np.float32(FOLD_KS[(key % 8) // 2])))
+             for key in FOLD_K}
+    m = np.float32(np.float32(acc[45]) * scale[45])
+    shifted = np.float32(np.float32(np.float32(acc[96]) * scale[96]) - m)
+    assert round(_rn32(Fraction(float(shifted)) * A + B)) == FOLD_CODE_UNFUSED
+    gain = Fraction(float(np.float32(scale[96] * np.float32(11.541560173034668))))
+    bias = _rn32(-Fraction(float(m)) * A + B)
+    assert round(_rn32(Fraction(acc[96]) * gain + bias)) == FOLD_CODE_FOLDED
+
+
+def test_folded_encode_falls_back_per_sixteen_row_group():
+    # vc_math.cuh:102-110: if any row of the warp's 16 rows has |m'| > 128 (or a scale
+    # underflows / the gain overflows), the whole group uses the unfused encode this tile.
+    _, same_group = o.reference(folded_encode_payload(extreme_rows=(3,)), return_codes=True, affine=True)
+    assert same_group[0, 0, 0, 96] == FOLD_CODE_UNFUSED
+    s = folded_encode_payload(extreme_rows=(19,))
+    _, other_group = o.reference(s, return_codes=True, affine=True)
+    _, unfused = o.reference(s, return_codes=True)
+    assert other_group[0, 0, 0, 96] == FOLD_CODE_FOLDED
+    np.testing.assert_array_equal(other_group[0, 0, 16:], unfused[0, 0, 16:])
+
+
+def test_folded_encode_differs_from_unfused_only_next_to_ties():
+    # On N(0,1) inputs the two encodes disagree on a few bytes per million, by one code.
+    q, k, v = make_qkv(1, 1, 128, 2048, 128, torch.bfloat16, seed=0)
+    st = o.prepare(bits(q), bits(k), bits(v), v_smooth=False, dtype="bfloat16")
+    out1, c1 = o.reference(st, return_codes=True)
+    out2, c2 = o.reference(st, return_codes=True, affine=True)
+    d = np.abs(c1.astype(int) - c2.astype(int))
+    assert d.max() <= 1 and np.count_nonzero(d) <= d.size // 50000
+    np.testing.assert_allclose(out1, out2, rtol=0, atol=1e-3)
+    with pytest.raises(ValueError, match="without block values"):
+        o.reference(o.prepare(bits(q), bits(k), bits(v), v_smooth=True, dtype="bfloat16"), affine=True)

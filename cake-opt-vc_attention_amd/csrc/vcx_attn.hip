@@ -27,7 +27,13 @@
 // The P bytes follow the contract exactly; alpha, O and den only feed the
 // bf16/fp16 output, whose tolerance covers the exp2 approximation.
 //
-// EC = false is the Sage FP8 control path (expcast=False; vc_sm90.cu:177,
+// PM = 2 (expcast = 2, no block values) is the folded encode of the reference's default
+// kernel modes (vc_math.cuh:16-111): code = sat_u8(RNE(fmaf(base, RN(scale*A), fmaf(-m', A, B))))
+// with scale = RN(sm*RN(qs*ks)) (last tile: base = RN(float(acc)*dq), scale = sm), and the
+// unfused code above for a whole 16-row group in a tile where some |m'| > 128, a scale
+// underflows or a gain overflows (the reference's warp-wide fallback).
+//
+// PM = 0 is the Sage FP8 control path (expcast=False; vc_sm90.cu:177,
 // attn_utils.cuh:355-455): a.sm = RN(sm * RN(log2 e)), base/factor as above,
 // m' = max(m, max fmaf(base, factor, -8.807)), P = E4M3(exp2(fmaf(base, factor, -m'))),
 // den and the mean restore use the unrounded sum of P. exp2 is v_exp_f32, so a P

@@ -110,9 +110,12 @@ int vcx_prepare_v_fp8(const void* v, int dtype, int64_t B, int64_t H, int64_t N,
 
 /* Fused attention forward: INT8 QK^T on MFMA, ExpCast E4M3 probabilities,
  * FP8 PV on MFMA, online max/sum, block-mean restore, epilogue.
- * expcast = 1: ExpCast bytes (exact contract). expcast = 0: the Sage FP8 control
- * path, P = E4M3(exp2(.)) with the 8.807 offset and an unrounded exp2 mass
- * (hardware exp2). block_values = 1 consumes means/vs as written by
+ * expcast = 1: unfused ExpCast bytes (the reference's oracle and vc4..vc11 modes).
+ * expcast = 2: the folded ExpCast encode of the reference's default modes
+ * (vc12..vc15, "optimized"; vc_math.cuh:16-111), only with block_values = 0, with the
+ * reference's per-16-row-group fallback to the unfused bytes when some |m'| > 128.
+ * expcast = 0: the Sage FP8 control path, P = E4M3(exp2(.)) with the 8.807 offset and
+ * an unrounded exp2 mass (hardware exp2). block_values = 1 consumes means/vs as written by
  * vcx_prepare_v_fp8(smooth=1, channel_scale): channel_scale = 1 applies vs
  * [B,H,D] in the epilogue, channel_scale = 0 scales every tile's contribution
  * by its vs [B,H,tiles,D]; block_values = 0 uses vs [B,H,D], ignores means and

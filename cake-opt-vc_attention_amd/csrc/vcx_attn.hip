@@ -184,6 +184,10 @@ __device__ inline float row_sum(float x) {
 // Sage's FP8 offset: the control path's row maximum is lowered by 8.807 so that the
 // largest probability is 2^8.807 ~ 448, the E4M3 maximum (sal/csrc/qattn/attn_utils.cuh:30).
 constexpr float kFp8Offset = 8.807f;
+// The folded path starts its QK accumulators at the bits of 1.5 * 2^23: with |acc| < 2^22
+// they read as the float 12582912 + acc, so float(acc) is one exact subtraction.
+constexpr int kBias = 0x4B400000;
+constexpr float kBiasF = 12582912.0f;
 
 template <int D, int VM, bool DUMP, int PM>
 struct Wave {
@@ -227,7 +231,7 @@ struct Wave {
       }
 #pragma unroll
       for (int qg = 0; qg < 2; ++qg) {
-        v4i acc = {0, 0, 0, 0};
+        v4i acc = PM == 2 ? v4i{kBias, kBias, kBias, kBias} : v4i{0, 0, 0, 0};
 #pragma unroll
         for (int ds = 0; ds < DS; ++ds) acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(kf[j][ds], qf[qg][ds], acc, 0, 0, 0);
         S[qg][j] = acc;
@@ -258,9 +262,9 @@ struct Wave {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
               im = im > S[qg][j][r] ? im : S[qg][j][r];
-              bs[j][r] = static_cast<float>(S[qg][j][r]);
+              bs[j][r] = __int_as_float(S[qg][j][r]) - kBiasF;
             }
-          tmax = static_cast<float>(im) * scale;
+          tmax = static_cast<float>(im - kBias) * scale;
         } else {
           float bm = -INFINITY;
 #pragma unroll
@@ -268,7 +272,7 @@ struct Wave {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
               const int64_t key = t * kTile + 16 * j + 8 * (r >> 1) + 2 * G + (r & 1);
-              bs[j][r] = key < a.Nk ? static_cast<float>(S[qg][j][r]) * dq : -INFINITY;
+              bs[j][r] = key < a.Nk ? (__int_as_float(S[qg][j][r]) - kBiasF) * dq : -INFINITY;
               bm = fmaxf(bm, bs[j][r]);
             }
           tmax = bm * scale;

@@ -30,7 +30,7 @@ PEAK_HBM_GBS = 8000.0   # MI355X HBM3E, GB/s (published)
 # 2.0, the factor a plain 1 GiB copy reads) plus WRITE_SIZE (factor 1.0); the run and its
 # commands are in profiles/attn_kernel_main_hbm_bytes.txt. Counters cannot be read from
 # inside this process, so the figure is keyed by configuration and null where unmeasured.
-MEASURED_TRAFFIC_BYTES = {"main": 3.131e9}
+MEASURED_TRAFFIC_BYTES = {"main": 3.109e9}
 
 CONFIGS = {
     # name: (B, H, N, D, kind, v_smooth, description)

@@ -393,6 +393,65 @@ VCO_EXPORT void vco_quant_k(const uint16_t* k, int dtype, int64_t BH, int64_t n,
 }
 
 /* ------------------------------------------------------------------ */
+/* FP8 block-scaled Q/K (vc27)                                        */
+/* ------------------------------------------------------------------ */
+
+/* K channel mean kept in binary32: km = RN_f32(S / n) with S the fp64 sum of the
+ * channel over all keys in the tile-tree order of vco_k_mean. The reference sums in
+ * fp32 per 128-key block and then over blocks (sal/csrc/vc/qk_fp8.cu:10-35); its
+ * validation accepts any mean within rtol 2e-5 of the fp64 mean
+ * (scripts/validate_fp8_qk.py:42), and this definition is that mean rounded once. */
+VCO_EXPORT void vco_k_mean_f32(const uint16_t* k, int dtype, int64_t BH, int64_t n, int D,
+                               float* km) {
+  int64_t tiles = (n + 127) / 128;
+  double x[128];
+  for (int64_t h = 0; h < BH; ++h) {
+    for (int d = 0; d < D; ++d) {
+      double s = 0.0;
+      for (int64_t t = 0; t < tiles; ++t) {
+        for (int i = 0; i < 128; ++i) {
+          int64_t key = t * 128 + i;
+          x[i] = key < n ? (double)load_in(k + (h * n + key) * D + d, dtype) : 0.0;
+        }
+        s += vco_tile_tree_sum(x);
+      }
+      km[h * D + d] = (float)(s / (double)n);
+    }
+  }
+}
+
+/* One E4M3 block of `rows` rows x D channels: x' = mean ? RN_f32(x - mean_d) : x;
+ * s = max(RN(amax / 448), 1e-12f); code = e4m3_satfinite(RN(x' / s)) with IEEE division.
+ * Rows past n are not part of the block. scales [BH][ceil(n/rows)].
+ * Reference: quantize_qk_fp8, sal/csrc/vc/qk_fp8.cu:38-74 (Q: rows 64, K: rows 128 and
+ * centred); restated by scripts/validate_fp8_qk.py:8-20. */
+VCO_EXPORT void vco_quant_fp8_block(const uint16_t* x, int dtype, int64_t BH, int64_t n, int D,
+                                    int rows, const float* mean, uint8_t* codes, float* scales) {
+  const int64_t blocks = (n + rows - 1) / rows;
+  for (int64_t h = 0; h < BH; ++h) {
+    for (int64_t b = 0; b < blocks; ++b) {
+      float amax = 0.0f;
+      const int64_t r1 = (b + 1) * rows < n ? (b + 1) * rows : n;
+      for (int64_t r = b * rows; r < r1; ++r)
+        for (int d = 0; d < D; ++d) {
+          float v = load_in(x + (h * n + r) * D + d, dtype);
+          if (mean) v = v - mean[h * D + d];
+          amax = fmaxf(amax, fabsf(v));
+        }
+      float s = amax / 448.0f;
+      s = fmaxf(s, 1e-12f);
+      scales[h * blocks + b] = s;
+      for (int64_t r = b * rows; r < r1; ++r)
+        for (int d = 0; d < D; ++d) {
+          float v = load_in(x + (h * n + r) * D + d, dtype);
+          if (mean) v = v - mean[h * D + d];
+          codes[(h * n + r) * D + d] = vco_e4m3_encode(v / s);
+        }
+    }
+  }
+}
+
+/* ------------------------------------------------------------------ */
 /* V quantization                                                     */
 /* ------------------------------------------------------------------ */
 
@@ -510,6 +569,50 @@ static inline uint8_t cvt_u8_rne(float u) {
   return (uint8_t)rintf(u);
 }
 
+/* How a (row, key) pair's raw QK score and scales come out of a payload.
+ * INT8 (sageattn_vc): exact int32 dot product, qs index (row/16)*8 + row%8 over
+ *   ceil(nq/64)*32 entries, ks index tile*4 + (key%8)/2 (sal/csrc/vc/vc_sm90.cu:288-289).
+ * FP8 block (vc27, sal/sageattention_local/vc_fp8.py; vc_reference.py:23-24,37-40): the
+ *   binary32 rounding of the exact sum of decoded E4M3 products, qs index row/64 over
+ *   ceil(nq/64) entries, ks index tile. Rows past nq score 0 (zero Q rows). */
+typedef struct {
+  const int8_t* q8;
+  const int8_t* k8;
+  const float* qs;
+  const float* ks;
+  const float* dec; /* E4M3 decode table (FP8 block) */
+  int64_t nq, nk, tiles, qsn;
+  int D, fp8;
+} qk_view;
+
+static inline qk_view make_qk_view(const int8_t* q8, const int8_t* k8, const float* qs, const float* ks,
+                                   int64_t nq, int64_t nk, int D, int fp8, const float* dec) {
+  qk_view v = {q8, k8, qs, ks, dec, nq, nk, (nk + 127) / 128, fp8 ? (nq + 63) / 64 : (nq + 63) / 64 * 32, D, fp8};
+  return v;
+}
+
+static inline float qk_raw(const qk_view* v, int64_t h, int64_t r, int64_t key) {
+  if (r >= v->nq) return 0.0f;
+  const int8_t* qrow = v->q8 + (h * v->nq + r) * v->D;
+  const int8_t* krow = v->k8 + (h * v->nk + key) * v->D;
+  if (v->fp8) {
+    double acc = 0.0;  /* every product of two E4M3 values and their sum are exact in fp64 */
+    for (int d = 0; d < v->D; ++d) acc += (double)v->dec[(uint8_t)qrow[d]] * (double)v->dec[(uint8_t)krow[d]];
+    return (float)acc;
+  }
+  int32_t acc = 0;
+  for (int d = 0; d < v->D; ++d) acc += (int32_t)qrow[d] * (int32_t)krow[d];
+  return (float)acc;
+}
+
+static inline float qk_qscale(const qk_view* v, int64_t h, int64_t r) {
+  return v->fp8 ? v->qs[h * v->qsn + r / 64] : v->qs[h * v->qsn + (r / 16) * 8 + r % 8];
+}
+
+static inline float qk_kscale(const qk_view* v, int64_t h, int64_t t, int i) {
+  return v->fp8 ? v->ks[h * v->tiles + t] : v->ks[h * v->tiles * 4 + t * 4 + (i % 8) / 2];
+}
+
 /* Folded ExpCast encode of the reference's default kernel modes (vc12..vc15, "optimized")
  * without block values: sal/csrc/vc/vc_math.cuh:16-111, vc_probability_prepare with
  * FoldAffine. Per 16-row group and tile (one Hopper warp: 16 rows x 4 key groups),
@@ -519,10 +622,9 @@ static inline uint8_t cvt_u8_rne(float u) {
  * one falls back to the unfused code of every row. Rows past nq (zero Q rows in the
  * reference's tile) take part with acc = 0. Returns safe[BH][ceil(nq/16)][tiles] for the
  * groups that hold a requested row (others are left 0). */
-static uint8_t* affine_safe_flags(const int8_t* q8, const int8_t* k8, const float* qs,
-                                  const float* ks, int64_t BH, int64_t nq, int64_t nk, int D,
-                                  float sm, const int64_t* rows, int64_t nrows) {
-  const int64_t tiles = (nk + 127) / 128, groups = (nq + 15) / 16, qsn = (nq + 63) / 64 * 32;
+static uint8_t* affine_safe_flags(const qk_view* v, int64_t BH, float sm, const int64_t* rows,
+                                  int64_t nrows) {
+  const int64_t nq = v->nq, nk = v->nk, tiles = v->tiles, groups = (nq + 15) / 16;
   uint8_t* flags = (uint8_t*)calloc((size_t)(BH * groups * tiles), 1);
   uint8_t* wanted = (uint8_t*)calloc((size_t)groups, 1);
   for (int64_t i = 0; i < nrows; ++i) wanted[rows[i] / 16] = 1;
@@ -537,24 +639,18 @@ static uint8_t* affine_safe_flags(const int8_t* q8, const int8_t* k8, const floa
         int ok = 1;
         for (int rr = 0; rr < 16; ++rr) {
           const int64_t r = g * 16 + rr;
-          const float qscale = qs[h * qsn + (r / 16) * 8 + r % 8];
+          const float qscale = qk_qscale(v, h, r);
           float tmax = -INFINITY;
           for (int gk = 0; gk < 4; ++gk) {
-            const float scale = last ? sm : sm * (qscale * ks[h * tiles * 4 + t * 4 + gk]);
+            const float scale = last ? sm : sm * (qscale * qk_kscale(v, h, t, 2 * gk));
             const float gain = scale * kExpA;
             if (!(scale >= 1.1754943508222875e-38f) || !isfinite(gain)) ok = 0;
           }
           for (int i = 0; i < 128; ++i) {
             const int64_t key = t * 128 + i;
             if (key >= nk) continue;
-            int32_t acc = 0;
-            if (r < nq) {
-              const int8_t* qrow = q8 + (h * nq + r) * D;
-              const int8_t* krow = k8 + (h * nk + key) * D;
-              for (int d = 0; d < D; ++d) acc += (int32_t)qrow[d] * (int32_t)krow[d];
-            }
-            const float dq = qscale * ks[h * tiles * 4 + t * 4 + (i % 8) / 2];
-            const float f = (float)acc;
+            const float dq = qscale * qk_kscale(v, h, t, i);
+            const float f = qk_raw(v, h, r, key);
             const float lg = last ? (f * dq) * sm : f * (sm * dq);
             tmax = fmaxf(tmax, lg);
           }
@@ -603,20 +699,19 @@ static void attention_rows(const int8_t* q8, const int8_t* k8, const uint8_t* v8
                            const float* qs, const float* ks, const float* vs,
                            const uint16_t* means, int block_scale, int64_t BH, int64_t nq,
                            int64_t nk, int D, float sm, const int64_t* rows, int64_t nrows,
-                           float* out, uint8_t* pcodes, int mode) {
+                           float* out, uint8_t* pcodes, int mode, int qk_fp8) {
   const int expcast = mode != 0, affine = mode == 2;
   int64_t tiles = (nk + 127) / 128, npad = tiles * 128;
-  int64_t qsn = (nq + 63) / 64 * 32;
   float* vdec = (float*)malloc(sizeof(float) * 256);  /* decode table */
   for (int c = 0; c < 256; ++c) vdec[c] = vco_e4m3_decode((uint8_t)c);
+  const qk_view view = make_qk_view(q8, k8, qs, ks, nq, nk, D, qk_fp8, vdec);
   const float s = expcast ? sm : sm * 1.4426950408889634f;
-  uint8_t* safe = affine ? affine_safe_flags(q8, k8, qs, ks, BH, nq, nk, D, sm, rows, nrows) : NULL;
+  uint8_t* safe = affine ? affine_safe_flags(&view, BH, sm, rows, nrows) : NULL;
 #pragma omp parallel for schedule(dynamic) collapse(2)
   for (int64_t h = 0; h < BH; ++h) {
     for (int64_t ri = 0; ri < nrows; ++ri) {
       int64_t r = rows[ri];
-      const int8_t* qrow = q8 + (h * nq + r) * D;
-      float qscale = qs[h * qsn + (r / 16) * 8 + r % 8];
+      const float qscale = qk_qscale(&view, h, r);
       float m = -5000000.0f;
       double den = 0.0;
       double o[128];
@@ -629,11 +724,8 @@ static void attention_rows(const int8_t* q8, const int8_t* k8, const uint8_t* v8
         for (int i = 0; i < 128; ++i) {
           int64_t key = t * 128 + i;
           if (key >= nk) { logit[i] = -INFINITY; abase[i] = -INFINITY; factor[i] = 1.0f; continue; }
-          const int8_t* krow = k8 + (h * nk + key) * D;
-          int32_t acc = 0;
-          for (int d = 0; d < D; ++d) acc += (int32_t)qrow[d] * (int32_t)krow[d];
-          float dq = qscale * ks[h * tiles * 4 + t * 4 + (i % 8) / 2];
-          float f = (float)acc;
+          float dq = qscale * qk_kscale(&view, h, t, i);
+          float f = qk_raw(&view, h, r, key);
           float base, fac;
           if (!last) { base = f; fac = s * dq; }
           else { base = f * dq; fac = s; }
@@ -706,7 +798,7 @@ VCO_EXPORT void vco_attention(const int8_t* q8, const int8_t* k8, const uint8_t*
                               int64_t nk, int D, float sm, const int64_t* rows, int64_t nrows,
                               float* out, uint8_t* pcodes) {
   attention_rows(q8, k8, v8, qs, ks, vs, means, block_scale, BH, nq, nk, D, sm, rows, nrows,
-                 out, pcodes, 1);
+                 out, pcodes, 1, 0);
 }
 
 /* The folded ExpCast encode of the reference's default modes without block values. */
@@ -717,7 +809,7 @@ VCO_EXPORT void vco_attention_affine(const int8_t* q8, const int8_t* k8, const u
                                      const int64_t* rows, int64_t nrows, float* out,
                                      uint8_t* pcodes) {
   attention_rows(q8, k8, v8, qs, ks, vs, means, block_scale, BH, nq, nk, D, sm, rows, nrows,
-                 out, pcodes, 2);
+                 out, pcodes, 2, 0);
 }
 
 /* The Sage FP8 control path (expcast=False); pcodes receives the E4M3 bytes of P. */
@@ -728,5 +820,17 @@ VCO_EXPORT void vco_attention_control(const int8_t* q8, const int8_t* k8, const 
                                       const int64_t* rows, int64_t nrows, float* out,
                                       uint8_t* pcodes) {
   attention_rows(q8, k8, v8, qs, ks, vs, means, block_scale, BH, nq, nk, D, sm, rows, nrows,
-                 out, pcodes, 0);
+                 out, pcodes, 0, 0);
+}
+
+/* The FP8 block-scaled QK variant (vc27: sal/sageattention_local/vc_fp8.py:12-60,
+ * sal/csrc/vc/fp8_dispatch.cuh): q8/k8 hold E4M3 bytes, qs [BH][ceil(nq/64)],
+ * ks [BH][tiles]; mode 0 control, 1 unfused ExpCast, 2 folded ExpCast (the reference's
+ * FP8 kernel folds the ExpCast encode, fp8_dispatch.cuh:4-9). No block values. */
+VCO_EXPORT void vco_attention_fp8(const uint8_t* q8, const uint8_t* k8, const uint8_t* v8,
+                                  const float* qs, const float* ks, const float* vs, int64_t BH,
+                                  int64_t nq, int64_t nk, int D, float sm, const int64_t* rows,
+                                  int64_t nrows, float* out, uint8_t* pcodes, int mode) {
+  attention_rows((const int8_t*)q8, (const int8_t*)k8, v8, qs, ks, vs, NULL, 0, BH, nq, nk, D, sm,
+                 rows, nrows, out, pcodes, mode, 1);
 }

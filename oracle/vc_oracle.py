@@ -81,6 +81,9 @@ def _declare(L):
     L.vco_attention.argtypes = [P, P, P, P, P, P, P, i32, i64, i64, i64, i32, f32, P, i64, P, P]
     L.vco_attention_control.argtypes = L.vco_attention.argtypes
     L.vco_attention_affine.argtypes = L.vco_attention.argtypes
+    L.vco_attention_fp8.argtypes = [P, P, P, P, P, P, i64, i64, i64, i32, f32, P, i64, P, P, i32]
+    L.vco_k_mean_f32.argtypes = [P, i32, i64, i64, i32, P]
+    L.vco_quant_fp8_block.argtypes = [P, i32, i64, i64, i32, i32, P, P, P]
 
 
 def _ptr(a):
@@ -192,6 +195,39 @@ def quant_k(k, km=None, perm=None, dtype: str = "bfloat16"):
     return k8, ks
 
 
+def k_mean_f32(k, dtype: str = "bfloat16") -> np.ndarray:
+    """vc27 K channel mean in binary32 (qk_fp8.cu:10-35)."""
+    B, H, N, D = _shape4(k)
+    km = np.empty((B, H, D), np.float32)
+    lib().vco_k_mean_f32(_ptr(_c(k, np.uint16)), DTYPES[dtype], B * H, N, D, _ptr(km))
+    return km
+
+
+def quant_fp8_block(x, rows: int, mean=None, dtype: str = "bfloat16"):
+    """Block E4M3 quantizer of vc27 (qk_fp8.cu:38-74): codes uint8 [B,H,N,D] and scales
+    float32 [B,H,ceil(N/rows)]; mean (float32 [B,H,D]) centres first."""
+    B, H, N, D = _shape4(x)
+    codes = np.zeros((B, H, N, D), np.uint8)
+    scales = np.empty((B, H, (N + rows - 1) // rows), np.float32)
+    lib().vco_quant_fp8_block(_ptr(_c(x, np.uint16)), DTYPES[dtype], B * H, N, D, rows,
+                              _ptr(None if mean is None else _c(mean, np.float32)), _ptr(codes), _ptr(scales))
+    return codes, scales
+
+
+def prepare_fp8(q, k, v, *, expcast=True, sm_scale=None, dtype: str = "bfloat16"):
+    """State of the vc27 FP8 block-scaled QK path (vc_fp8.py:12-33): Q in 64-row E4M3
+    blocks, K centred in binary32 and in 128-row blocks, V per-channel E4M3 (no smoothing)."""
+    km = k_mean_f32(k, dtype)
+    q8, qs = quant_fp8_block(q, 64, None, dtype)
+    k8, ks = quant_fp8_block(k, 128, km, dtype)
+    v8, vs = per_channel_fp8(v, None, dtype)
+    D = np.asarray(q).shape[-1]
+    return {"q": q8, "k": k8, "v": v8, "qs": qs, "ks": ks, "vs": vs, "means": None, "k_mean": km,
+            "qk_format": "fp8_block", "expcast": bool(expcast), "block_values": False,
+            "output_type": 1 if dtype == "bfloat16" else 0,
+            "scale": D ** -0.5 if sm_scale is None else sm_scale, "permutation": None}
+
+
 def per_thread_int8(q, k, km=None, perm=None, dtype: str = "bfloat16"):
     """Q per row-pair and K per key-set INT8 with FP32 scales (BLKQ=64, WARPQ=16, BLKK=128, WARPK=128)."""
     q8, qs = quant_q(q, dtype)
@@ -270,6 +306,15 @@ def reference(state, query_indices=None, return_codes=False, affine=False):
     block_scale = int(means is not None and vs is not None and vs.ndim == 4)
     out = np.empty((B, H, ids.size, D), np.float32)
     codes = np.empty((B, H, ids.size, tiles * 128), np.uint8) if return_codes else None
+    if state.get("qk_format", "int8") == "fp8_block":
+        if means is not None or vs is None or vs.ndim != 3:
+            raise ValueError("the FP8 block QK path has no block values")
+        mode = 0 if not state.get("expcast", True) else (2 if affine else 1)
+        lib().vco_attention_fp8(_ptr(_c(q8, np.uint8)), _ptr(_c(k8, np.uint8)), _ptr(_c(v8, np.uint8)),
+                                _ptr(_c(state["qs"], np.float32)), _ptr(_c(state["ks"], np.float32)),
+                                _ptr(_c(vs, np.float32)), B * H, Nq, Nk, D, float(np.float32(state["scale"])),
+                                _ptr(ids), ids.size, _ptr(out), _ptr(codes), mode)
+        return (out, codes) if return_codes else out
     if affine and (not state.get("expcast", True) or means is not None):
         raise ValueError("the folded ExpCast encode applies to ExpCast without block values")
     fn = (lib().vco_attention_control if not state.get("expcast", True)

@@ -616,3 +616,105 @@ def test_folded_encode_differs_from_unfused_only_next_to_ties():
     np.testing.assert_allclose(out1, out2, rtol=0, atol=1e-3)
     with pytest.raises(ValueError, match="without block values"):
         o.reference(o.prepare(bits(q), bits(k), bits(v), v_smooth=True, dtype="bfloat16"), affine=True)
+
+
+# ------------------------------------------------------------------ FP8 block QK (vc27)
+
+def _fp8_quant_reference(x, rows, mean=None):
+    # scripts/validate_fp8_qk.py:8-20, restated with torch: per block of `rows` rows the scale
+    # is RN(amax/448) (>= 1e-12, IEEE division via float64) and the code RN(x/s) cast to E4M3.
+    x = x.float()
+    if mean is not None:
+        x = x - mean.unsqueeze(2)
+    packed, scales = [], []
+    for start in range(0, x.shape[2], rows):
+        block = x[:, :, start:start + rows]
+        scale = (block.abs().amax((-2, -1)).double() / 448).float().clamp_min(1e-12)
+        normalized = (block.double() / scale[..., None, None].double()).float()
+        packed.append(normalized.clamp(-448, 448).to(torch.float8_e4m3fn).view(torch.uint8))
+        scales.append(scale)
+    return torch.cat(packed, 2).numpy(), torch.stack(scales, 2).numpy()
+
+
+@pytest.mark.parametrize("nq,nk,dim", [(1, 1, 64), (63, 127, 128), (65, 129, 64), (193, 513, 128)])
+def test_fp8_block_quantizer_matches_reference_validation_formula(nq, nk, dim):
+    gen = torch.Generator().manual_seed(2701 + nq)
+    q = torch.randn(2, 3, nq, dim, generator=gen).to(torch.bfloat16)
+    k = torch.randn(2, 3, nk, dim, generator=gen).to(torch.bfloat16)
+    k = (k.float() + torch.arange(dim).view(1, 1, 1, -1) / 4).to(torch.bfloat16)  # distinct channel means
+    q[:, :, 64:] *= 3
+    km = o.k_mean_f32(bits(k))
+    exact = k.double().mean(2)
+    np.testing.assert_allclose(km, exact.numpy(), rtol=2e-5, atol=1e-5)  # validate_fp8_qk.py:42
+    assert np.array_equal(km, exact.float().numpy())  # this definition: the fp64 mean rounded once
+    for x, rows, mean in ((q, 64, None), (k, 128, torch.from_numpy(km))):
+        codes, scales = o.quant_fp8_block(bits(x), rows, None if mean is None else mean.numpy())
+        want_codes, want_scales = _fp8_quant_reference(x, rows, mean)
+        np.testing.assert_array_equal(scales, want_scales)
+        np.testing.assert_array_equal(codes, want_codes)
+
+
+def _fp8_payload(nq, nk, dim=64, expcast=True):
+    tiles = (nk + 127) // 128
+    return {"q": np.zeros((1, 1, nq, dim), np.uint8), "k": np.zeros((1, 1, nk, dim), np.uint8),
+            "v": np.zeros((1, 1, dim, tiles * 128), np.uint8), "qs": np.ones((1, 1, (nq + 63) // 64), np.float32),
+            "ks": np.ones((1, 1, tiles), np.float32), "vs": np.ones((1, 1, dim), np.float32), "means": None,
+            "qk_format": "fp8_block", "expcast": expcast, "block_values": False, "scale": 0.125}
+
+
+@pytest.mark.parametrize("expcast", [False, True])
+@pytest.mark.parametrize("nk", [1, 129, 257])
+def test_fp8_zero_logits_tail_and_v_scale_known_answer(expcast, nk):
+    # tests/test_fp8_qk.py:46-59: zero Q/K, V = 2 on the valid keys, vs = 3 -> 6 * weight.
+    s = _fp8_payload(65, nk, expcast=expcast)
+    s["v"][..., :nk] = o.e4m3_encode(np.float32(2.0))
+    s["vs"][...] = 3.0
+    weight = 1.0 if expcast else CONTROL_WEIGHT
+    for affine in ((False, True) if expcast else (False,)):
+        out = o.reference(s, affine=affine)
+        np.testing.assert_allclose(out, 6 * weight, rtol=2e-6, atol=2e-6)
+
+
+@pytest.mark.parametrize("expcast", [False, True])
+def test_fp8_sampling_keeps_block_scales(expcast):
+    # tests/test_fp8_qk.py:24-43: rows sampled from 64-row blocks keep their own scale.
+    gen = torch.Generator().manual_seed(2711)
+    q = torch.randn(1, 2, 129, 64, generator=gen)
+    k = torch.randn(1, 2, 257, 64, generator=gen)
+    q[:, :, 64:128] *= 4
+    k[:, :, 128:256] *= .125
+    s = o.prepare_fp8(bits(q.to(torch.bfloat16)), bits(k.to(torch.bfloat16)),
+                      bits(torch.randn(1, 2, 257, 64, generator=gen).to(torch.bfloat16)), expcast=expcast)
+    ids = [0, 7, 63, 64, 65, 127, 128]
+    for affine in ((False, True) if expcast else (False,)):
+        full, fc = o.reference(s, return_codes=True, affine=affine)
+        part, pc = o.reference(s, query_indices=ids, return_codes=True, affine=affine)
+        np.testing.assert_array_equal(part, full[:, :, ids])
+        np.testing.assert_array_equal(pc, fc[:, :, ids])
+
+
+def test_fp8_control_path_is_a_softmax_of_the_block_dequantized_logits():
+    # The scale of a score is qs[row // 64] * ks[key // 128] * sm (vc_reference.py:37-40):
+    # the control output stays within the E4M3 bound of the float64 softmax of those logits,
+    # and per-16-row or per-key-group scale indexing (the INT8 layout) would not.
+    gen = torch.Generator().manual_seed(31)
+    q = torch.randn(1, 1, 128, 64, generator=gen) * torch.tensor([1.0] * 64 + [4.0] * 64).view(1, 1, -1, 1)
+    k = torch.randn(1, 1, 300, 64, generator=gen)
+    k[:, :, 128:256] *= 0.125
+    v = torch.randn(1, 1, 300, 64, generator=gen)
+    s = o.prepare_fp8(*(bits(x.to(torch.bfloat16)) for x in (q, k, v)), expcast=False)
+    out = o.reference(s)[0, 0].astype(np.float64)
+    dq = o.e4m3_decode(s["q"][0, 0]).astype(np.float64) * np.repeat(s["qs"][0, 0], 64)[:128, None]
+    dk = o.e4m3_decode(s["k"][0, 0]).astype(np.float64) * np.repeat(s["ks"][0, 0], 128)[:300, None]
+    lg = dq @ dk.T * 0.125 * math.log2(math.e)
+    w = np.exp2(lg - lg.max(-1, keepdims=True) + 8.807)
+    dv = o.e4m3_decode(s["v"][0, 0, :, :300]).astype(np.float64) * s["vs"][0, 0, :, None]
+    exact = (w @ dv.T) / w.sum(-1, keepdims=True)
+    bound = ((2.0 ** -4 * w + 2.0 ** -10) @ np.abs(dv.T)) / w.sum(-1, keepdims=True)
+    assert np.all(np.abs(out - exact) <= bound + 1e-4)
+    # the check is sensitive to the scale indexing: K scales shifted by one tile break it
+    dk2 = o.e4m3_decode(s["k"][0, 0]).astype(np.float64) * np.repeat(np.roll(s["ks"][0, 0], 1), 128)[:300, None]
+    lg2 = dq @ dk2.T * 0.125 * math.log2(math.e)
+    w2 = np.exp2(lg2 - lg2.max(-1, keepdims=True) + 8.807)
+    wrong = (w2 @ dv.T) / w2.sum(-1, keepdims=True)
+    assert np.mean(np.abs(wrong - exact) > bound) > 0.3

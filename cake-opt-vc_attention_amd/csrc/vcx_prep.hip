@@ -176,9 +176,11 @@ __global__ __launch_bounds__(kThreads) void tile_stats_kernel(
 
 // grid (B*H), D threads. km = RN_in(RN_f32(sum over tiles / n)); also the
 // widened value for the K quantizer and, optionally, the caller's km_out.
-template <int DT>
+// RAW (FP8 block path, vc27): km = RN_f32(sum / n), written to km_f32 and, as binary32,
+// to the caller's km_out.
+template <int DT, bool RAW = false>
 __global__ void k_mean_kernel(const double* sums, int64_t tiles, int64_t n, int D, float* km_f32,
-                              uint16_t* km_out) {
+                              void* km_out) {
   const int64_t bh = blockIdx.x;
   const int ch = threadIdx.x;
   const double* col = sums + bh * tiles * D + ch;
@@ -196,9 +198,14 @@ __global__ void k_mean_kernel(const double* sums, int64_t tiles, int64_t n, int 
   }
   for (; t < tiles; ++t) s = __dadd_rn(s, col[t * D]);
   float mean = static_cast<float>(__ddiv_rn(s, static_cast<double>(n)));
-  uint32_t bits = f32_to_in<DT>(mean);
-  km_f32[bh * D + ch] = in_to_f32<DT>(bits);
-  if (km_out) km_out[bh * D + ch] = static_cast<uint16_t>(bits);
+  if constexpr (RAW) {
+    km_f32[bh * D + ch] = mean;
+    if (km_out) static_cast<float*>(km_out)[bh * D + ch] = mean;
+  } else {
+    uint32_t bits = f32_to_in<DT>(mean);
+    km_f32[bh * D + ch] = in_to_f32<DT>(bits);
+    if (km_out) static_cast<uint16_t*>(km_out)[bh * D + ch] = static_cast<uint16_t>(bits);
+  }
 }
 
 // grid (B*H), D threads. Smoothing off: vs = RN(amax/448), recip = RN(448/amax)
@@ -298,6 +305,71 @@ __global__ __launch_bounds__(kThreads) void quant_q_kernel(const void* q, int64_
       else *reinterpret_cast<uint32_t*>(dst) = packed[0];
     }
     if ((lane & 31) == 0) qs[bh * qs_len + (blk * 4 + g) * 8 + t] = s;
+  }
+}
+
+// ---------------------------------------------------------------- FP8 block Q/K (vc27)
+
+// grid (ceil(n/ROWS), B*H), 256 threads; one block of ROWS rows x D channels shares one
+// scale. Thread (rr = tid/16, c = tid%16) holds channels [c*CPT, c*CPT+CPT) of the rows
+// blk*ROWS + rr + 16*i. x' = CENTER ? RN(x - km) : x (binary32); s = max(RN(amax/448), 1e-12);
+// code = E4M3_satfinite(RN(x'/s)). Rows past n are not part of the block.
+// Reference: quantize_qk_fp8, sal/csrc/vc/qk_fp8.cu:38-74 (Q: 64 rows; K: 128 rows, centred).
+template <int DT, int D, int ROWS, bool CENTER>
+__global__ __launch_bounds__(kThreads) void quant_fp8_kernel(const void* x, int64_t H, int64_t n,
+                                                             int64_t sb, int64_t sh, int64_t sn,
+                                                             const float* km, uint8_t* codes, float* scales) {
+  constexpr int CPT = D / 16, NR = ROWS / 16;
+  __shared__ float wmax[kThreads / 64];
+  const int64_t blk = blockIdx.x, bh = blockIdx.y, blocks = gridDim.x;
+  const int tid = threadIdx.x, rr = tid >> 4, c = tid & 15, lane = tid & 63, w = tid >> 6;
+  const uint16_t* base = head_base(x, bh, H, sb, sh);
+  // Every row of the thread is loaded before any is used.
+  Row<D> rows[NR];
+#pragma unroll
+  for (int i = 0; i < NR; ++i) {
+    const int64_t row = blk * ROWS + rr + 16 * i;
+    load_row<D>(base, sn, row < n ? row : 0, c, rows[i]);
+  }
+  float mean[CPT];
+#pragma unroll
+  for (int j = 0; j < CPT; ++j) mean[j] = CENTER ? km[bh * D + c * CPT + j] : 0.0f;
+  float v[NR][CPT];
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NR; ++i) {
+    const bool valid = blk * ROWS + rr + 16 * i < n;
+#pragma unroll
+    for (int j = 0; j < CPT; ++j) {
+      float y = valid ? row_val<DT, D>(rows[i], j) : 0.0f;
+      if constexpr (CENTER) y = valid ? __fsub_rn(y, mean[j]) : 0.0f;
+      v[i][j] = y;
+      amax = fmaxf(amax, fabsf(y));
+    }
+  }
+#pragma unroll
+  for (int m = 1; m < 64; m <<= 1) amax = wave_xor_max(amax, m);
+  if (lane == 0) wmax[w] = amax;
+  __syncthreads();
+  amax = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+  const float s = fmaxf(__fdiv_rn(amax, 448.0f), 1e-12f);
+  if (tid == 0) scales[bh * blocks + blk] = s;
+#pragma unroll
+  for (int i = 0; i < NR; ++i) {
+    const int64_t row = blk * ROWS + rr + 16 * i;
+    if (row >= n) continue;
+    uint32_t packed[CPT / 4];
+#pragma unroll
+    for (int j = 0; j < CPT / 4; ++j) {
+      float y[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) y[e] = fminf(448.0f, fmaxf(-448.0f, __fdiv_rn(v[i][4 * j + e], s)));
+      int wv = __builtin_amdgcn_cvt_pk_fp8_f32(y[0], y[1], 0, false);
+      packed[j] = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(y[2], y[3], wv, true));
+    }
+    uint8_t* dst = codes + (bh * n + row) * D + c * CPT;
+    if constexpr (CPT == 8) *reinterpret_cast<uint2*>(dst) = make_uint2(packed[0], packed[1]);
+    else *reinterpret_cast<uint32_t*>(dst) = packed[0];
   }
 }
 
@@ -564,10 +636,48 @@ extern "C" int vcx_prepare_qk_int8(const void* q, const void* k, int dtype, int6
     tile_stats_kernel<DT, DD, kKSum><<<dim3(tiles, BH), kThreads, 0, st>>>(k, H, Nk, k_sb, k_sh, k_sn, perm,
                                                                           ksum, nullptr, nullptr);
     VCX_LAUNCHED("tile_stats_kernel<K>");
-    k_mean_kernel<DT><<<dim3(BH), DD, 0, st>>>(ksum, tiles, Nk, DD, km, static_cast<uint16_t*>(km_out));
+    k_mean_kernel<DT><<<dim3(BH), DD, 0, st>>>(ksum, tiles, Nk, DD, km, km_out);
     VCX_LAUNCHED("k_mean_kernel");
     quant_k_kernel<DT, DD><<<dim3(tiles, BH), kThreads, 0, st>>>(k, H, Nk, k_sb, k_sh, k_sn, perm, km, k8, ks);
     VCX_LAUNCHED("quant_k_kernel");
+    return VCX_OK;
+  });
+}
+
+extern "C" int vcx_prepare_qk_fp8(const void* q, const void* k, int dtype, int64_t B, int64_t H,
+                                  int64_t Nq, int64_t Nk, int64_t D, int64_t q_sb, int64_t q_sh,
+                                  int64_t q_sn, int64_t k_sb, int64_t k_sh, int64_t k_sn, uint8_t* q8,
+                                  float* qs, uint8_t* k8, float* ks, float* km_out, void* workspace,
+                                  size_t workspace_bytes, void* stream) {
+  if (int rc = check_shape(B, H, Nq, D)) return rc;
+  if (int rc = check_shape(B, H, Nk, D)) return rc;
+  VCX_REQUIRE(dtype == VCX_FLOAT16 || dtype == VCX_BFLOAT16, "dtype must be float16 or bfloat16");
+  if (int rc = check_input("q", q, B, H, Nq, D, q_sb, q_sh, q_sn)) return rc;
+  if (int rc = check_input("k", k, B, H, Nk, D, k_sb, k_sh, k_sn)) return rc;
+  VCX_REQUIRE(q8 && qs && k8 && ks, "output pointers must be non-null");
+  VCX_REQUIRE(aligned(q8, 8) && aligned(k8, 8), "q8/k8 must be 8-byte aligned");
+  VCX_REQUIRE(aligned(km_out, 4), "km_out misaligned");
+  const int64_t BH = B * H, tiles = cdiv(Nk, kTile);
+  VCX_REQUIRE(workspace != nullptr && aligned(workspace, 256), "workspace must be non-null and 256-byte aligned");
+  VCX_REQUIRE(workspace_bytes >= ws_prepare_qk(BH, Nk, D), "workspace too small: need %zu bytes",
+              ws_prepare_qk(BH, Nk, D));
+  auto* ws = static_cast<char*>(workspace);
+  double* ksum = reinterpret_cast<double*>(ws);
+  float* km = reinterpret_cast<float*>(ws + align_up(sizeof(double) * BH * tiles * D));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  return dispatch(dtype, D, [&](auto dt, auto dd) -> int {
+    constexpr int DT = decltype(dt)::value, DD = decltype(dd)::value;
+    quant_fp8_kernel<DT, DD, 64, false><<<dim3(cdiv(Nq, 64), BH), kThreads, 0, st>>>(q, H, Nq, q_sb, q_sh, q_sn,
+                                                                                   nullptr, q8, qs);
+    VCX_LAUNCHED("quant_fp8_kernel<Q>");
+    tile_stats_kernel<DT, DD, kKSum><<<dim3(tiles, BH), kThreads, 0, st>>>(k, H, Nk, k_sb, k_sh, k_sn, nullptr,
+                                                                          ksum, nullptr, nullptr);
+    VCX_LAUNCHED("tile_stats_kernel<K>");
+    k_mean_kernel<DT, true><<<dim3(BH), DD, 0, st>>>(ksum, tiles, Nk, DD, km, km_out);
+    VCX_LAUNCHED("k_mean_kernel");
+    quant_fp8_kernel<DT, DD, 128, true><<<dim3(tiles, BH), kThreads, 0, st>>>(k, H, Nk, k_sb, k_sh, k_sn, km, k8,
+                                                                              ks);
+    VCX_LAUNCHED("quant_fp8_kernel<K>");
     return VCX_OK;
   });
 }

@@ -42,6 +42,9 @@ def _declare(L):
     L.vcx_prepare_qk_int8.restype = i32
     L.vcx_prepare_qk_int8.argtypes = [P, P, i32, i64, i64, i64, i64, i64, i64, i64, i64, i64, i64, i64,
                                       P, P, P, P, P, P, P, ctypes.c_size_t, P]
+    L.vcx_prepare_qk_fp8.restype = i32
+    L.vcx_prepare_qk_fp8.argtypes = [P, P, i32, i64, i64, i64, i64, i64, i64, i64, i64, i64, i64, i64,
+                                     P, P, P, P, P, P, ctypes.c_size_t, P]
     L.vcx_prepare_v_fp8.restype = i32
     L.vcx_prepare_v_fp8.argtypes = [P, i32, i64, i64, i64, i64, i64, i64, i64, P, i32, i32, P, P, P, P,
                                     ctypes.c_size_t, P]
@@ -57,7 +60,7 @@ def _declare(L):
 
 
 EXPORTED = ("vcx_abi_version", "vcx_last_error", "vcx_value_token", "vcx_workspace_bytes",
-            "vcx_group_values", "vcx_prepare_qk_int8", "vcx_prepare_v_fp8", "vcx_attention_fwd",
+            "vcx_group_values", "vcx_prepare_qk_int8", "vcx_prepare_qk_fp8", "vcx_prepare_v_fp8", "vcx_attention_fwd",
             "vcx_expcast_codes", "vcx_convert_probe", "vcx_kernel_resources")
 
 
@@ -181,6 +184,30 @@ def prepare_qk(q, k, perm=None):
     _check(lib().vcx_prepare_qk_int8(_ptr(q), _ptr(k), _DTYPE[q.dtype], B, H, Nq, Nk, D, qsb, qsh, qsn,
                                      ksb, ksh, ksn, _ptr(perm), _ptr(q8), _ptr(qs), _ptr(k8), _ptr(ks), _ptr(km),
                                      _ptr(ws), ws.numel(), _stream(dev)), "vcx_prepare_qk_int8")
+    return q8, qs, k8, ks, km
+
+
+@torch.no_grad()
+def prepare_qk_fp8(q, k):
+    """Block-scaled E4M3 Q/K (Q 64-row blocks, centred K 128-row blocks):
+    (q8 uint8 [B,H,Nq,D], qs [B,H,ceil(Nq/64)], k8 uint8 [B,H,Nk,D], ks [B,H,ceil(Nk/128)],
+    km fp32 [B,H,D])."""
+    dev = _require_device(q, k)
+    if q.dtype not in _DTYPE or k.dtype != q.dtype:
+        raise VcxError("Q/K require matching float16/bfloat16")
+    B, H, Nq, D = q.shape
+    Nk = k.shape[2]
+    qsb, qsh, qsn = _strides4(q)
+    ksb, ksh, ksn = _strides4(k)
+    q8 = torch.empty((B, H, Nq, D), dtype=torch.uint8, device=dev)
+    k8 = torch.empty((B, H, Nk, D), dtype=torch.uint8, device=dev)
+    qs = torch.empty((B, H, (Nq + 63) // 64), dtype=torch.float32, device=dev)
+    ks = torch.empty((B, H, (Nk + 127) // 128), dtype=torch.float32, device=dev)
+    km = torch.empty((B, H, D), dtype=torch.float32, device=dev)
+    ws = _workspace(workspace_bytes(WS_PREPARE_QK, B, H, Nk, D), dev)
+    _check(lib().vcx_prepare_qk_fp8(_ptr(q), _ptr(k), _DTYPE[q.dtype], B, H, Nq, Nk, D, qsb, qsh, qsn,
+                                    ksb, ksh, ksn, _ptr(q8), _ptr(qs), _ptr(k8), _ptr(ks), _ptr(km),
+                                    _ptr(ws), ws.numel(), _stream(dev)), "vcx_prepare_qk_fp8")
     return q8, qs, k8, ks, km
 
 

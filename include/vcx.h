@@ -96,6 +96,20 @@ int vcx_prepare_qk_int8(const void* q, const void* k, int dtype, int64_t B, int6
                         const int64_t* perm, int8_t* q8, float* qs, int8_t* k8, float* ks,
                         void* km_out, void* workspace, size_t workspace_bytes, void* stream);
 
+/* Q/K block-scaled E4M3 (the experimental vc27 QK format). K is centred by its
+ * binary32 channel mean km = RN_f32(S/Nk) (S the fp64 sum in this library's fixed
+ * tile-tree order); Q in 64-row blocks, centred K in 128-row blocks, each block with
+ * one scale s = max(RN(amax/448), 1e-12) and codes E4M3_satfinite(RN(x/s)).
+ * Outputs: q8 [B,H,Nq,D], qs fp32 [B,H,ceil(Nq/64)], k8 [B,H,Nk,D], ks fp32
+ * [B,H,ceil(Nk/128)], km_out (nullable) fp32 [B,H,D]. Workspace: VCX_WS_PREPARE_QK.
+ * Replaces _vc_sm90.prepare_qk_fp8 (third_party/sageattention_local/csrc/vc/pybind.cpp:56,
+ * qk_fp8.cu:10-109). */
+int vcx_prepare_qk_fp8(const void* q, const void* k, int dtype, int64_t B, int64_t H,
+                       int64_t Nq, int64_t Nk, int64_t D, int64_t q_sb, int64_t q_sh,
+                       int64_t q_sn, int64_t k_sb, int64_t k_sh, int64_t k_sn, uint8_t* q8,
+                       float* qs, uint8_t* k8, float* ks, float* km_out, void* workspace,
+                       size_t workspace_bytes, void* stream);
+
 /* V to E4M3. smooth = 0: per-channel amax scale (vs [B,H,D], means unused).
  * smooth = 1: 128-token block-mean residuals with per-channel (channel_scale=1,
  * vs [B,H,D]) or per-block (channel_scale=0, vs [B,H,tiles,D]) scales and

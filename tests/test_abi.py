@@ -74,6 +74,11 @@ def test_invalid_calls_rejected_before_launch():
     rc, msg = _fwd(block_values=0, channel_scale=0)
     assert rc == 1 and "per-block" in msg
     L = vcx.lib()
+    assert L.vcx_prepare_qk_fp8(None, None, 1, 1, 1, 64, 128, 96, 0, 0, 96, 0, 0, 96,
+                                None, None, None, None, None, None, 0, None) == 1
+    assert "D must be 64 or 128" in L.vcx_last_error().decode()
+    assert L.vcx_prepare_qk_fp8(None, None, 1, 1, 1, 64, 128, 128, 0, 0, 128, 0, 0, 128,
+                                None, None, None, None, None, None, 0, None) == 1
     assert L.vcx_expcast_codes(None, None, -1, None) == 1
     assert L.vcx_group_values(None, 1, 1, 1, 10, 128, 0, 0, 128, 9, 2, None, None, None, None, 0, None) == 2
     assert "8 effective clusters" in L.vcx_last_error().decode()

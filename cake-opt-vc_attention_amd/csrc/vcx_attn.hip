@@ -33,12 +33,20 @@
 // unfused code above for a whole 16-row group in a tile where some |m'| > 128, a scale
 // underflows or a gain overflows (the reference's warp-wide fallback).
 //
+// QF = 1 is the block-scaled FP8 QK format (the reference's experimental vc27,
+// sal/sageattention_local/vc_fp8.py, fp8_dispatch.cuh): E4M3 Q/K with one scale per
+// 64 query rows and one per 128-key tile, scores from v_mfma_f32_16x16x128_f8f6f4 (the
+// same K/Q fragment loads, two 16-byte halves per lane; D64 pads the second half with
+// zeros), V per-channel E4M3 with no block values, and the PM 0/1/2 probability paths.
+//
 // PM = 0 is the Sage FP8 control path (expcast=False; vc_sm90.cu:177,
 // attn_utils.cuh:355-455): a.sm = RN(sm * RN(log2 e)), base/factor as above,
 // m' = max(m, max fmaf(base, factor, -8.807)), P = E4M3(exp2(fmaf(base, factor, -m'))),
 // den and the mean restore use the unrounded sum of P. exp2 is v_exp_f32, so a P
 // byte can differ by one code from an exactly rounded exp2 next to a midpoint.
 #include "vcx_common.hpp"
+
+#include <type_traits>
 
 namespace vcx {
 namespace {
@@ -94,12 +102,13 @@ __device__ inline __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t by
 // Value modes: VM 0 = no smoothing (per-channel V scale in the epilogue),
 // 1 = block-mean smoothing with per-channel scales, 2 = block-mean smoothing
 // with per-block scales (applied to every tile's contribution).
-template <int D, int VM>
+template <int D, int VM, int QF = 0>
 struct TileLoader {
   static constexpr bool SMOOTH = VM >= 1, BSCALE = VM == 2;
   // Meta region of a buffer: SMOOTH ? fp16 means of the tile (2*D bytes) : nothing,
   // then BSCALE ? the tile's fp32 V scales (4*D bytes) : nothing, then the tile's
-  // 4 K scales (16 bytes). Means and K scales are loaded by wave 0, V scales by wave 1.
+  // K scales (INT8: 4 Sage key-group scales, 16 bytes; FP8 block: one scale, 4 bytes).
+  // Means and K scales are loaded by wave 0, V scales by wave 1.
   static constexpr int ML = SMOOTH ? (2 * D) / 16 : 0;
   static constexpr int VL = BSCALE ? (4 * D) / 16 : 0;
   static constexpr int VS_OFF = 16 * ML;
@@ -127,7 +136,8 @@ struct TileLoader {
     // Per-head resources. K rows past Nk read zeros (their logits are masked anyway).
     rk = make_rsrc(a.k8 + bh * a.Nk * D, static_cast<uint32_t>(a.Nk * D));
     rv = make_rsrc(a.v8 + bh * D * npad, static_cast<uint32_t>(D * npad));
-    rs = make_rsrc(a.ks + bh * a.tiles * 4, static_cast<uint32_t>(a.tiles * 16));
+    if constexpr (QF == 1) rs = make_rsrc(a.ks + bh * a.tiles, static_cast<uint32_t>(a.tiles * 4));
+    else rs = make_rsrc(a.ks + bh * a.tiles * 4, static_cast<uint32_t>(a.tiles * 16));
     if constexpr (SMOOTH) rm = make_rsrc(a.means + bh * a.tiles * D, static_cast<uint32_t>(a.tiles * D * 2));
     if constexpr (BSCALE) rb = make_rsrc(a.vs + bh * a.tiles * D, static_cast<uint32_t>(a.tiles * D * 4));
     moff = static_cast<uint32_t>(lane * 16);
@@ -142,8 +152,12 @@ struct TileLoader {
         if (lane < ML)
           __builtin_amdgcn_raw_ptr_buffer_load_lds(rm, (lds_void*)lm, 16, moff, static_cast<int>(t * D * 2), 0, 0);
       }
-      if (lane == 0)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)(lm + KS_OFF), 16, 0, static_cast<int>(t * 16), 0, 0);
+      if (lane == 0) {
+        if constexpr (QF == 1)
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)(lm + KS_OFF), 4, 0, static_cast<int>(t * 4), 0, 0);
+        else
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)(lm + KS_OFF), 16, 0, static_cast<int>(t * 16), 0, 0);
+      }
     }
     if constexpr (BSCALE) {
       if (wave == 1 && lane < VL)
@@ -189,13 +203,20 @@ constexpr float kFp8Offset = 8.807f;
 constexpr int kBias = 0x4B400000;
 constexpr float kBiasF = 12582912.0f;
 
-template <int D, int VM, bool DUMP, int PM>
+// Score of accumulator element r: FP8 scores are floats already; the folded path's
+// INT8 accumulators carry the kBias offset.
+__device__ inline float acc_value(const v4f& acc, int r) { return acc[r]; }
+__device__ inline float acc_value(const v4i& acc, int r) { return __int_as_float(acc[r]) - kBiasF; }
+
+template <int D, int VM, bool DUMP, int PM, int QF = 0>
 struct Wave {
   static constexpr bool EC = PM != 0;  // ExpCast bytes (1 unfused, 2 folded) or the control path (0)
+  static constexpr bool IB = PM == 2 && QF == 0;  // biased INT8 accumulators (folded path)
   static constexpr int DS = D / 64;  // 64-deep QK steps
   static constexpr int CB = D / 16;  // 16-channel output blocks
   static constexpr bool SMOOTH = VM >= 1, BSCALE = VM == 2;
-  typedef TileLoader<D, VM> LD;
+  typedef TileLoader<D, VM, QF> LD;
+  typedef std::conditional_t<QF == 1, v4f, v4i> Acc;  // 16x16 score accumulator
 
   v4i qf[2][DS];
   float qsv[2];
@@ -214,10 +235,10 @@ struct Wave {
 
   template <bool LAST>
   __device__ inline void tile(const AttnArgs& a, int64_t t, const uint8_t* lk, const uint8_t* lv, const uint8_t* lm) {
-    const float ksv = *reinterpret_cast<const float*>(lm + LD::KS_OFF + 4 * G);
+    const float ksv = *reinterpret_cast<const float*>(lm + LD::KS_OFF + (QF == 1 ? 0 : 4 * G));
 
     // ---- S^T = K Q^T
-    v4i S[2][8];
+    Acc S[2][8];
     v4i kf[8][DS];
 #pragma unroll
     for (int j = 0; j < 2; ++j)
@@ -231,10 +252,22 @@ struct Wave {
       }
 #pragma unroll
       for (int qg = 0; qg < 2; ++qg) {
-        v4i acc = PM == 2 ? v4i{kBias, kBias, kBias, kBias} : v4i{0, 0, 0, 0};
+        if constexpr (QF == 1) {
+          // E4M3 x E4M3 over all D channels in one 128-deep step; lane group G holds the
+          // channel sets {16G..16G+15} and {64+16G..64+16G+15} for both operands.
+          const v8i ka = DS == 2 ? v8i{kf[j][0][0], kf[j][0][1], kf[j][0][2], kf[j][0][3],
+                                       kf[j][DS - 1][0], kf[j][DS - 1][1], kf[j][DS - 1][2], kf[j][DS - 1][3]}
+                                 : v8i{kf[j][0][0], kf[j][0][1], kf[j][0][2], kf[j][0][3], 0, 0, 0, 0};
+          const v8i qb = DS == 2 ? v8i{qf[qg][0][0], qf[qg][0][1], qf[qg][0][2], qf[qg][0][3],
+                                       qf[qg][DS - 1][0], qf[qg][DS - 1][1], qf[qg][DS - 1][2], qf[qg][DS - 1][3]}
+                                 : v8i{qf[qg][0][0], qf[qg][0][1], qf[qg][0][2], qf[qg][0][3], 0, 0, 0, 0};
+          S[qg][j] = mfma_fp8(ka, qb, v4f{0.0f, 0.0f, 0.0f, 0.0f});
+        } else {
+          v4i acc = IB ? v4i{kBias, kBias, kBias, kBias} : v4i{0, 0, 0, 0};
 #pragma unroll
-        for (int ds = 0; ds < DS; ++ds) acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(kf[j][ds], qf[qg][ds], acc, 0, 0, 0);
-        S[qg][j] = acc;
+          for (int ds = 0; ds < DS; ++ds) acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(kf[j][ds], qf[qg][ds], acc, 0, 0, 0);
+          S[qg][j] = acc;
+        }
       }
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -254,7 +287,18 @@ struct Wave {
         const float dq = qsv[qg] * ksv;
         const float scale = LAST ? a.sm : a.sm * dq;
         float tmax;
-        if constexpr (!LAST) {
+        if constexpr (!LAST && QF == 1) {
+          // scale > 0, so RN(max(base) * scale) is the maximum of the rounded logits
+          float bm = -INFINITY;
+#pragma unroll
+          for (int j = 0; j < 8; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              bs[j][r] = S[qg][j][r];
+              bm = fmaxf(bm, bs[j][r]);
+            }
+          tmax = bm * scale;
+        } else if constexpr (!LAST) {
           // float(acc) is exact and monotone: the row maximum is taken on the integers
           int im = S[qg][0][0];
 #pragma unroll
@@ -272,7 +316,8 @@ struct Wave {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
               const int64_t key = t * kTile + 16 * j + 8 * (r >> 1) + 2 * G + (r & 1);
-              bs[j][r] = key < a.Nk ? (__int_as_float(S[qg][j][r]) - kBiasF) * dq : -INFINITY;
+              const float f = acc_value(S[qg][j], r);
+              bs[j][r] = key < a.Nk ? f * dq : -INFINITY;
               bm = fmaxf(bm, bs[j][r]);
             }
           tmax = bm * scale;
@@ -470,9 +515,10 @@ struct Wave {
   }
 };
 
-template <int D, int VM, bool DUMP, int OUT, int PM>
+template <int D, int VM, bool DUMP, int OUT, int PM, int QF = 0>
 __global__ __launch_bounds__(kThreadsPerBlock, 2) void attn_kernel(AttnArgs a) {
-  typedef TileLoader<D, VM> LD;
+  typedef TileLoader<D, VM, QF> LD;
+  typedef Wave<D, VM, DUMP, PM, QF> W;
   constexpr int KB = kTile * D, VB = D * kTile;
   __shared__ __attribute__((aligned(16))) uint8_t lds0[KB + VB];
   __shared__ __attribute__((aligned(16))) uint8_t lds1[KB + VB];
@@ -487,14 +533,14 @@ __global__ __launch_bounds__(kThreadsPerBlock, 2) void attn_kernel(AttnArgs a) {
   const int64_t bh = logical / a.qblocks, qb = logical % a.qblocks;
 
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  Wave<D, VM, DUMP, PM> w;
+  W w;
   w.G = lane >> 4;
   w.li = lane & 15;
   w.bh_ = bh;
   // Lane-constant LDS offsets.
   const int kr = 8 * ((w.li & 3) >> 1) + 2 * (w.li >> 2) + (w.li & 1);
 #pragma unroll
-  for (int ds = 0; ds < Wave<D, VM, DUMP, PM>::DS; ++ds)
+  for (int ds = 0; ds < W::DS; ++ds)
     w.koff[ds] = kr * D + ((((D == 128) ? 4 * ds : 0) + w.G) ^ swz_k<D>(kr)) * 16;
 #pragma unroll
   for (int h = 0; h < 2; ++h) w.voff[h] = w.li * kTile + (((2 * w.G + h) ^ swz_v(w.li)) * 16);
@@ -504,17 +550,18 @@ __global__ __launch_bounds__(kThreadsPerBlock, 2) void attn_kernel(AttnArgs a) {
   for (int qg = 0; qg < 2; ++qg) {
     const int64_t r = qb * kRowsPerBlock + wave * 32 + qg * 16 + w.li;
     w.row[qg] = r;
-    const int64_t si = (r / 16) * 8 + r % 8;
+    // Q scale: Sage per-thread INT8 index (row/16)*8 + row%8, or the FP8 row block row/64
+    const int64_t si = QF == 1 ? r / 64 : (r / 16) * 8 + r % 8;
     w.qsv[qg] = si < a.qs_len ? a.qs[bh * a.qs_len + si] : 1.0f;
 #pragma unroll
-    for (int ds = 0; ds < Wave<D, VM, DUMP, PM>::DS; ++ds) {
+    for (int ds = 0; ds < W::DS; ++ds) {
       if (r < a.Nq) w.qf[qg][ds] = *reinterpret_cast<const v4i*>(a.q8 + (bh * a.Nq + r) * D + ds * 64 + w.G * 16);
       else w.qf[qg][ds] = v4i{0, 0, 0, 0};
     }
     w.m[qg] = -5000000.0f;
     w.den[qg] = 0.0f;
 #pragma unroll
-    for (int cb = 0; cb < Wave<D, VM, DUMP, PM>::CB; ++cb) w.O[qg][cb] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int cb = 0; cb < W::CB; ++cb) w.O[qg][cb] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
   }
 
   LD ld;
@@ -553,10 +600,10 @@ __global__ __launch_bounds__(kThreadsPerBlock, 2) void attn_kernel(AttnArgs a) {
     const float inv = 1.0f / w.den[qg];
     uint16_t* out = static_cast<uint16_t*>(a.out) + b * a.osb + h * a.osh + w.row[qg] * a.osn;
 #pragma unroll
-    for (int cb = 0; cb < Wave<D, VM, DUMP, PM>::CB; ++cb) {
+    for (int cb = 0; cb < W::CB; ++cb) {
       const int ch = 16 * cb + 4 * w.G;
       // per-channel V scale (per-block scales were applied tile by tile)
-      const float4 sc = Wave<D, VM, DUMP, PM>::BSCALE ? make_float4(1.0f, 1.0f, 1.0f, 1.0f)
+      const float4 sc = W::BSCALE ? make_float4(1.0f, 1.0f, 1.0f, 1.0f)
                                                   : *reinterpret_cast<const float4*>(a.vs + bh * D + ch);
       const float y0 = w.O[qg][cb][0] * inv * sc.x, y1 = w.O[qg][cb][1] * inv * sc.y;
       const float y2 = w.O[qg][cb][2] * inv * sc.z, y3 = w.O[qg][cb][3] * inv * sc.w;
@@ -632,29 +679,75 @@ template __global__ void attn_kernel<128, 2, false, 1, 0>(AttnArgs);
 template __global__ void attn_kernel<128, 2, true, 0, 0>(AttnArgs);
 template __global__ void attn_kernel<128, 2, true, 1, 0>(AttnArgs);
 
-template <int D, int VM, bool DUMP, int OUT, int PM>
+template __global__ void attn_kernel<64, 0, false, 0, 2, 1>(AttnArgs);
+template __global__ void attn_kernel<64, 0, false, 1, 2, 1>(AttnArgs);
+template __global__ void attn_kernel<64, 0, true, 0, 2, 1>(AttnArgs);
+template __global__ void attn_kernel<64, 0, true, 1, 2, 1>(AttnArgs);
+template __global__ void attn_kernel<128, 0, false, 0, 2, 1>(AttnArgs);
+template __global__ void attn_kernel<128, 0, false, 1, 2, 1>(AttnArgs);
+template __global__ void attn_kernel<128, 0, true, 0, 2, 1>(AttnArgs);
+template __global__ void attn_kernel<128, 0, true, 1, 2, 1>(AttnArgs);
+template __global__ void attn_kernel<64, 0, false, 0, 1, 1>(AttnArgs);
+template __global__ void attn_kernel<64, 0, false, 1, 1, 1>(AttnArgs);
+template __global__ void attn_kernel<64, 0, true, 0, 1, 1>(AttnArgs);
+template __global__ void attn_kernel<64, 0, true, 1, 1, 1>(AttnArgs);
+template __global__ void attn_kernel<128, 0, false, 0, 1, 1>(AttnArgs);
+template __global__ void attn_kernel<128, 0, false, 1, 1, 1>(AttnArgs);
+template __global__ void attn_kernel<128, 0, true, 0, 1, 1>(AttnArgs);
+template __global__ void attn_kernel<128, 0, true, 1, 1, 1>(AttnArgs);
+template __global__ void attn_kernel<64, 0, false, 0, 0, 1>(AttnArgs);
+template __global__ void attn_kernel<64, 0, false, 1, 0, 1>(AttnArgs);
+template __global__ void attn_kernel<64, 0, true, 0, 0, 1>(AttnArgs);
+template __global__ void attn_kernel<64, 0, true, 1, 0, 1>(AttnArgs);
+template __global__ void attn_kernel<128, 0, false, 0, 0, 1>(AttnArgs);
+template __global__ void attn_kernel<128, 0, false, 1, 0, 1>(AttnArgs);
+template __global__ void attn_kernel<128, 0, true, 0, 0, 1>(AttnArgs);
+template __global__ void attn_kernel<128, 0, true, 1, 0, 1>(AttnArgs);
+
+template <int D, int VM, bool DUMP, int OUT, int PM, int QF>
 int launch(const AttnArgs& a, int64_t nblocks, hipStream_t st) {
-  attn_kernel<D, VM, DUMP, OUT, PM><<<dim3(static_cast<unsigned>(nblocks)), kThreadsPerBlock, 0, st>>>(a);
+  attn_kernel<D, VM, DUMP, OUT, PM, QF><<<dim3(static_cast<unsigned>(nblocks)), kThreadsPerBlock, 0, st>>>(a);
   return check_launch("attn_kernel");
 }
 
-template <int D, int VM, int PM>
+template <int D, int VM, int PM, int QF>
 int launch_out(const AttnArgs& a, int64_t nblocks, bool dump, int out_dtype, hipStream_t st) {
   if (dump) {
-    return out_dtype == VCX_BFLOAT16 ? launch<D, VM, true, VCX_BFLOAT16, PM>(a, nblocks, st)
-                                     : launch<D, VM, true, VCX_FLOAT16, PM>(a, nblocks, st);
+    return out_dtype == VCX_BFLOAT16 ? launch<D, VM, true, VCX_BFLOAT16, PM, QF>(a, nblocks, st)
+                                     : launch<D, VM, true, VCX_FLOAT16, PM, QF>(a, nblocks, st);
   }
-  return out_dtype == VCX_BFLOAT16 ? launch<D, VM, false, VCX_BFLOAT16, PM>(a, nblocks, st)
-                                   : launch<D, VM, false, VCX_FLOAT16, PM>(a, nblocks, st);
+  return out_dtype == VCX_BFLOAT16 ? launch<D, VM, false, VCX_BFLOAT16, PM, QF>(a, nblocks, st)
+                                   : launch<D, VM, false, VCX_FLOAT16, PM, QF>(a, nblocks, st);
 }
 
-template <int D, int VM>
+template <int D, int VM, int QF = 0>
 int launch_mode(const AttnArgs& a, int64_t nblocks, bool dump, int out_dtype, int mode, hipStream_t st) {
   if constexpr (VM == 0) {
-    if (mode == 2) return launch_out<D, VM, 2>(a, nblocks, dump, out_dtype, st);
+    if (mode == 2) return launch_out<D, VM, 2, QF>(a, nblocks, dump, out_dtype, st);
   }
-  return mode == 1 ? launch_out<D, VM, 1>(a, nblocks, dump, out_dtype, st)
-                   : launch_out<D, VM, 0>(a, nblocks, dump, out_dtype, st);
+  return mode == 1 ? launch_out<D, VM, 1, QF>(a, nblocks, dump, out_dtype, st)
+                   : launch_out<D, VM, 0, QF>(a, nblocks, dump, out_dtype, st);
+}
+
+// Argument checks shared by the INT8 and FP8 block entry points.
+int check_common(int64_t B, int64_t H, int64_t Nq, int64_t Nk, int64_t D, int expcast, int out_dtype,
+                 float sm_scale, void* out, int64_t o_sb, int64_t o_sh, int64_t o_sn, const uint8_t* p_dump,
+                 int64_t p_row_begin, int64_t p_row_end) {
+  VCX_REQUIRE(B >= 1 && H >= 1 && Nq >= 1 && Nk >= 1, "B, H, Nq, Nk must be positive");
+  VCX_REQUIRE(D == 64 || D == 128, "D must be 64 or 128");
+  VCX_REQUIRE(B * H <= 65535, "B*H exceeds 65535");
+  VCX_REQUIRE(Nq < (int64_t(1) << 30) && Nk < (int64_t(1) << 30), "sequence too long");
+  VCX_REQUIRE(cdiv(Nk, kTile) * kTile * D < (int64_t(1) << 31), "K/V payload of one head must be below 2 GiB");
+  VCX_REQUIRE(expcast >= 0 && expcast <= 2, "expcast must be 0, 1 or 2");
+  VCX_REQUIRE(out_dtype == VCX_FLOAT16 || out_dtype == VCX_BFLOAT16, "out_dtype must be float16 or bfloat16");
+  VCX_REQUIRE(std::isfinite(sm_scale) && sm_scale > 0.0f, "sm_scale must be positive and finite FP32");
+  VCX_REQUIRE(aligned(out, 8) && o_sb % 4 == 0 && o_sh % 4 == 0 && o_sn % 4 == 0 && o_sn >= D && o_sb >= 0 &&
+                  o_sh >= 0,
+              "out must be 8-byte aligned with strides that are multiples of 4 elements and sn >= D");
+  if (p_dump) {
+    VCX_REQUIRE(p_row_begin >= 0 && p_row_begin < p_row_end && p_row_end <= Nq, "invalid P dump row range");
+  }
+  return VCX_OK;
 }
 
 }  // namespace
@@ -668,27 +761,16 @@ extern "C" int vcx_attention_fwd(const int8_t* q8, const int8_t* k8, const uint8
                                  int block_values, int channel_scale, float sm_scale, int out_dtype,
                                  void* out, int64_t o_sb, int64_t o_sh, int64_t o_sn, uint8_t* p_dump,
                                  int64_t p_row_begin, int64_t p_row_end, void* stream) {
-  VCX_REQUIRE(B >= 1 && H >= 1 && Nq >= 1 && Nk >= 1, "B, H, Nq, Nk must be positive");
-  VCX_REQUIRE(D == 64 || D == 128, "D must be 64 or 128");
-  VCX_REQUIRE(B * H <= 65535, "B*H exceeds 65535");
-  VCX_REQUIRE(Nq < (int64_t(1) << 30) && Nk < (int64_t(1) << 30), "sequence too long");
-  VCX_REQUIRE(cdiv(Nk, kTile) * kTile * D < (int64_t(1) << 31), "K/V payload of one head must be below 2 GiB");
-  VCX_REQUIRE(expcast >= 0 && expcast <= 2, "expcast must be 0, 1 or 2");
+  if (int rc = check_common(B, H, Nq, Nk, D, expcast, out_dtype, sm_scale, out, o_sb, o_sh, o_sn, p_dump,
+                            p_row_begin, p_row_end))
+    return rc;
   VCX_REQUIRE(expcast != 2 || !block_values, "the folded ExpCast encode (expcast = 2) is defined without block values");
   VCX_REQUIRE(block_values || channel_scale, "per-block V scales require block values (smoothing)");
-  VCX_REQUIRE(out_dtype == VCX_FLOAT16 || out_dtype == VCX_BFLOAT16, "out_dtype must be float16 or bfloat16");
-  VCX_REQUIRE(std::isfinite(sm_scale) && sm_scale > 0.0f, "sm_scale must be positive and finite FP32");
   VCX_REQUIRE(q8 && k8 && v8 && qs && ks && vs && out, "null tensor pointer");
   VCX_REQUIRE(!block_values || means, "means must be non-null with block values");
   VCX_REQUIRE(aligned(q8, 16) && aligned(k8, 16) && aligned(v8, 16), "q8/k8/v8 must be 16-byte aligned");
   VCX_REQUIRE(aligned(qs, 4) && aligned(ks, 4) && aligned(vs, 16), "scale pointer alignment (vs needs 16 bytes)");
   VCX_REQUIRE(!block_values || aligned(means, 8), "means must be 8-byte aligned");
-  VCX_REQUIRE(aligned(out, 8) && o_sb % 4 == 0 && o_sh % 4 == 0 && o_sn % 4 == 0 && o_sn >= D && o_sb >= 0 &&
-                  o_sh >= 0,
-              "out must be 8-byte aligned with strides that are multiples of 4 elements and sn >= D");
-  if (p_dump) {
-    VCX_REQUIRE(p_row_begin >= 0 && p_row_begin < p_row_end && p_row_end <= Nq, "invalid P dump row range");
-  }
   AttnArgs a{};
   a.q8 = q8; a.k8 = k8; a.v8 = v8; a.qs = qs; a.ks = ks; a.vs = vs; a.means = means; a.out = out;
   a.osb = o_sb; a.osh = o_sh; a.osn = o_sn;
@@ -711,15 +793,36 @@ extern "C" int vcx_attention_fwd(const int8_t* q8, const int8_t* k8, const uint8
                        : launch_mode<64, 2>(a, nblocks, dump, out_dtype, expcast, st);
 }
 
-extern "C" int vcx_kernel_resources(int64_t D, int block_values, int64_t* out) {
-  VCX_REQUIRE(out != nullptr, "out is null");
-  VCX_REQUIRE(D == 64 || D == 128, "D must be 64 or 128");
+extern "C" int vcx_attention_fwd_fp8(const uint8_t* q8, const uint8_t* k8, const uint8_t* v8, const float* qs,
+                                     const float* ks, const float* vs, int64_t B, int64_t H, int64_t Nq,
+                                     int64_t Nk, int64_t D, int expcast, float sm_scale, int out_dtype, void* out,
+                                     int64_t o_sb, int64_t o_sh, int64_t o_sn, uint8_t* p_dump,
+                                     int64_t p_row_begin, int64_t p_row_end, void* stream) {
+  if (int rc = check_common(B, H, Nq, Nk, D, expcast, out_dtype, sm_scale, out, o_sb, o_sh, o_sn, p_dump,
+                            p_row_begin, p_row_end))
+    return rc;
+  VCX_REQUIRE(q8 && k8 && v8 && qs && ks && vs && out, "null tensor pointer");
+  VCX_REQUIRE(aligned(q8, 16) && aligned(k8, 16) && aligned(v8, 16), "q8/k8/v8 must be 16-byte aligned");
+  VCX_REQUIRE(aligned(qs, 4) && aligned(ks, 4) && aligned(vs, 16), "scale pointer alignment (vs needs 16 bytes)");
+  AttnArgs a{};
+  a.q8 = reinterpret_cast<const int8_t*>(q8); a.k8 = reinterpret_cast<const int8_t*>(k8); a.v8 = v8;
+  a.qs = qs; a.ks = ks; a.vs = vs; a.means = nullptr; a.out = out;
+  a.osb = o_sb; a.osh = o_sh; a.osn = o_sn;
+  a.H = H; a.Nq = Nq; a.Nk = Nk; a.tiles = cdiv(Nk, kTile); a.qblocks = cdiv(Nq, kRowsPerBlock);
+  a.qs_len = cdiv(Nq, 64);
+  a.sm = expcast != 0 ? sm_scale : sm_scale * 1.4426950408889634f;
+  a.pdump = p_dump; a.prow0 = p_row_begin; a.prow1 = p_row_end;
+  const int64_t nblocks = B * H * a.qblocks;
+  VCX_REQUIRE(nblocks < (int64_t(1) << 31), "too many blocks");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const bool dump = p_dump != nullptr;
+  return D == 128 ? launch_mode<128, 0, 1>(a, nblocks, dump, out_dtype, expcast, st)
+                  : launch_mode<64, 0, 1>(a, nblocks, dump, out_dtype, expcast, st);
+}
+
+namespace {
+int resources_of(const void* fn, int64_t* out) {
   hipFuncAttributes attr{};
-  const void* fn;
-  if (D == 128) fn = block_values ? reinterpret_cast<const void*>(&attn_kernel<128, 1, false, VCX_BFLOAT16, 1>)
-                                  : reinterpret_cast<const void*>(&attn_kernel<128, 0, false, VCX_BFLOAT16, 2>);
-  else fn = block_values ? reinterpret_cast<const void*>(&attn_kernel<64, 1, false, VCX_BFLOAT16, 1>)
-                         : reinterpret_cast<const void*>(&attn_kernel<64, 0, false, VCX_BFLOAT16, 2>);
   hipError_t e = hipFuncGetAttributes(&attr, fn);
   if (e != hipSuccess) return fail(VCX_EHIP, "hipFuncGetAttributes: %s", hipGetErrorString(e));
   out[0] = attr.numRegs;
@@ -729,4 +832,27 @@ extern "C" int vcx_kernel_resources(int64_t D, int block_values, int64_t* out) {
   out[4] = attr.maxThreadsPerBlock;
   out[5] = static_cast<int64_t>(attr.localSizeBytes);
   return VCX_OK;
+}
+}  // namespace
+
+extern "C" int vcx_kernel_resources(int64_t D, int block_values, int64_t* out) {
+  VCX_REQUIRE(out != nullptr, "out is null");
+  VCX_REQUIRE(D == 64 || D == 128, "D must be 64 or 128");
+  const void* fn;
+  if (D == 128) fn = block_values ? reinterpret_cast<const void*>(&attn_kernel<128, 1, false, VCX_BFLOAT16, 1>)
+                                  : reinterpret_cast<const void*>(&attn_kernel<128, 0, false, VCX_BFLOAT16, 2>);
+  else fn = block_values ? reinterpret_cast<const void*>(&attn_kernel<64, 1, false, VCX_BFLOAT16, 1>)
+                         : reinterpret_cast<const void*>(&attn_kernel<64, 0, false, VCX_BFLOAT16, 2>);
+  return resources_of(fn, out);
+}
+
+extern "C" int vcx_kernel_resources_fp8(int64_t D, int expcast, int64_t* out) {
+  VCX_REQUIRE(out != nullptr, "out is null");
+  VCX_REQUIRE(D == 64 || D == 128, "D must be 64 or 128");
+  const void* fn;
+  if (D == 128) fn = expcast ? reinterpret_cast<const void*>(&attn_kernel<128, 0, false, VCX_BFLOAT16, 2, 1>)
+                             : reinterpret_cast<const void*>(&attn_kernel<128, 0, false, VCX_BFLOAT16, 0, 1>);
+  else fn = expcast ? reinterpret_cast<const void*>(&attn_kernel<64, 0, false, VCX_BFLOAT16, 2, 1>)
+                    : reinterpret_cast<const void*>(&attn_kernel<64, 0, false, VCX_BFLOAT16, 0, 1>);
+  return resources_of(fn, out);
 }

@@ -51,17 +51,22 @@ def _declare(L):
     L.vcx_attention_fwd.restype = i32
     L.vcx_attention_fwd.argtypes = [P, P, P, P, P, P, P, i64, i64, i64, i64, i64, i32, i32, i32, f32, i32,
                                     P, i64, i64, i64, P, i64, i64, P]
+    L.vcx_attention_fwd_fp8.restype = i32
+    L.vcx_attention_fwd_fp8.argtypes = [P, P, P, P, P, P, i64, i64, i64, i64, i64, i32, f32, i32,
+                                        P, i64, i64, i64, P, i64, i64, P]
     L.vcx_expcast_codes.restype = i32
     L.vcx_expcast_codes.argtypes = [P, P, i64, P]
     L.vcx_convert_probe.restype = i32
     L.vcx_convert_probe.argtypes = [P, P, P, i64, P]
     L.vcx_kernel_resources.restype = i32
     L.vcx_kernel_resources.argtypes = [i64, i32, ctypes.POINTER(ctypes.c_int64)]
+    L.vcx_kernel_resources_fp8.restype = i32
+    L.vcx_kernel_resources_fp8.argtypes = [i64, i32, ctypes.POINTER(ctypes.c_int64)]
 
 
 EXPORTED = ("vcx_abi_version", "vcx_last_error", "vcx_value_token", "vcx_workspace_bytes",
-            "vcx_group_values", "vcx_prepare_qk_int8", "vcx_prepare_qk_fp8", "vcx_prepare_v_fp8", "vcx_attention_fwd",
-            "vcx_expcast_codes", "vcx_convert_probe", "vcx_kernel_resources")
+            "vcx_group_values", "vcx_prepare_qk_int8", "vcx_prepare_qk_fp8", "vcx_prepare_v_fp8", "vcx_attention_fwd", "vcx_attention_fwd_fp8",
+            "vcx_expcast_codes", "vcx_convert_probe", "vcx_kernel_resources", "vcx_kernel_resources_fp8")
 
 
 def lib():
@@ -292,6 +297,48 @@ def forward(q8, k8, v8, qs, ks, vs, means, expcast: bool, block_values: bool, ou
 
 
 @torch.no_grad()
+def forward_fp8(q8, k8, v8, qs, ks, vs, expcast: bool, output_type: int, scale: float,
+                *, affine: bool = True, out=None, p_rows=None):
+    """Fused attention on block-scaled FP8 Q/K payloads (vcx.prepare_qk_fp8) and the
+    per-channel V payload (vcx.prepare_v) -> out [B,H,Nq,D].
+
+    expcast=True folds the ExpCast encode (affine=True, the reference's FP8 kernel) or
+    runs the unfused encode (affine=False); expcast=False runs the Sage FP8 control
+    probabilities. p_rows as in forward().
+    """
+    dev = _require_device(q8, k8, v8, qs, ks, vs)
+    B, H, Nq, D = q8.shape
+    Nk = k8.shape[2]
+    tiles = (Nk + 127) // 128
+    for name, t in (("q", q8), ("k", k8), ("v", v8)):
+        if t.dtype not in (torch.float8_e4m3fn, torch.uint8) or not t.is_contiguous():
+            raise VcxError(f"{name} must be contiguous float8_e4m3fn")
+    for name, t in (("qs", qs), ("ks", ks), ("vs", vs)):
+        if t.dtype != torch.float32 or not t.is_contiguous():
+            raise VcxError(f"{name} must be contiguous float32")
+    if tuple(k8.shape) != (B, H, Nk, D) or tuple(v8.shape) != (B, H, D, tiles * 128):
+        raise VcxError("K/V payload shapes do not match Q")
+    if tuple(qs.shape) != (B, H, (Nq + 63) // 64) or tuple(ks.shape) != (B, H, tiles) \
+            or tuple(vs.shape) != (B, H, D):
+        raise VcxError("Incorrect FP8 block scales")
+    out_dtype = torch.float16 if output_type == 0 else torch.bfloat16
+    if out is None:
+        out = torch.empty((B, H, Nq, D), dtype=out_dtype, device=dev)
+    osb, osh, osn = _strides4(out)
+    pd = None
+    r0 = r1 = 0
+    if p_rows is not None:
+        r0, r1 = int(p_rows[0]), int(p_rows[1])
+        pd = torch.zeros((B, H, max(r1 - r0, 0), tiles * 128), dtype=torch.uint8, device=dev)
+    _check(lib().vcx_attention_fwd_fp8(_ptr(q8), _ptr(k8), _ptr(v8), _ptr(qs), _ptr(ks), _ptr(vs), B, H, Nq, Nk,
+                                       D, (2 if affine else 1) if expcast else 0, float(scale),
+                                       1 if output_type else 0, _ptr(out), osb, osh, osn, _ptr(pd), r0, r1,
+                                       _stream(dev)),
+           "vcx_attention_fwd_fp8")
+    return (out, pd) if p_rows is not None else out
+
+
+@torch.no_grad()
 def expcast_codes(x):
     dev = _require_device(x)
     x = x.float().contiguous()
@@ -310,8 +357,12 @@ def convert_probe(x):
     return u8, f8
 
 
-def kernel_resources(D: int = 128, block_values: bool = False) -> dict:
+def kernel_resources(D: int = 128, block_values: bool = False, *, qk_fp8: bool = False,
+                     expcast: bool = True) -> dict:
     arr = (ctypes.c_int64 * 6)()
-    _check(lib().vcx_kernel_resources(D, int(block_values), arr), "vcx_kernel_resources")
+    if qk_fp8:
+        _check(lib().vcx_kernel_resources_fp8(D, int(expcast), arr), "vcx_kernel_resources_fp8")
+    else:
+        _check(lib().vcx_kernel_resources(D, int(block_values), arr), "vcx_kernel_resources")
     return {"vgprs": arr[0], "agprs": arr[1], "static_lds_bytes": arr[2], "dynamic_lds_bytes": arr[3],
             "threads_per_block": arr[4], "scratch_bytes_per_lane": arr[5]}

@@ -146,6 +146,21 @@ int vcx_attention_fwd(const int8_t* q8, const int8_t* k8, const uint8_t* v8, con
                       void* out, int64_t o_sb, int64_t o_sh, int64_t o_sn, uint8_t* p_dump,
                       int64_t p_row_begin, int64_t p_row_end, void* stream);
 
+/* Fused attention forward on block-scaled FP8 Q/K (vcx_prepare_qk_fp8): E4M3 QK^T on
+ * v_mfma_f32_16x16x128_f8f6f4, logit scale RN(qs[row/64] * ks[tile]), then the same
+ * probability paths, PV and epilogue as vcx_attention_fwd without block values. V is
+ * the per-channel payload of vcx_prepare_v_fp8(smooth = 0) with vs [B,H,D].
+ * expcast: 2 folded ExpCast encode (the reference's FP8 kernel), 1 unfused ExpCast,
+ * 0 Sage FP8 control. q8 [B,H,Nq,D], k8 [B,H,Nk,D] E4M3 bytes; qs [B,H,ceil(Nq/64)];
+ * ks [B,H,ceil(Nk/128)]. out, p_dump as for vcx_attention_fwd.
+ * Replaces _vc_sm90.forward_fp8 (third_party/sageattention_local/csrc/vc/pybind.cpp:57,
+ * fp8_dispatch.cuh:76-111). */
+int vcx_attention_fwd_fp8(const uint8_t* q8, const uint8_t* k8, const uint8_t* v8, const float* qs,
+                          const float* ks, const float* vs, int64_t B, int64_t H, int64_t Nq,
+                          int64_t Nk, int64_t D, int expcast, float sm_scale, int out_dtype,
+                          void* out, int64_t o_sb, int64_t o_sh, int64_t o_sn, uint8_t* p_dump,
+                          int64_t p_row_begin, int64_t p_row_end, void* stream);
+
 /* ExpCast byte probe: y[i] = clamp(RNE(fmaf(x[i], 11.54156, 119.65)), 0, 120).
  * Replaces _vc_sm90.expcast_codes (third_party/sageattention_local/csrc/vc/preprocess.cu:170-179). */
 int vcx_expcast_codes(const float* x, uint8_t* y, int64_t n, void* stream);
@@ -162,6 +177,11 @@ int vcx_convert_probe(const float* x, uint8_t* u8, uint8_t* f8, int64_t n, void*
  * out[5] scratch (spill) bytes per lane.
  * Replaces _vc_sm90.kernel_resources (third_party/sageattention_local/csrc/vc/vc_sm90.cu:786-822). */
 int vcx_kernel_resources(int64_t D, int block_values, int64_t* out);
+
+/* The same six values for the FP8 block QK kernel (expcast = 1: folded ExpCast,
+ * 0: control). Replaces _vc_sm90.fp8_kernel_resources
+ * (third_party/sageattention_local/csrc/vc/fp8_dispatch.cuh:61-73). */
+int vcx_kernel_resources_fp8(int64_t D, int expcast, int64_t* out);
 
 #ifdef __cplusplus
 }

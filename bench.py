@@ -6,7 +6,11 @@ attention kernel, with bf16 inputs already resident in HBM. The headline value
 is the fused kernel's effective TOPS = 4*B*H*Nq*Nk*D / kernel time, timed with
 HIP events on the stream the kernels run on; preprocessing is timed separately.
 
-    python bench.py [--steps K] [--warmup W] [--config main|smooth|d64|long|cpu]
+    python bench.py [--steps K] [--warmup W] [--config main|smooth|d64|long|cpu] [--qk int8|fp8]
+
+--qk fp8 measures the block-scaled FP8 QK variant (the reference's experimental vc27:
+E4M3 Q/K in 64/128-row blocks, K centred in binary32) on the same workload; it has no
+V smoothing, so it runs the configurations without smoothing only.
 
 Prints ONE JSON line (rank 0, N=1). --gpus N with N > 1 exits: this build runs
 on one GPU only.
@@ -28,9 +32,10 @@ PEAK_HBM_GBS = 8000.0   # MI355X HBM3E, GB/s (published)
 
 # HBM bytes per fused-kernel launch, measured with rocprofv3 --pmc FETCH_SIZE (scaled by
 # 2.0, the factor a plain 1 GiB copy reads) plus WRITE_SIZE (factor 1.0); the run and its
-# commands are in profiles/attn_kernel_main_hbm_bytes.txt. Counters cannot be read from
-# inside this process, so the figure is keyed by configuration and null where unmeasured.
-MEASURED_TRAFFIC_BYTES = {"main": 3.109e9}
+# commands are in profiles/attn_kernel_main_hbm_bytes.txt (FP8 QK variant:
+# profiles/attn_kernel_fp8_main_hbm_bytes.txt). Counters cannot be read from inside this
+# process, so the figure is keyed by QK format and configuration and null where unmeasured.
+MEASURED_TRAFFIC_BYTES = {("int8", "main"): 3.109e9, ("fp8", "main"): 3.123e9}
 
 CONFIGS = {
     # name: (B, H, N, D, kind, v_smooth, description)
@@ -74,7 +79,7 @@ def make_inputs(B, H, N, D, kind, seed=0):
     return q.to(torch.bfloat16), k.to(torch.bfloat16), v.to(torch.bfloat16)
 
 
-def cpu_baseline(q, k, v, smooth, rows, budget_s):
+def cpu_baseline(q, k, v, smooth, rows, budget_s, qk="int8"):
     """The CPU oracle (C restatement, OpenMP over rows) on the box's host cores:
     full preprocessing of the same workload plus attention for `rows` evenly
     spaced query rows of every head against all keys, extrapolated to all rows."""
@@ -86,7 +91,7 @@ def cpu_baseline(q, k, v, smooth, rows, budget_s):
     B, H, N, D = q.shape
     qb, kb, vb = bits(q), bits(k), bits(v)
     t0 = time.perf_counter()
-    st = o.prepare(qb, kb, vb, v_smooth=smooth)
+    st = o.prepare_fp8(qb, kb, vb) if qk == "fp8" else o.prepare(qb, kb, vb, v_smooth=smooth)
     prep_s = time.perf_counter() - t0
     # Without smoothing the GPU path uses the folded ExpCast encode, whose fallback is decided
     # per 16-row group: sample whole groups so the oracle's group pass covers only them.
@@ -107,7 +112,8 @@ def cpu_baseline(q, k, v, smooth, rows, budget_s):
         "cores": threads,
         "kind": "port",
         "sample": f"oracle/vc_oracle.c: attention of {len(ids)} query rows "
-                  f"({'evenly spaced 16-row groups, folded ExpCast encode' if affine else 'evenly spaced, ExpCast'}) "
+                  f"({'evenly spaced 16-row groups, folded ExpCast encode' if affine else 'evenly spaced, ExpCast'}"
+                  f"{', FP8 block QK' if qk == 'fp8' else ''}) "
                   f"x all {N} keys x {B * H} heads (P bytes + decoded-payload fp64 accumulation), OpenMP over rows; "
                   f"value = 4*B*H*rows*N*D / time. Full preprocessing of the same inputs (single thread) "
                   f"took {prep_s:.2f} s; extrapolated full forward = {prep_s + attn_s * N / len(ids):.1f} s",
@@ -125,6 +131,8 @@ def main():
     ap.add_argument("--config", default="main", choices=sorted(CONFIGS))
     ap.add_argument("--cpu-rows", type=int, default=2048, help="query rows per head for the CPU baseline")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--qk", default="int8", choices=("int8", "fp8"),
+                    help="int8: the sageattn_vc path (headline); fp8: the block-scaled FP8 QK variant")
     ap.add_argument("--mode", default="full", choices=("full", "kernel", "copy"),
                     help="full: the benchmark; kernel: prepare once, then only the fused kernel "
                          "(--steps launches, for profilers); copy: a plain 1 GiB device copy "
@@ -139,6 +147,12 @@ def main():
     import vcx
 
     B, H, N, D, kind, smooth, desc = CONFIGS[args.config]
+    fp8 = args.qk == "fp8"
+    if fp8 and smooth:
+        print(f"bench.py: --qk fp8 has no V smoothing; config {args.config!r} needs it", file=sys.stderr)
+        sys.exit(2)
+    if fp8:
+        desc = desc.replace("INT8 QK (Sage per-thread scales)", "FP8 E4M3 QK (64/128-row block scales, K centred)")
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     if args.mode == "copy":
@@ -156,6 +170,10 @@ def main():
     clusters, iterations = 8, 2
 
     def prep():
+        if fp8:
+            q8, qs, k8, ks, _ = vcx.prepare_qk_fp8(q, k)
+            v8, vs, means = vcx.prepare_v(v, None, smooth=False, channel_scale=True)
+            return q8, qs, k8, ks, v8, vs, means
         perm = vcx.group_values(v, clusters, iterations) if smooth else None
         q8, qs, k8, ks, _ = vcx.prepare_qk(q, k, perm)
         v8, vs, means = vcx.prepare_v(v, perm, smooth=smooth, channel_scale=True)
@@ -165,6 +183,9 @@ def main():
 
     def fused(p):
         q8, qs, k8, ks, v8, vs, means = p
+        if fp8:  # the reference's FP8 kernel folds the ExpCast encode
+            vcx.forward_fp8(q8, k8, v8, qs, ks, vs, True, 1, scale, affine=True, out=out)
+            return
         # the reference's default kernel mode: folded ExpCast encode without block values
         vcx.forward(q8, k8, v8, qs, ks, vs, means, True, smooth, 1, scale, affine=not smooth, out=out)
 
@@ -199,11 +220,15 @@ def main():
     mean_kernel_ms = sum(kern_ms) / len(kern_ms)
     achieved = ops / (mean_kernel_ms * 1e-3) / 1e12
     tiles = (N + 127) // 128
-    prep_bytes = 6.0 * B * H * N * D + 3.0 * B * H * N * D + 4.0 * B * H * ((N + 63) // 64 * 32) \
-        + 4.0 * B * H * tiles * 4 + 4.0 * B * H * D + (2.0 * B * H * tiles * D if smooth else 0.0)
+    if fp8:  # block scales: one per 64 query rows and one per key tile, plus the fp32 K mean
+        prep_bytes = 9.0 * B * H * N * D + 4.0 * B * H * ((N + 63) // 64 + tiles) + 8.0 * B * H * D
+    else:
+        prep_bytes = 6.0 * B * H * N * D + 3.0 * B * H * N * D + 4.0 * B * H * ((N + 63) // 64 * 32) \
+            + 4.0 * B * H * tiles * 4 + 4.0 * B * H * D + (2.0 * B * H * tiles * D if smooth else 0.0)
     prep_gbs = prep_bytes / (prep_med * 1e-3) / 1e9
     result = {
-        "metric": "sageattn_vc fused-kernel TOPS at BNSD [1,28,37741,128] bf16 (4*B*H*N^2*D / kernel time); "
+        "metric": ("sageattn_vc_fp8 (FP8 block QK) " if fp8 else "sageattn_vc ")
+                  + "fused-kernel TOPS at BNSD [1,28,37741,128] bf16 (4*B*H*N^2*D / kernel time); "
                   "kernel ms and fraction of INT8/FP8 MFMA peak",
         "value": round(tops, 2),
         "unit": "TOPS",
@@ -214,10 +239,10 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "int8 QK / fp8-e4m3 PV, fp32 accumulate",
+        "dtype": ("fp8-e4m3" if fp8 else "int8") + " QK / fp8-e4m3 PV, fp32 accumulate",
         "data": "synthetic (seeded torch.Generator on CPU, cast to bf16, copied to HBM before timing)",
         "config": {"workload": desc, "shape_bnsd": [B, H, N, D], "config_name": args.config,
-                   "v_smooth": smooth, "expcast": True,
+                   "v_smooth": smooth, "expcast": True, "qk_format": "fp8_block" if fp8 else "int8",
                    "expcast_encode": "unfused (block values)" if smooth else "folded (the reference's default kernel mode)"},
         "kernel_ms": round(kernel_ms, 4),
         "prep_ms": round(prep_med, 4),
@@ -225,13 +250,13 @@ def main():
         "frac_of_mfma_peak": round(tops / PEAK_TOPS, 4),
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_TOPS, "unit": "TFLOP/s",
                      "frac": round(achieved / PEAK_TOPS, 4),
-                     "traffic": MEASURED_TRAFFIC_BYTES.get(args.config),
+                     "traffic": MEASURED_TRAFFIC_BYTES.get((args.qk, args.config)),
                      "kernel": "attn_kernel (fused QK/ExpCast/PV)", "ops_per_launch": ops},
         "roofline_prep": {"bound": "hbm", "achieved": round(prep_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                           "frac": round(prep_gbs / PEAK_HBM_GBS, 4), "algorithmic_bytes": prep_bytes},
     }
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(qc, kc, vc_, smooth, args.cpu_rows, 30.0)
+        result["cpu_baseline"] = cpu_baseline(qc, kc, vc_, smooth, args.cpu_rows, 30.0, args.qk)
     print(json.dumps(result), flush=True)
 
 

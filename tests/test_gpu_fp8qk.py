@@ -277,3 +277,107 @@ def test_fp8_kernel_resources_and_rejections():
         vcx.forward_fp8(q8, k8, v8, qs[..., :1].contiguous(), ks, vs, True, 1, 0.125)
     with pytest.raises(vcx.VcxError, match="int8|E4M3|float8"):
         vcx.forward_fp8(q8.view(torch.int8), k8, v8, qs, ks, vs, True, 1, 0.125)
+
+
+# ------------------------------------------------------------------ the reference's vc27 gates
+
+GATE_ATTN = [(1, 1), (17, 63), (63, 127), (64, 128), (65, 129), (127, 255), (128, 256), (129, 257), (193, 513)]
+
+
+def _relative_rmse(actual, expected):
+    d = np.asarray(actual, np.float64) - np.asarray(expected, np.float64)
+    return float(np.sqrt((d ** 2).mean()) / max(np.sqrt((np.asarray(expected, np.float64) ** 2).mean()), 1e-12))
+
+
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16], ids=["f16", "bf16"])
+@pytest.mark.parametrize("D", [64, 128])
+def test_fp8_attention_gate_all_rows(D, dt):
+    # scripts/validate_fp8_qk.py:128-155: every shape and both probability paths within 1 %
+    # relative RMSE of the decoded-payload oracle (here, as everywhere, also the elementwise
+    # bound against the attention the kernel's own P bytes define); the public API and its
+    # NHD layout give the same bits as forward_prepared.
+    from sageattention_local import sageattn_vc_fp8
+    from sageattention_local.vc_fp8 import forward_prepared, prepare
+    gen = torch.Generator().manual_seed(2702 + D)
+    for nq, nk in GATE_ATTN:
+        q = torch.randn(2, 2, nq, D, generator=gen).to(dt)
+        k = torch.randn(2, 2, nk, D, generator=gen).to(dt)
+        v = torch.randn(2, 2, nk, D, generator=gen).to(dt)
+        qd, kd, vd = (x.to(DEV) for x in (q, k, v))
+        ost = o.prepare_fp8(bits(q), bits(k), bits(v), dtype=dtype_name(dt))
+        for cast in (False, True):
+            _print_case("fp8 gate", nq, nk, D, dt, cast)
+            st = prepare(qd, kd, vd, expcast=cast)
+            out = forward_prepared(st)
+            ost["expcast"] = cast
+            eout = o.reference(ost, affine=cast)
+            got = out.float().cpu().numpy()
+            assert np.isfinite(got).all()
+            assert _relative_rmse(got, eout) <= 0.01
+            _, codes = vcx.forward_fp8(st["q"], st["k"], st["v"], st["qs"], st["ks"], st["vs"], cast,
+                                       st["output_type"], st["scale"], p_rows=(0, nq))
+            err, bound = output_bound(got, _expected_from_codes(ost, codes.cpu().numpy(), cast))
+            assert np.all(err <= bound)
+            assert torch.equal(sageattn_vc_fp8(qd, kd, vd, expcast=cast), out)
+            nhd = sageattn_vc_fp8(qd.transpose(1, 2), kd.transpose(1, 2), vd.transpose(1, 2), tensor_layout="NHD",
+                                  expcast=cast)
+            assert torch.equal(nhd.transpose(1, 2), out)
+
+
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16], ids=["f16", "bf16"])
+@pytest.mark.parametrize("D", [64, 128])
+def test_fp8_known_constant_values_and_zero_channels(D, dt):
+    # scripts/validate_fp8_qk.py:156-170: zero Q/K, V = (channel % 8) / 8 (every 8th channel
+    # zero) or all zero: finite payloads, and the output is V's constant row.
+    from sageattention_local import sageattn_vc_fp8
+    from sageattention_local.vc_fp8 import prepare
+    q = torch.zeros(1, 2, 65, D, device=DEV, dtype=dt)
+    for nk in (1, 129, 257):
+        k = torch.zeros(1, 2, nk, D, device=DEV, dtype=dt)
+        for all_zero in (False, True):
+            _print_case("fp8 known constant", D, dt, nk, all_zero)
+            v = (torch.arange(D, device=DEV, dtype=dt).remainder(8).view(1, 1, 1, D).expand_as(k).contiguous() / 8)
+            if all_zero:
+                v.zero_()
+            st = prepare(q, k, v)
+            for name in ("qs", "ks", "vs"):
+                assert torch.isfinite(st[name]).all(), name
+            for name in ("q", "k", "v"):
+                assert torch.isfinite(st[name].view(torch.float8_e4m3fn).float()).all(), name
+            for cast in (False, True):
+                out = sageattn_vc_fp8(q, k, v, expcast=cast)
+                assert torch.isfinite(out).all()
+                torch.testing.assert_close(out, v[:, :, :1].expand_as(out), rtol=0.004, atol=0.002)
+
+
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16], ids=["f16", "bf16"])
+@pytest.mark.parametrize("D", [64, 128])
+def test_fp8_value_zero_channels_on_a_side_stream(D, dt):
+    # scripts/validate_fp8_qk.py:85-122 and tests/test_fp8_zero_values.py: zero channels get a
+    # zero scale and zero bytes, every other scale is amax/448, on a non-default stream.
+    gen = torch.Generator().manual_seed(27101)
+    tok = vcx.value_token()
+    for n in (1, 128, 129, 257, 4097):
+        for kind in ("mixed_random", "mixed_constant", "all_zero"):
+            _print_case("fp8 V zero channels", D, dt, n, kind)
+            v = torch.randn(2, 3, n, D, generator=gen).to(dt)
+            if kind == "mixed_constant":
+                v.copy_(torch.arange(D, dtype=dt).remainder(8).view(1, 1, 1, D) / 8)
+            if kind == "all_zero":
+                v.zero_()
+            v[..., ::8] = 0
+            vd = v.to(DEV)
+            side = torch.cuda.Stream()
+            side.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(side):
+                v8, vs, _ = vcx.prepare_v(vd)
+            torch.cuda.current_stream().wait_stream(side)
+            logical = storage_to_logical(v8, tok)
+            ev8, evs = o.per_channel_fp8(bits(v), None, dtype_name(dt))
+            np.testing.assert_array_equal(logical, ev8)
+            np.testing.assert_array_equal(vs.cpu().numpy(), evs)
+            amax = v.float().abs().amax(2).numpy()
+            zero = amax == 0
+            assert np.all(vs.cpu().numpy()[zero] == 0)
+            assert np.count_nonzero(logical[zero]) == 0
+            np.testing.assert_allclose(vs.cpu().numpy(), amax / 448, rtol=2e-7, atol=0)

@@ -115,4 +115,32 @@ __device__ inline int int8_code(float x, float s) {
 
 __device__ inline float wave_xor_max(float v, int mask) { return fmaxf(v, __shfl_xor(v, mask, 64)); }
 
+// Normalized Sylvester-Hadamard rotation of one row of W = CPT * L values held by L
+// consecutive lanes (lane c of the group holds entries c*CPT .. c*CPT + CPT - 1). Strides
+// 1, 2, 4, ... in order: the in-lane strides first, then lane xor 1, 2, ...; each pair
+// (a, b) with a the lower entry becomes (RN(a + b), RN(a - b)); then every entry is
+// multiplied by norm = RN_f32(1/sqrt(W)). Every lane of the group must take part.
+// Reference: hadamard, src/vc_attention/core.py:79-92; transform_qk_kernel, csrc/kernels.cu:104-123.
+template <int CPT, int L>
+__device__ inline void hadamard_row(float (&x)[CPT], int c, float norm) {
+#pragma unroll
+  for (int s = 1; s < CPT; s <<= 1)
+#pragma unroll
+    for (int j = 0; j < CPT; ++j)
+      if (!(j & s)) {
+        const float a = x[j], b = x[j + s];
+        x[j] = __fadd_rn(a, b);
+        x[j + s] = __fsub_rn(a, b);
+      }
+#pragma unroll
+  for (int m = 1; m < L; m <<= 1)
+#pragma unroll
+    for (int j = 0; j < CPT; ++j) {
+      const float other = __shfl_xor(x[j], m, 64);
+      x[j] = (c & m) ? __fsub_rn(other, x[j]) : __fadd_rn(x[j], other);
+    }
+#pragma unroll
+  for (int j = 0; j < CPT; ++j) x[j] = __fmul_rn(x[j], norm);
+}
+
 }  // namespace vcx

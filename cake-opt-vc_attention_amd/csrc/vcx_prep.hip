@@ -260,10 +260,12 @@ __global__ void v_scale_kernel(const float* a0, const float* a1, int64_t tiles, 
 
 // grid (ceil(n/64), B*H), 256 threads. Groups of rows {16g+t, 16g+t+8}; each
 // group is 32 lanes (16 per row) of one wave; 4 passes of 8 groups.
-template <int DT, int D>
+// ROT: the rows are rotated by the normalized Hadamard transform (hadamard_row, norm =
+// RN_f32(1/sqrt(D))) in binary32 before the group maximum and the codes.
+template <int DT, int D, bool ROT = false>
 __global__ __launch_bounds__(kThreads) void quant_q_kernel(const void* q, int64_t H, int64_t n,
                                                            int64_t sb, int64_t sh, int64_t sn,
-                                                           int8_t* q8, float* qs) {
+                                                           int8_t* q8, float* qs, float norm) {
   constexpr int CPT = D / 16;
   const int64_t blk = blockIdx.x, bh = blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, c = lane & 15, sel = (lane >> 4) & 1;
@@ -285,6 +287,7 @@ __global__ __launch_bounds__(kThreads) void quant_q_kernel(const void* q, int64_
     float x[CPT];
 #pragma unroll
     for (int j = 0; j < CPT; ++j) x[j] = row < n ? row_val<DT, D>(rows[pass], j) : 0.0f;
+    if constexpr (ROT) hadamard_row<CPT, 16>(x, c, norm);
     float amax = 0.0f;
 #pragma unroll
     for (int j = 0; j < CPT; ++j) amax = fmaxf(amax, fabsf(x[j]));
@@ -373,15 +376,90 @@ __global__ __launch_bounds__(kThreads) void quant_fp8_kernel(const void* x, int6
   }
 }
 
+// ---------------------------------------------------------------- generic Q/K preprocessing
+
+// The reference's preprocess_qk (csrc/bindings.cpp:87-116, kernels.cu:104-123): fp32/fp16/bf16
+// [B,H,N,D] with D <= 128 (any), widened to binary32; K centred by its binary32 channel mean;
+// Q and K optionally rotated (width W = next power of two >= D, zero padded).
+template <int DT>
+__device__ inline float elem(const void* x, int64_t i) {
+  if constexpr (DT == VCX_FLOAT32) return static_cast<const float*>(x)[i];
+  else return in_to_f32<DT>(static_cast<const uint16_t*>(x)[i]);
+}
+
+// grid (tiles, B*H), D threads: binary64 sum of channel d over the tile's keys in key order.
+template <int DT>
+__global__ __launch_bounds__(128) void pre_tile_sum_kernel(const void* x, int64_t H, int64_t n, int64_t sb,
+                                                           int64_t sh, int64_t sn, double* part) {
+  const int64_t t = blockIdx.x, bh = blockIdx.y, tiles = gridDim.x;
+  const int d = threadIdx.x, D = blockDim.x;
+  const int64_t off = (bh / H) * sb + (bh % H) * sh + d;
+  const int64_t r0 = t * kTile, r1 = r0 + kTile < n ? r0 + kTile : n;
+  double s = 0.0;
+  int64_t r = r0;
+  for (; r + 8 <= r1; r += 8) {
+    float v[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = elem<DT>(x, off + (r + i) * sn);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) s = __dadd_rn(s, static_cast<double>(v[i]));
+  }
+  for (; r < r1; ++r) s = __dadd_rn(s, static_cast<double>(elem<DT>(x, off + r * sn)));
+  part[(bh * tiles + t) * D + d] = s;
+}
+
+// grid (ceil(n / RPB), B*H): RPB rows of one head per block; L = min(W, 16) lanes per row
+// with CPT = W / L entries each. out = rotate(x - mean) (mean nullable), [B*H][n][W] binary32.
+template <int DT, int W>
+__global__ __launch_bounds__(kThreads) void pre_rotate_kernel(const void* x, int64_t H, int64_t n, int D,
+                                                              int64_t sb, int64_t sh, int64_t sn,
+                                                              const float* mean, float* out, float norm) {
+  constexpr int L = W < 16 ? W : 16, CPT = W / L, RPB = kThreads / L;
+  const int tid = threadIdx.x, c = tid % L;
+  const int64_t bh = blockIdx.y, r = static_cast<int64_t>(blockIdx.x) * RPB + tid / L;
+  const bool valid = r < n;
+  const int64_t g = bh * n + r;
+  const int64_t off = (bh / H) * sb + (bh % H) * sh + (valid ? r : 0) * sn;
+  float v[CPT];
+#pragma unroll
+  for (int j = 0; j < CPT; ++j) {
+    const int ch = c * CPT + j;
+    float y = valid && ch < D ? elem<DT>(x, off + ch) : 0.0f;
+    if (mean != nullptr && valid && ch < D) y = __fsub_rn(y, mean[bh * D + ch]);
+    v[j] = y;
+  }
+  hadamard_row<CPT, L>(v, c, norm);
+  if (valid) {
+#pragma unroll
+    for (int j = 0; j < CPT; ++j) out[g * W + c * CPT + j] = v[j];
+  }
+}
+
+// Without rotation: out[B*H*n][D] = x - mean (mean nullable), binary32.
+template <int DT>
+__global__ __launch_bounds__(kThreads) void pre_center_kernel(const void* x, int64_t H, int64_t n, int D,
+                                                              int64_t sb, int64_t sh, int64_t sn,
+                                                              const float* mean, float* out, int64_t total) {
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; i < total;
+       i += static_cast<int64_t>(gridDim.x) * kThreads) {
+    const int64_t g = i / D, bh = g / n, r = g % n;
+    const int ch = static_cast<int>(i % D);
+    float y = elem<DT>(x, (bh / H) * sb + (bh % H) * sh + r * sn + ch);
+    if (mean != nullptr) y = __fsub_rn(y, mean[bh * D + ch]);
+    out[i] = y;
+  }
+}
+
 // ---------------------------------------------------------------- K INT8
 
 // grid (tiles, B*H), 256 threads. Thread (kk, c) holds keys kk+16i, all in
 // scale group g = (kk%8)/2; a group is lanes 0-31 or 32-63 of waves w and w+2.
-template <int DT, int D>
+// ROT: each centred key row k'' is rotated (hadamard_row) in binary32 before quantizing.
+template <int DT, int D, bool ROT = false>
 __global__ __launch_bounds__(kThreads) void quant_k_kernel(const void* k, int64_t H, int64_t n,
                                                            int64_t sb, int64_t sh, int64_t sn,
                                                            const int64_t* perm, const float* km,
-                                                           int8_t* k8, float* ks) {
+                                                           int8_t* k8, float* ks, float norm) {
   constexpr int CPT = D / 16;
   __shared__ float gred[4][2];
   const int64_t tile = blockIdx.x, bh = blockIdx.y, tiles = gridDim.x;
@@ -397,10 +475,10 @@ __global__ __launch_bounds__(kThreads) void quant_k_kernel(const void* k, int64_
   for (int i = 0; i < 8; ++i) {
     const bool valid = tile * kTile + kk + 16 * i < n;
 #pragma unroll
-    for (int j = 0; j < CPT; ++j) {
-      v[i][j] = valid ? round_in<DT>(__fsub_rn(v[i][j], mean[j])) : 0.0f;
-      amax = fmaxf(amax, fabsf(v[i][j]));
-    }
+    for (int j = 0; j < CPT; ++j) v[i][j] = valid ? round_in<DT>(__fsub_rn(v[i][j], mean[j])) : 0.0f;
+    if constexpr (ROT) hadamard_row<CPT, 16>(v[i], c, norm);
+#pragma unroll
+    for (int j = 0; j < CPT; ++j) amax = fmaxf(amax, fabsf(v[i][j]));
   }
 #pragma unroll
   for (int m = 1; m < 32; m <<= 1) amax = wave_xor_max(amax, m);
@@ -598,6 +676,9 @@ size_t ws_prepare_qk(int64_t BH, int64_t N, int64_t D) {
   int64_t tiles = cdiv(N, kTile);
   return align_up(sizeof(double) * BH * tiles * D) + align_up(sizeof(float) * BH * D);
 }
+size_t ws_preprocess_qk(int64_t BH, int64_t N, int64_t D) {
+  return align_up(sizeof(double) * BH * cdiv(N, kTile) * D) + align_up(sizeof(float) * BH * D);
+}
 size_t ws_prepare_v(int64_t BH, int64_t N, int64_t D) {
   int64_t tiles = cdiv(N, kTile);
   return 2 * align_up(sizeof(float) * BH * tiles * D) + align_up(sizeof(float) * BH * D);
@@ -607,12 +688,11 @@ size_t ws_prepare_v(int64_t BH, int64_t N, int64_t D) {
 
 using namespace vcx;
 
-extern "C" int vcx_prepare_qk_int8(const void* q, const void* k, int dtype, int64_t B, int64_t H,
-                                   int64_t Nq, int64_t Nk, int64_t D, int64_t q_sb, int64_t q_sh,
-                                   int64_t q_sn, int64_t k_sb, int64_t k_sh, int64_t k_sn,
-                                   const int64_t* perm, int8_t* q8, float* qs, int8_t* k8, float* ks,
-                                   void* km_out, void* workspace, size_t workspace_bytes,
-                                   void* stream) {
+namespace {
+int prepare_qk_int8(const void* q, const void* k, int dtype, int64_t B, int64_t H, int64_t Nq, int64_t Nk,
+                    int64_t D, int64_t q_sb, int64_t q_sh, int64_t q_sn, int64_t k_sb, int64_t k_sh, int64_t k_sn,
+                    const int64_t* perm, int8_t* q8, float* qs, int8_t* k8, float* ks, void* km_out,
+                    void* workspace, size_t workspace_bytes, void* stream, bool rotate) {
   if (int rc = check_shape(B, H, Nq, D)) return rc;
   if (int rc = check_shape(B, H, Nk, D)) return rc;
   VCX_REQUIRE(dtype == VCX_FLOAT16 || dtype == VCX_BFLOAT16, "dtype must be float16 or bfloat16");
@@ -629,19 +709,50 @@ extern "C" int vcx_prepare_qk_int8(const void* q, const void* k, int dtype, int6
   double* ksum = reinterpret_cast<double*>(ws);
   float* km = reinterpret_cast<float*>(ws + align_up(sizeof(double) * BH * tiles * D));
   hipStream_t st = static_cast<hipStream_t>(stream);
+  const float norm = static_cast<float>(1.0 / std::sqrt(static_cast<double>(D)));
   return dispatch(dtype, D, [&](auto dt, auto dd) -> int {
     constexpr int DT = decltype(dt)::value, DD = decltype(dd)::value;
-    quant_q_kernel<DT, DD><<<dim3(cdiv(Nq, 64), BH), kThreads, 0, st>>>(q, H, Nq, q_sb, q_sh, q_sn, q8, qs);
+    if (rotate)
+      quant_q_kernel<DT, DD, true><<<dim3(cdiv(Nq, 64), BH), kThreads, 0, st>>>(q, H, Nq, q_sb, q_sh, q_sn, q8, qs,
+                                                                              norm);
+    else
+      quant_q_kernel<DT, DD><<<dim3(cdiv(Nq, 64), BH), kThreads, 0, st>>>(q, H, Nq, q_sb, q_sh, q_sn, q8, qs, norm);
     VCX_LAUNCHED("quant_q_kernel");
     tile_stats_kernel<DT, DD, kKSum><<<dim3(tiles, BH), kThreads, 0, st>>>(k, H, Nk, k_sb, k_sh, k_sn, perm,
                                                                           ksum, nullptr, nullptr);
     VCX_LAUNCHED("tile_stats_kernel<K>");
     k_mean_kernel<DT><<<dim3(BH), DD, 0, st>>>(ksum, tiles, Nk, DD, km, km_out);
     VCX_LAUNCHED("k_mean_kernel");
-    quant_k_kernel<DT, DD><<<dim3(tiles, BH), kThreads, 0, st>>>(k, H, Nk, k_sb, k_sh, k_sn, perm, km, k8, ks);
+    if (rotate)
+      quant_k_kernel<DT, DD, true><<<dim3(tiles, BH), kThreads, 0, st>>>(k, H, Nk, k_sb, k_sh, k_sn, perm, km, k8,
+                                                                        ks, norm);
+    else
+      quant_k_kernel<DT, DD><<<dim3(tiles, BH), kThreads, 0, st>>>(k, H, Nk, k_sb, k_sh, k_sn, perm, km, k8, ks,
+                                                                  norm);
     VCX_LAUNCHED("quant_k_kernel");
     return VCX_OK;
   });
+}
+}  // namespace
+
+extern "C" int vcx_prepare_qk_int8(const void* q, const void* k, int dtype, int64_t B, int64_t H,
+                                   int64_t Nq, int64_t Nk, int64_t D, int64_t q_sb, int64_t q_sh,
+                                   int64_t q_sn, int64_t k_sb, int64_t k_sh, int64_t k_sn,
+                                   const int64_t* perm, int8_t* q8, float* qs, int8_t* k8, float* ks,
+                                   void* km_out, void* workspace, size_t workspace_bytes,
+                                   void* stream) {
+  return prepare_qk_int8(q, k, dtype, B, H, Nq, Nk, D, q_sb, q_sh, q_sn, k_sb, k_sh, k_sn, perm, q8, qs, k8, ks,
+                         km_out, workspace, workspace_bytes, stream, false);
+}
+
+extern "C" int vcx_prepare_qk_int8_rotated(const void* q, const void* k, int dtype, int64_t B, int64_t H,
+                                           int64_t Nq, int64_t Nk, int64_t D, int64_t q_sb, int64_t q_sh,
+                                           int64_t q_sn, int64_t k_sb, int64_t k_sh, int64_t k_sn,
+                                           const int64_t* perm, int8_t* q8, float* qs, int8_t* k8, float* ks,
+                                           void* km_out, void* workspace, size_t workspace_bytes,
+                                           void* stream) {
+  return prepare_qk_int8(q, k, dtype, B, H, Nq, Nk, D, q_sb, q_sh, q_sn, k_sb, k_sh, k_sn, perm, q8, qs, k8, ks,
+                         km_out, workspace, workspace_bytes, stream, true);
 }
 
 extern "C" int vcx_prepare_qk_fp8(const void* q, const void* k, int dtype, int64_t B, int64_t H,
@@ -749,4 +860,93 @@ extern "C" int vcx_convert_probe(const float* x, uint8_t* u8, uint8_t* f8, int64
   convert_probe_kernel<<<cdiv(n, 256), 256, 0, static_cast<hipStream_t>(stream)>>>(x, u8, f8, n);
   VCX_LAUNCHED("convert_probe_kernel");
   return VCX_OK;
+}
+
+namespace {
+template <int DT>
+int preprocess_launch(const void* q, const void* k, int64_t BH, int64_t H, int64_t Nq, int64_t Nk, int64_t D,
+                      int64_t q_sb, int64_t q_sh, int64_t q_sn, int64_t k_sb, int64_t k_sh, int64_t k_sn,
+                      int k_smooth, int hadamard, float* q_out, float* k_out, double* part, float* mean,
+                      hipStream_t st) {
+  const int64_t tiles = cdiv(Nk, kTile);
+  const float* km = nullptr;
+  if (k_smooth) {
+    pre_tile_sum_kernel<DT><<<dim3(tiles, BH), static_cast<unsigned>(D), 0, st>>>(k, H, Nk, k_sb, k_sh, k_sn,
+                                                                                   part);
+    VCX_LAUNCHED("pre_tile_sum_kernel");
+    k_mean_kernel<VCX_BFLOAT16, true><<<dim3(BH), static_cast<unsigned>(D), 0, st>>>(
+        part, tiles, Nk, static_cast<int>(D), mean, nullptr);
+    VCX_LAUNCHED("k_mean_kernel");
+    km = mean;
+  }
+  if (!hadamard) {
+    const int64_t tq = BH * Nq * D, tk = BH * Nk * D;
+    pre_center_kernel<DT><<<dim3(static_cast<unsigned>(std::min<int64_t>(cdiv(tq, kThreads), 65536))), kThreads, 0,
+                            st>>>(q, H, Nq, static_cast<int>(D), q_sb, q_sh, q_sn, nullptr, q_out, tq);
+    VCX_LAUNCHED("pre_center_kernel<Q>");
+    pre_center_kernel<DT><<<dim3(static_cast<unsigned>(std::min<int64_t>(cdiv(tk, kThreads), 65536))), kThreads, 0,
+                            st>>>(k, H, Nk, static_cast<int>(D), k_sb, k_sh, k_sn, km, k_out, tk);
+    VCX_LAUNCHED("pre_center_kernel<K>");
+    return VCX_OK;
+  }
+  int W = 1;
+  while (W < D) W <<= 1;
+  const float norm = static_cast<float>(1.0 / std::sqrt(static_cast<double>(W)));
+  auto run = [&](auto wc) -> int {
+    constexpr int WW = decltype(wc)::value, L = WW < 16 ? WW : 16, RPB = kThreads / L;
+    pre_rotate_kernel<DT, WW><<<dim3(static_cast<unsigned>(cdiv(Nq, RPB)), static_cast<unsigned>(BH)), kThreads, 0,
+                                st>>>(q, H, Nq, static_cast<int>(D), q_sb, q_sh, q_sn, nullptr, q_out, norm);
+    VCX_LAUNCHED("pre_rotate_kernel<Q>");
+    pre_rotate_kernel<DT, WW><<<dim3(static_cast<unsigned>(cdiv(Nk, RPB)), static_cast<unsigned>(BH)), kThreads, 0,
+                                st>>>(k, H, Nk, static_cast<int>(D), k_sb, k_sh, k_sn, km, k_out, norm);
+    VCX_LAUNCHED("pre_rotate_kernel<K>");
+    return VCX_OK;
+  };
+  switch (W) {
+    case 1: return run(std::integral_constant<int, 1>());
+    case 2: return run(std::integral_constant<int, 2>());
+    case 4: return run(std::integral_constant<int, 4>());
+    case 8: return run(std::integral_constant<int, 8>());
+    case 16: return run(std::integral_constant<int, 16>());
+    case 32: return run(std::integral_constant<int, 32>());
+    case 64: return run(std::integral_constant<int, 64>());
+    default: return run(std::integral_constant<int, 128>());
+  }
+}
+}  // namespace
+
+extern "C" int vcx_preprocess_qk(const void* q, const void* k, int dtype, int64_t B, int64_t H, int64_t Nq,
+                                 int64_t Nk, int64_t D, int64_t q_sb, int64_t q_sh, int64_t q_sn, int64_t k_sb,
+                                 int64_t k_sh, int64_t k_sn, int k_smooth, int hadamard, float* q_out,
+                                 float* k_out, void* workspace, size_t workspace_bytes, void* stream) {
+  VCX_REQUIRE(B >= 1 && H >= 1 && Nq >= 1 && Nk >= 1, "B, H, Nq, Nk must be positive");
+  VCX_REQUIRE(D >= 1 && D <= 128, "Q/K preprocessing supports head dimensions 1..128");
+  VCX_REQUIRE(B * H <= 65535, "B*H exceeds 65535");
+  VCX_REQUIRE(Nq < (int64_t(1) << 30) && Nk < (int64_t(1) << 30), "sequence too long");
+  VCX_REQUIRE(dtype == VCX_FLOAT16 || dtype == VCX_BFLOAT16 || dtype == VCX_FLOAT32,
+              "dtype must be float16, bfloat16 or float32");
+  VCX_REQUIRE(q && k && q_out && k_out, "null tensor pointer");
+  const int esz = dtype == VCX_FLOAT32 ? 4 : 2;
+  VCX_REQUIRE(aligned(q, esz) && aligned(k, esz) && aligned(q_out, 4) && aligned(k_out, 4), "pointer alignment");
+  VCX_REQUIRE(q_sb >= 0 && q_sh >= 0 && q_sn >= D && k_sb >= 0 && k_sh >= 0 && k_sn >= D,
+              "strides invalid (need sn >= D, last dim contiguous)");
+  const int64_t BH = B * H;
+  double* part = nullptr;
+  float* mean = nullptr;
+  if (k_smooth) {
+    VCX_REQUIRE(workspace != nullptr && aligned(workspace, 256), "workspace must be non-null and 256-byte aligned");
+    VCX_REQUIRE(workspace_bytes >= ws_preprocess_qk(BH, Nk, D), "workspace too small: need %zu bytes",
+                ws_preprocess_qk(BH, Nk, D));
+    part = static_cast<double*>(workspace);
+    mean = reinterpret_cast<float*>(static_cast<char*>(workspace) + align_up(sizeof(double) * BH * cdiv(Nk, kTile) * D));
+  }
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (dtype == VCX_FLOAT32)
+    return preprocess_launch<VCX_FLOAT32>(q, k, BH, H, Nq, Nk, D, q_sb, q_sh, q_sn, k_sb, k_sh, k_sn, k_smooth,
+                                          hadamard, q_out, k_out, part, mean, st);
+  if (dtype == VCX_BFLOAT16)
+    return preprocess_launch<VCX_BFLOAT16>(q, k, BH, H, Nq, Nk, D, q_sb, q_sh, q_sn, k_sb, k_sh, k_sn, k_smooth,
+                                           hadamard, q_out, k_out, part, mean, st);
+  return preprocess_launch<VCX_FLOAT16>(q, k, BH, H, Nq, Nk, D, q_sb, q_sh, q_sn, k_sb, k_sh, k_sn, k_smooth,
+                                        hadamard, q_out, k_out, part, mean, st);
 }

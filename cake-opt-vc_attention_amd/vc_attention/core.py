@@ -10,8 +10,10 @@ Backends of this build:
   the Sage FP8 control probabilities (``expcast=False``), FP8 PV, optional V
   grouping + block smoothing) through libvcx. It requires ``qk_format="int8"``
   and the sageattn_vc block geometry (q_block=64, k_quant_block=128,
-  kv_block=128, k_smooth=True, qk_hadamard=False, mean_dtype="float16",
-  quantize=True).
+  kv_block=128, k_smooth=True, mean_dtype="float16", quantize=True).
+  ``qk_hadamard=True`` rotates Q and the centred K by the normalized Sylvester
+  transform (core.py:79-107's) inside the INT8 quantizers; ``False`` is the
+  reference's sageattn_vc contract.
 * ``"reference"``, ``"npu_fp8"``, ``"cuda_fp8"``: validated by ``Config``
   exactly as in the reference (core.py:36-65) so existing configurations keep
   constructing; ``attention`` raises NotImplementedError for them (the eager
@@ -78,7 +80,7 @@ class Config:
                 raise ValueError("cuda_fp8 k_quant_block must be <= 4096")
         if self.backend == "hip":
             required = dict(qk_format="int8", quantize=True, q_block=64, k_quant_block=128,
-                            kv_block=128, k_smooth=True, qk_hadamard=False, mean_dtype="float16")
+                            kv_block=128, k_smooth=True, mean_dtype="float16")
             bad = [f"{k}={v!r}" for k, v in required.items() if getattr(self, k) != v]
             if bad:
                 raise ValueError("hip backend implements the sageattn_vc contract; it requires " + ", ".join(bad))
@@ -191,7 +193,7 @@ def attention(q, k, v, config=None, *, cache=None, step=0, total_steps=1, reques
                                          layer_id=layer_id)
     import vcx
 
-    q8, qs, k8, ks, km = vcx.prepare_qk(q, k, pi)
+    q8, qs, k8, ks, km = vcx.prepare_qk(q, k, pi, hadamard=cfg.qk_hadamard)
     v8, vs, means = vcx.prepare_v(v, pi, smooth=active, channel_scale=True)
     # The ExpCast encode of the reference's default kernel mode: folded without block values.
     out = vcx.forward(q8, k8, v8, qs, ks, vs, means, cfg.expcast, active, 0 if q.dtype == torch.float16 else 1,
@@ -202,7 +204,7 @@ def attention(q, k, v, config=None, *, cache=None, step=0, total_steps=1, reques
         "layout_refreshed": refreshed,
         "expcast": cfg.expcast,
         "k_smooth": True,
-        "qk_hadamard": False,
+        "qk_hadamard": cfg.qk_hadamard,
         "qk_format": "int8",
         "numerical_contract_version": "sageattn_vc-1",
         "tiles": math.ceil(q.shape[-2] / 128) * math.ceil(k.shape[-2] / 128),

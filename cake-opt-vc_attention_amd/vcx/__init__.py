@@ -17,8 +17,9 @@ ABI_VERSION = 1
 LIB_PATH = Path(__file__).resolve().parents[1] / "lib" / "libvcx.so"
 
 _OK, _EINVAL, _EUNSUPPORTED, _EHIP = 0, 1, 2, 3
-WS_PREPARE_QK, WS_PREPARE_V, WS_GROUP = 1, 2, 3
+WS_PREPARE_QK, WS_PREPARE_V, WS_GROUP, WS_PREPROCESS_QK = 1, 2, 3, 4
 _DTYPE = {torch.float16: 0, torch.bfloat16: 1}
+_PRE_DTYPE = {torch.float16: 0, torch.bfloat16: 1, torch.float32: 2}
 _lib = None
 
 
@@ -42,6 +43,11 @@ def _declare(L):
     L.vcx_prepare_qk_int8.restype = i32
     L.vcx_prepare_qk_int8.argtypes = [P, P, i32, i64, i64, i64, i64, i64, i64, i64, i64, i64, i64, i64,
                                       P, P, P, P, P, P, P, ctypes.c_size_t, P]
+    L.vcx_prepare_qk_int8_rotated.restype = i32
+    L.vcx_prepare_qk_int8_rotated.argtypes = L.vcx_prepare_qk_int8.argtypes
+    L.vcx_preprocess_qk.restype = i32
+    L.vcx_preprocess_qk.argtypes = [P, P, i32, i64, i64, i64, i64, i64, i64, i64, i64, i64, i64, i64, i32, i32,
+                                    P, P, P, ctypes.c_size_t, P]
     L.vcx_prepare_qk_fp8.restype = i32
     L.vcx_prepare_qk_fp8.argtypes = [P, P, i32, i64, i64, i64, i64, i64, i64, i64, i64, i64, i64, i64,
                                      P, P, P, P, P, P, ctypes.c_size_t, P]
@@ -65,7 +71,8 @@ def _declare(L):
 
 
 EXPORTED = ("vcx_abi_version", "vcx_last_error", "vcx_value_token", "vcx_workspace_bytes",
-            "vcx_group_values", "vcx_prepare_qk_int8", "vcx_prepare_qk_fp8", "vcx_prepare_v_fp8", "vcx_attention_fwd", "vcx_attention_fwd_fp8",
+            "vcx_group_values", "vcx_prepare_qk_int8", "vcx_prepare_qk_int8_rotated", "vcx_preprocess_qk",
+            "vcx_prepare_qk_fp8", "vcx_prepare_v_fp8", "vcx_attention_fwd", "vcx_attention_fwd_fp8",
             "vcx_expcast_codes", "vcx_convert_probe", "vcx_kernel_resources", "vcx_kernel_resources_fp8")
 
 
@@ -169,8 +176,9 @@ def group_values(v, clusters: int, iterations: int, debug: bool = False):
 
 
 @torch.no_grad()
-def prepare_qk(q, k, perm=None):
-    """INT8 Q/K with Sage per-thread scales after K centring: (q8, qs, k8, ks, km)."""
+def prepare_qk(q, k, perm=None, hadamard: bool = False):
+    """INT8 Q/K with Sage per-thread scales after K centring: (q8, qs, k8, ks, km).
+    hadamard=True rotates Q and the centred K (normalized Sylvester transform) first."""
     dev = _require_device(q, k, perm)
     if q.dtype not in _DTYPE or k.dtype != q.dtype:
         raise VcxError("Q/K require matching float16/bfloat16")
@@ -186,10 +194,37 @@ def prepare_qk(q, k, perm=None):
     ks = torch.empty((B, H, (Nk + 127) // 128 * 4), dtype=torch.float32, device=dev)
     km = torch.empty((B, H, 1, D), dtype=q.dtype, device=dev)
     ws = _workspace(workspace_bytes(WS_PREPARE_QK, B, H, Nk, D), dev)
-    _check(lib().vcx_prepare_qk_int8(_ptr(q), _ptr(k), _DTYPE[q.dtype], B, H, Nq, Nk, D, qsb, qsh, qsn,
-                                     ksb, ksh, ksn, _ptr(perm), _ptr(q8), _ptr(qs), _ptr(k8), _ptr(ks), _ptr(km),
-                                     _ptr(ws), ws.numel(), _stream(dev)), "vcx_prepare_qk_int8")
+    name = "vcx_prepare_qk_int8_rotated" if hadamard else "vcx_prepare_qk_int8"
+    _check(getattr(lib(), name)(_ptr(q), _ptr(k), _DTYPE[q.dtype], B, H, Nq, Nk, D, qsb, qsh, qsn,
+                                ksb, ksh, ksn, _ptr(perm), _ptr(q8), _ptr(qs), _ptr(k8), _ptr(ks), _ptr(km),
+                                _ptr(ws), ws.numel(), _stream(dev)), name)
     return q8, qs, k8, ks, km
+
+
+@torch.no_grad()
+def preprocess_qk(q, k, k_smooth: bool, hadamard: bool):
+    """Binary32 post-RoPE Q/K preprocessing (the reference's preprocess_qk): K centred by its
+    channel mean when k_smooth, Q and K rotated by the normalized Sylvester-Hadamard transform
+    (zero padded to a power of two) when hadamard. fp16/bf16/fp32 [B,H,N,D], D <= 128."""
+    dev = _require_device(q, k)
+    if q.dim() != 4 or k.dim() != 4 or q.numel() == 0 or k.numel() == 0:
+        raise VcxError("Expected nonempty [B,H,N,D]")
+    if q.shape[0] != k.shape[0] or q.shape[1] != k.shape[1] or q.shape[3] != k.shape[3]:
+        raise VcxError("Q/K shapes must match")
+    if q.dtype not in _PRE_DTYPE or k.dtype != q.dtype:
+        raise VcxError("Q/K require one of float16/bfloat16/float32")
+    if q.stride(-1) != 1 or k.stride(-1) != 1:
+        q, k = q.contiguous(), k.contiguous()
+    B, H, Nq, D = q.shape
+    Nk = k.shape[2]
+    W = (1 << (D - 1).bit_length()) if hadamard else D
+    qo = torch.empty((B, H, Nq, W), dtype=torch.float32, device=dev)
+    ko = torch.empty((B, H, Nk, W), dtype=torch.float32, device=dev)
+    ws = _workspace(workspace_bytes(WS_PREPROCESS_QK, B, H, Nk, D), dev) if k_smooth else None
+    _check(lib().vcx_preprocess_qk(_ptr(q), _ptr(k), _PRE_DTYPE[q.dtype], B, H, Nq, Nk, D, *q.stride()[:3],
+                                   *k.stride()[:3], int(k_smooth), int(hadamard), _ptr(qo), _ptr(ko), _ptr(ws),
+                                   0 if ws is None else ws.numel(), _stream(dev)), "vcx_preprocess_qk")
+    return qo, ko
 
 
 @torch.no_grad()

@@ -44,12 +44,13 @@ enum vcx_status {
   VCX_EHIP = 3          /* a HIP runtime call failed */
 };
 
-enum vcx_dtype { VCX_FLOAT16 = 0, VCX_BFLOAT16 = 1 };
+enum vcx_dtype { VCX_FLOAT16 = 0, VCX_BFLOAT16 = 1, VCX_FLOAT32 = 2 /* vcx_preprocess_qk only */ };
 
 enum vcx_workspace_op {
   VCX_WS_PREPARE_QK = 1, /* vcx_prepare_qk_int8 */
   VCX_WS_PREPARE_V = 2,  /* vcx_prepare_v_fp8 (smoothing off or on) */
-  VCX_WS_GROUP = 3       /* vcx_group_values */
+  VCX_WS_GROUP = 3,      /* vcx_group_values */
+  VCX_WS_PREPROCESS_QK = 4 /* vcx_preprocess_qk (k_smooth = 1); any D in 1..128 */
 };
 
 /* Library ABI version (VCX_ABI_VERSION). Replaces the reference's build-stamp
@@ -95,6 +96,31 @@ int vcx_prepare_qk_int8(const void* q, const void* k, int dtype, int64_t B, int6
                         int64_t q_sn, int64_t k_sb, int64_t k_sh, int64_t k_sn,
                         const int64_t* perm, int8_t* q8, float* qs, int8_t* k8, float* ks,
                         void* km_out, void* workspace, size_t workspace_bytes, void* stream);
+
+/* vcx_prepare_qk_int8 with Q and the centred K rotated by the normalized Sylvester-
+ * Hadamard transform before the INT8 quantizer: q' = H(q), k' = H(RN_in(k - km)), in
+ * binary32 with butterflies of stride 1, 2, 4, ... ((a + b, a - b), each RN) and a final
+ * multiply by RN_f32(1/sqrt(D)); not rounded back to the input dtype. Same arguments,
+ * outputs and workspace as vcx_prepare_qk_int8. No counterpart inside the reference's
+ * sageattn_vc, whose H200_INT8.md:99-104 names the rotation as its remaining gap; the
+ * transform is the reference's (src/vc_attention/core.py:79-107, csrc/kernels.cu:104-123). */
+int vcx_prepare_qk_int8_rotated(const void* q, const void* k, int dtype, int64_t B, int64_t H,
+                                int64_t Nq, int64_t Nk, int64_t D, int64_t q_sb, int64_t q_sh,
+                                int64_t q_sn, int64_t k_sb, int64_t k_sh, int64_t k_sn,
+                                const int64_t* perm, int8_t* q8, float* qs, int8_t* k8, float* ks,
+                                void* km_out, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Post-RoPE Q/K preprocessing in binary32: inputs (fp16, bf16 or fp32; D in 1..128; strided)
+ * are widened; k_smooth subtracts K's binary32 channel mean RN_f32(S/Nk) (S the binary64 sum
+ * per 128-key tile in key order, then over tiles in order); hadamard rotates Q and K rows as
+ * above with W = the power of two >= D (zero padded). Outputs q_out [B,H,Nq,W'] and
+ * k_out [B,H,Nk,W'] binary32 contiguous, W' = hadamard ? W : D. Workspace
+ * VCX_WS_PREPROCESS_QK when k_smooth (else nullable).
+ * Replaces the reference's preprocess_qk (csrc/bindings.cpp:87-116, kernels.cu:104-123,396-405). */
+int vcx_preprocess_qk(const void* q, const void* k, int dtype, int64_t B, int64_t H, int64_t Nq,
+                      int64_t Nk, int64_t D, int64_t q_sb, int64_t q_sh, int64_t q_sn, int64_t k_sb,
+                      int64_t k_sh, int64_t k_sn, int k_smooth, int hadamard, float* q_out,
+                      float* k_out, void* workspace, size_t workspace_bytes, void* stream);
 
 /* Q/K block-scaled E4M3 (the experimental vc27 QK format). K is centred by its
  * binary32 channel mean km = RN_f32(S/Nk) (S the fp64 sum in this library's fixed

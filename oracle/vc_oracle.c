@@ -306,6 +306,90 @@ VCO_EXPORT void vco_k_mean(const uint16_t* k, int dtype, int64_t BH, int64_t n, 
 }
 
 /* ------------------------------------------------------------------ */
+/* Normalized Sylvester-Hadamard rotation of Q/K rows                 */
+/* ------------------------------------------------------------------ */
+
+/* In place on one row of W = 2^p binary32 values: for stride s = 1, 2, 4, ..., W/2 every
+ * pair (i, i + s) with bit s of i clear becomes (x_i + x_{i+s}, x_i - x_{i+s}), each RN;
+ * then every value is multiplied by norm = RN_f32(1 / sqrt(W)) (computed in binary64).
+ * Reference: hadamard, src/vc_attention/core.py:79-92 (stride order, (left+right,
+ * left-right)); transform_qk_kernel, csrc/kernels.cu:104-123 and its normalization :402. */
+static void hadamard_row(float* x, int W) {
+  for (int s = 1; s < W; s <<= 1)
+    for (int i = 0; i < W; ++i)
+      if (!(i & s)) {
+        const float a = x[i], b = x[i + s];
+        x[i] = a + b;
+        x[i + s] = a - b;
+      }
+  const float norm = (float)(1.0 / sqrt((double)W));
+  for (int i = 0; i < W; ++i) x[i] = x[i] * norm;
+}
+
+static int pow2_at_least(int D) {
+  int W = 1;
+  while (W < D) W <<= 1;
+  return W;
+}
+
+/* rows x D binary32 values -> rows x W (W the power of two >= D; zero padded). */
+VCO_EXPORT void vco_hadamard(const float* x, int64_t rows, int D, float* out) {
+  const int W = pow2_at_least(D);
+  for (int64_t r = 0; r < rows; ++r) {
+    float* y = out + r * W;
+    for (int i = 0; i < W; ++i) y[i] = i < D ? x[r * D + i] : 0.0f;
+    hadamard_row(y, W);
+  }
+}
+
+/* Reference preprocess_qk (csrc/bindings.cpp:87-116; core.py:96-107): inputs widened to
+ * binary32; k_smooth subtracts the binary32 channel mean of K, km = RN_f32(S/n) with S the
+ * binary64 sum over keys, taken per 128-key tile in key order and then over tiles in
+ * order; hadamard rotates Q and (centred) K rows (width W = pow2 >= D, else D).
+ * dtype: 0 fp16, 1 bf16, 2 fp32 (element type of q and k, contiguous [BH][n][D]).
+ * qo [BH][nq][Wq], ko [BH][nk][W]; Q is copied unchanged when hadamard = 0. */
+static float load_any(const void* p, int64_t i, int dtype) {
+  if (dtype == 2) return ((const float*)p)[i];
+  return load_in((const uint16_t*)p + i, dtype);
+}
+
+VCO_EXPORT void vco_preprocess_qk(const void* q, const void* k, int dtype, int64_t BH, int64_t nq,
+                                  int64_t nk, int D, int k_smooth, int hadamard, float* qo, float* ko) {
+  const int W = hadamard ? pow2_at_least(D) : D;
+  const int64_t tiles = (nk + 127) / 128;
+  float* mean = (float*)calloc((size_t)D, sizeof(float));
+  for (int64_t h = 0; h < BH; ++h) {
+    if (k_smooth) {
+      for (int d = 0; d < D; ++d) {
+        double total = 0.0;
+        for (int64_t t = 0; t < tiles; ++t) {
+          double part = 0.0;
+          for (int64_t key = t * 128; key < nk && key < t * 128 + 128; ++key)
+            part += (double)load_any(k, (h * nk + key) * D + d, dtype);
+          total += part;
+        }
+        mean[d] = (float)(total / (double)nk);
+      }
+    }
+    for (int64_t r = 0; r < nq; ++r) {
+      float* y = qo + (h * nq + r) * W;
+      for (int i = 0; i < W; ++i) y[i] = i < D ? load_any(q, (h * nq + r) * D + i, dtype) : 0.0f;
+      if (hadamard) hadamard_row(y, W);
+    }
+    for (int64_t r = 0; r < nk; ++r) {
+      float* y = ko + (h * nk + r) * W;
+      for (int i = 0; i < W; ++i) {
+        float x = i < D ? load_any(k, (h * nk + r) * D + i, dtype) : 0.0f;
+        if (k_smooth && i < D) x = x - mean[i];
+        y[i] = x;
+      }
+      if (hadamard) hadamard_row(y, W);
+    }
+  }
+  free(mean);
+}
+
+/* ------------------------------------------------------------------ */
 /* Sage per-thread INT8 quantizer                                     */
 /* ------------------------------------------------------------------ */
 
@@ -328,26 +412,45 @@ static inline int8_t int8_code(float x, float s) {
  * contribute 0 and groups made only of such rows get scale 1e-7f).
  * Reference: quant_per_thread.py:21-46, launch :180-193 (BLKQ=64, WARPQ=16
  * from sal/sageattention_local/vc.py:159). q: [BH][n][D]; q8 [BH][n][D]. */
-VCO_EXPORT void vco_quant_q(const uint16_t* q, int dtype, int64_t BH, int64_t n, int D,
-                            int8_t* q8, float* qs) {
+static void quant_q_rows(const uint16_t* q, int dtype, int64_t BH, int64_t n, int D, int rotate,
+                         int8_t* q8, float* qs) {
   int64_t groups16 = (n + 63) / 64 * 4;
+  float* rows = (float*)malloc(sizeof(float) * 2 * D);
   for (int64_t h = 0; h < BH; ++h) {
     for (int64_t g = 0; g < groups16; ++g) {
       for (int t = 0; t < 8; ++t) {
-        int64_t r0 = g * 16 + t, r1 = r0 + 8;
+        int64_t r0 = g * 16 + t;
         float amax = 0.0f;
-        for (int64_t r = r0; r <= r1; r += 8)
-          if (r < n)
-            for (int d = 0; d < D; ++d) amax = fmaxf(amax, fabsf(load_in(q + (h * n + r) * D + d, dtype)));
+        for (int e = 0; e < 2; ++e) {
+          const int64_t r = r0 + 8 * e;
+          for (int d = 0; d < D; ++d) rows[e * D + d] = r < n ? load_in(q + (h * n + r) * D + d, dtype) : 0.0f;
+          if (rotate) hadamard_row(rows + e * D, D);
+          for (int d = 0; d < D; ++d) amax = fmaxf(amax, fabsf(rows[e * D + d]));
+        }
         float s = int8_scale(amax);
         qs[h * groups16 * 8 + g * 8 + t] = s;
-        for (int64_t r = r0; r <= r1; r += 8)
+        for (int e = 0; e < 2; ++e) {
+          const int64_t r = r0 + 8 * e;
           if (r < n)
-            for (int d = 0; d < D; ++d)
-              q8[(h * n + r) * D + d] = int8_code(load_in(q + (h * n + r) * D + d, dtype), s);
+            for (int d = 0; d < D; ++d) q8[(h * n + r) * D + d] = int8_code(rows[e * D + d], s);
+        }
       }
     }
   }
+  free(rows);
+}
+
+VCO_EXPORT void vco_quant_q(const uint16_t* q, int dtype, int64_t BH, int64_t n, int D,
+                            int8_t* q8, float* qs) {
+  quant_q_rows(q, dtype, BH, n, D, 0, q8, qs);
+}
+
+/* The same quantizer on Hadamard-rotated rows: q' = hadamard_row(float(q)) in binary32, not
+ * rounded back to the input dtype. No counterpart in the reference's sageattn_vc (the
+ * rotation is the gap its H200_INT8.md:99-104 names); the rotation is core.py:79-92's. */
+VCO_EXPORT void vco_quant_q_rot(const uint16_t* q, int dtype, int64_t BH, int64_t n, int D,
+                                int8_t* q8, float* qs) {
+  quant_q_rows(q, dtype, BH, n, D, 1, q8, qs);
 }
 
 /* K: after centring k'' = RN_in(RN_f32(k - km)) (vc.py:158 and
@@ -355,8 +458,8 @@ VCO_EXPORT void vco_quant_q(const uint16_t* q, int dtype, int64_t BH, int64_t n,
  * t = (key%8)/2, i.e. keys 128j + 8i + 2t + e; scale index j*4 + t.
  * Reference: quant_per_thread.py:48-98, launch :181,195-202 (BLKK=128, WARPK=128).
  * perm (nullable) gathers keys first (vc.py:155). km (nullable) disables centring. */
-VCO_EXPORT void vco_quant_k(const uint16_t* k, int dtype, int64_t BH, int64_t n, int D,
-                            const int64_t* perm, const uint16_t* km, int8_t* k8, float* ks) {
+static void quant_k_rows(const uint16_t* k, int dtype, int64_t BH, int64_t n, int D,
+                         const int64_t* perm, const uint16_t* km, int rotate, int8_t* k8, float* ks) {
   int64_t tiles = (n + 127) / 128;
   float* buf = (float*)malloc(sizeof(float) * 32 * D);
   for (int64_t h = 0; h < BH; ++h) {
@@ -375,8 +478,9 @@ VCO_EXPORT void vco_quant_k(const uint16_t* k, int dtype, int64_t BH, int64_t n,
                 if (km) x = round_in(x - load_in(km + h * D + d, dtype), dtype);
               }
               row[d] = x;
-              amax = fmaxf(amax, fabsf(x));
             }
+            if (rotate) hadamard_row(row, D);
+            for (int d = 0; d < D; ++d) amax = fmaxf(amax, fabsf(row[d]));
           }
         float s = int8_scale(amax);
         ks[h * tiles * 4 + j * 4 + t] = s;
@@ -390,6 +494,17 @@ VCO_EXPORT void vco_quant_k(const uint16_t* k, int dtype, int64_t BH, int64_t n,
     }
   }
   free(buf);
+}
+
+VCO_EXPORT void vco_quant_k(const uint16_t* k, int dtype, int64_t BH, int64_t n, int D,
+                            const int64_t* perm, const uint16_t* km, int8_t* k8, float* ks) {
+  quant_k_rows(k, dtype, BH, n, D, perm, km, 0, k8, ks);
+}
+
+/* Rotated K: k'' = RN_in(RN_f32(k - km)) as above, then hadamard_row in binary32. */
+VCO_EXPORT void vco_quant_k_rot(const uint16_t* k, int dtype, int64_t BH, int64_t n, int D,
+                                const int64_t* perm, const uint16_t* km, int8_t* k8, float* ks) {
+  quant_k_rows(k, dtype, BH, n, D, perm, km, 1, k8, ks);
 }
 
 /* ------------------------------------------------------------------ */

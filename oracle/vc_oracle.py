@@ -84,6 +84,10 @@ def _declare(L):
     L.vco_attention_fp8.argtypes = [P, P, P, P, P, P, i64, i64, i64, i32, f32, P, i64, P, P, i32]
     L.vco_k_mean_f32.argtypes = [P, i32, i64, i64, i32, P]
     L.vco_quant_fp8_block.argtypes = [P, i32, i64, i64, i32, i32, P, P, P]
+    L.vco_quant_q_rot.argtypes = L.vco_quant_q.argtypes
+    L.vco_quant_k_rot.argtypes = L.vco_quant_k.argtypes
+    L.vco_hadamard.argtypes = [P, i64, i32, P]
+    L.vco_preprocess_qk.argtypes = [P, P, i32, i64, i64, i64, i32, i32, i32, P, P]
 
 
 def _ptr(a):
@@ -175,24 +179,56 @@ def k_mean(k, perm=None, dtype: str = "bfloat16") -> np.ndarray:
     return km
 
 
-def quant_q(q, dtype: str = "bfloat16"):
+def quant_q(q, dtype: str = "bfloat16", rotate: bool = False):
+    """Sage per-thread INT8 Q; rotate=True quantizes the Hadamard-rotated rows."""
     B, H, N, D = _shape4(q)
     q = _c(q, np.uint16)
     q8 = np.zeros((B, H, N, D), np.int8)
     qs = np.empty((B, H, (N + 63) // 64 * 32), np.float32)
-    lib().vco_quant_q(_ptr(q), DTYPES[dtype], B * H, N, D, _ptr(q8), _ptr(qs))
+    fn = lib().vco_quant_q_rot if rotate else lib().vco_quant_q
+    fn(_ptr(q), DTYPES[dtype], B * H, N, D, _ptr(q8), _ptr(qs))
     return q8, qs
 
 
-def quant_k(k, km=None, perm=None, dtype: str = "bfloat16"):
+def quant_k(k, km=None, perm=None, dtype: str = "bfloat16", rotate: bool = False):
+    """Sage per-thread INT8 K after centring; rotate=True rotates the centred rows first."""
     B, H, N, D = _shape4(k)
     k = _c(k, np.uint16)
     km = None if km is None else _c(km, np.uint16)
     perm = None if perm is None else _c(perm, np.int64)
     k8 = np.zeros((B, H, N, D), np.int8)
     ks = np.empty((B, H, (N + 127) // 128 * 4), np.float32)
-    lib().vco_quant_k(_ptr(k), DTYPES[dtype], B * H, N, D, _ptr(perm), _ptr(km), _ptr(k8), _ptr(ks))
+    fn = lib().vco_quant_k_rot if rotate else lib().vco_quant_k
+    fn(_ptr(k), DTYPES[dtype], B * H, N, D, _ptr(perm), _ptr(km), _ptr(k8), _ptr(ks))
     return k8, ks
+
+
+def hadamard(x) -> np.ndarray:
+    """Normalized Sylvester rotation of the last axis (core.py:79-92), zero padded to a
+    power of two; binary32 butterflies in stride order."""
+    x = np.ascontiguousarray(x, np.float32)
+    D = x.shape[-1]
+    W = 1 << (D - 1).bit_length()
+    out = np.empty(x.shape[:-1] + (W,), np.float32)
+    lib().vco_hadamard(_ptr(x), x.size // D, D, _ptr(out))
+    return out
+
+
+def preprocess_qk(q, k, *, k_smooth: bool, hadamard: bool, dtype: str = "float32"):
+    """The reference's preprocess_qk (csrc/bindings.cpp:87-116): binary32 K centring over all
+    keys and the normalized Q/K rotation. q, k: [B,H,N,D] arrays of the input dtype
+    (float32 values, or uint16 bit patterns for float16/bfloat16)."""
+    B, H, Nq, D = _shape4(q)
+    Nk = np.asarray(k).shape[2]
+    code = {"float16": 0, "bfloat16": 1, "float32": 2}[dtype]
+    store = np.float32 if code == 2 else np.uint16
+    q, k = _c(q, store), _c(k, store)
+    W = (1 << (D - 1).bit_length()) if hadamard else D
+    qo = np.empty((B, H, Nq, W), np.float32)
+    ko = np.empty((B, H, Nk, W), np.float32)
+    lib().vco_preprocess_qk(_ptr(q), _ptr(k), code, B * H, Nq, Nk, D, int(k_smooth), int(hadamard), _ptr(qo),
+                            _ptr(ko))
+    return qo, ko
 
 
 def k_mean_f32(k, dtype: str = "bfloat16") -> np.ndarray:
@@ -262,17 +298,18 @@ def prepare_values(v, perm=None, channel_scale: bool = True, dtype: str = "bfloa
 
 
 def prepare(q, k, v, *, expcast=True, v_smooth=True, clusters=8, iterations=2, sm_scale=None,
-            v_scale_mode="channel", dtype="bfloat16"):
+            v_scale_mode="channel", dtype="bfloat16", qk_hadamard=False):
     """State dict of the sageattn_vc contract (reference vc.py:141-170); v is LOGICAL.
 
     expcast only selects the probability path of ``reference``; the payloads are the same.
+    qk_hadamard rotates Q and the centred K before the INT8 quantizer.
     """
     perm = None
     if v_smooth:
         perm, _, _ = group_values(v, clusters, iterations, dtype)
     km = k_mean(k, perm, dtype)
-    q8, qs = quant_q(q, dtype)
-    k8, ks = quant_k(k, km, perm, dtype)
+    q8, qs = quant_q(q, dtype, rotate=qk_hadamard)
+    k8, ks = quant_k(k, km, perm, dtype, rotate=qk_hadamard)
     if v_smooth:
         v8, vs, means = prepare_values(v, perm, v_scale_mode == "channel", dtype)
     else:

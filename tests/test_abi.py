@@ -47,6 +47,11 @@ def test_workspace_sizes():
         vcx.workspace_bytes(9, 1, 1, 1, 128)
     with pytest.raises(vcx.VcxError, match="invalid shape"):
         vcx.workspace_bytes(1, 1, 1, 1, 96)
+    # the generic Q/K preprocessing takes any head dimension up to 128
+    # fp64 tile sums [4 heads][1 tile][37] = 1184 B -> 1280, fp32 means 592 B -> 768 (256-byte aligned)
+    assert vcx.workspace_bytes(vcx.WS_PREPROCESS_QK, 2, 2, 35, 37) == 1280 + 768
+    with pytest.raises(vcx.VcxError, match="invalid shape"):
+        vcx.workspace_bytes(vcx.WS_PREPROCESS_QK, 1, 1, 1, 129)
 
 
 def _fwd(**kw):
@@ -74,6 +79,15 @@ def test_invalid_calls_rejected_before_launch():
     rc, msg = _fwd(block_values=0, channel_scale=0)
     assert rc == 1 and "per-block" in msg
     L = vcx.lib()
+    assert L.vcx_preprocess_qk(None, None, 2, 1, 1, 8, 8, 129, 0, 0, 129, 0, 0, 129, 1, 1, None, None, None, 0,
+                               None) == 1
+    assert "1..128" in L.vcx_last_error().decode()
+    assert L.vcx_preprocess_qk(None, None, 3, 1, 1, 8, 8, 37, 0, 0, 37, 0, 0, 37, 1, 1, None, None, None, 0,
+                               None) == 1
+    assert "dtype" in L.vcx_last_error().decode()
+    assert L.vcx_prepare_qk_int8_rotated(None, None, 1, 1, 1, 64, 128, 96, 0, 0, 96, 0, 0, 96, None,
+                                         None, None, None, None, None, None, 0, None) == 1
+    assert "D must be 64 or 128" in L.vcx_last_error().decode()
     assert L.vcx_prepare_qk_fp8(None, None, 1, 1, 1, 64, 128, 96, 0, 0, 96, 0, 0, 96,
                                 None, None, None, None, None, None, 0, None) == 1
     assert "D must be 64 or 128" in L.vcx_last_error().decode()

@@ -718,3 +718,107 @@ def test_fp8_control_path_is_a_softmax_of_the_block_dequantized_logits():
     w2 = np.exp2(lg2 - lg2.max(-1, keepdims=True) + 8.807)
     wrong = (w2 @ dv.T) / w2.sum(-1, keepdims=True)
     assert np.mean(np.abs(wrong - exact) > bound) > 0.3
+
+
+# ------------------------------------------------------------------ Hadamard Q/K rotation
+
+def _explicit_hadamard(width):
+    # Sylvester entries H[i,j] = (-1)**popcount(i & j) / sqrt(width), independent of the
+    # butterfly (tests/test_paper_alignment.py:13-19).
+    i = np.arange(width)
+    pop = np.vectorize(lambda x: bin(x).count("1"))(i[:, None] & i[None, :])
+    return (-1.0) ** pop / math.sqrt(width)
+
+
+@pytest.mark.parametrize("dim", [1, 16, 37, 64, 128])
+def test_hadamard_against_matrix_and_preserves_dot_products(dim):
+    # tests/test_paper_alignment.py:22-29
+    gen = torch.Generator().manual_seed(31)
+    q, k = [torch.randn(2, 3, n, dim, generator=gen).numpy() for n in (7, 11)]
+    width = 1 << (dim - 1).bit_length()
+    hq, hk = o.hadamard(q), o.hadamard(k)
+    expected = np.pad(q.astype(np.float64), [(0, 0)] * 3 + [(0, width - dim)]) @ _explicit_hadamard(width)
+    np.testing.assert_allclose(hq, expected, atol=2e-6, rtol=2e-5)
+    np.testing.assert_allclose(hq @ np.swapaxes(hk, -1, -2), q @ np.swapaxes(k, -1, -2), atol=2e-5, rtol=2e-5)
+    # the rotation is an involution up to rounding: H(H(x)) = x
+    np.testing.assert_allclose(o.hadamard(hq), np.pad(q, [(0, 0)] * 3 + [(0, width - dim)]), atol=3e-6)
+
+
+def test_hadamard_butterfly_order_is_fixed():
+    # Bit-exact values fix the stride order and the (left + right, left - right) pairing: a row
+    # whose sums round differently under another stage order (large and small magnitudes).
+    x = np.array([[1e8, 1.0, 3.0, -1e8, 0.5, 7.0, -2.0, 1e-3]], np.float32)
+    want = x.astype(np.float32).copy()
+    for s in (1, 2, 4):  # the reference's order (core.py:86-91)
+        nxt = want.copy()
+        for i in range(8):
+            if not i & s:
+                nxt[0, i] = np.float32(want[0, i] + want[0, i + s])
+                nxt[0, i + s] = np.float32(want[0, i] - want[0, i + s])
+        want = nxt
+    want = want * np.float32(1 / math.sqrt(8))
+    np.testing.assert_array_equal(o.hadamard(x), want)
+    rev = x.astype(np.float32).copy()
+    for s in (4, 2, 1):
+        nxt = rev.copy()
+        for i in range(8):
+            if not i & s:
+                nxt[0, i] = np.float32(rev[0, i] + rev[0, i + s])
+                nxt[0, i + s] = np.float32(rev[0, i] - rev[0, i + s])
+        rev = nxt
+    assert not np.array_equal(rev * np.float32(1 / math.sqrt(8)), want)
+
+
+@pytest.mark.parametrize("dim", [37, 64, 128])
+@pytest.mark.parametrize("dtype", ["float32", "float16", "bfloat16"])
+@pytest.mark.parametrize("k_smooth,rotate", [(False, False), (False, True), (True, False), (True, True)])
+def test_preprocess_qk_matrix_oracle(dim, dtype, k_smooth, rotate):
+    # tests/test_paper_alignment.py:124-150: K centred over all keys, then both rotated.
+    gen = torch.Generator().manual_seed(14)
+    q, k = [torch.randn(2, 2, n, dim, generator=gen) for n in (13, 35)]
+    k += torch.linspace(-2, 2, dim)
+    tdt = {"float32": torch.float32, "float16": torch.float16, "bfloat16": torch.bfloat16}[dtype]
+    q, k = q.to(tdt), k.to(tdt)
+    arg = (lambda x: x.numpy()) if dtype == "float32" else bits
+    qo, ko = o.preprocess_qk(arg(q), arg(k), k_smooth=k_smooth, hadamard=rotate, dtype=dtype)
+    eq, ek = q.double(), k.double()
+    if k_smooth:
+        ek = ek - ek.mean(-2, keepdim=True)
+    if rotate:
+        width = 1 << (dim - 1).bit_length()
+        m = torch.from_numpy(_explicit_hadamard(width))
+        eq = torch.nn.functional.pad(eq, (0, width - dim)) @ m
+        ek = torch.nn.functional.pad(ek, (0, width - dim)) @ m
+    np.testing.assert_allclose(qo, eq.numpy(), atol=3e-6, rtol=3e-5)
+    np.testing.assert_allclose(ko, ek.numpy(), atol=3e-6, rtol=3e-5)
+
+
+@pytest.mark.parametrize("D", [64, 128])
+def test_rotated_int8_quantizers(D):
+    # The rotated quantizers are the plain ones applied to the rotated rows: checked through
+    # the per-thread invariants (|q8| <= 127, each group's maximum maps to +-127, the
+    # dequantized rows within s/2 + ulp of the rotated rows) and the preserved dot products.
+    q, k, _ = make_qkv(1, 2, 200, 300, D, torch.bfloat16, seed=8, kind="outlier")
+    qb, kb = bits(q), bits(k)
+    km = o.k_mean(kb)
+    q8, qs = o.quant_q(qb, rotate=True)
+    k8, ks = o.quant_k(kb, km, rotate=True)
+    rq = o.hadamard(q.float().numpy())
+    kmf = torch.from_numpy(np.ascontiguousarray(km).view(np.int16)).view(torch.bfloat16).float()
+    kc = (k.float() - kmf.reshape(1, 2, 1, D)).to(torch.bfloat16).float().numpy()
+    rk = o.hadamard(kc)
+    rows = np.arange(200)
+    sq = qs[:, :, (rows // 16) * 8 + rows % 8]
+    deq = q8.astype(np.float64) * sq[..., None]
+    assert np.all(np.abs(deq - rq) <= sq[..., None] / 2 * (1 + 1e-6) + 1e-6)
+    assert np.abs(q8).max() == 127
+    keys = np.arange(300)
+    sk = ks[:, :, (keys // 128) * 4 + (keys % 8) // 2]
+    dk = k8.astype(np.float64) * sk[..., None]
+    assert np.all(np.abs(dk - rk) <= sk[..., None] / 2 * (1 + 1e-6) + 1e-6)
+    # scores of the rotated payloads approximate the unrotated centred scores
+    exact = q.double().numpy() @ np.swapaxes(kc.astype(np.float64), -1, -2)
+    approx = deq @ np.swapaxes(dk, -1, -2)
+    assert np.abs(approx - exact).max() <= 0.05 * np.abs(exact).max()
+    # rotation changes the bytes (it is not silently skipped)
+    assert not np.array_equal(q8, o.quant_q(qb)[0])

@@ -51,7 +51,6 @@ def test_config_fields_and_defaults_match_reference():
     (dict(qk_format="int4"), "qk_format"),
     (dict(HIP, qk_format="fp8_block"), "qk_format='int8'"),
     (dict(HIP, q_block=128), "q_block=64"),
-    (dict(HIP, qk_hadamard=True), "qk_hadamard=False"),
     (dict(HIP, mean_dtype="float32"), "mean_dtype='float16'"),
     (dict(HIP, clusters=9), "at most 8 clusters"),
 ])
@@ -66,6 +65,7 @@ def test_config_accepts_reference_and_hip_configurations():
     Config(backend="npu_fp8", k_quant_block=256, kv_block=128)
     Config(**HIP, v_smooth=True, clusters=8, iterations=2)
     Config(**dict(HIP, expcast=False))  # the Sage FP8 control arm (reference replay.py:17)
+    Config(**dict(HIP, qk_hadamard=True))  # Q/K rotation inside the INT8 quantizers
 
 
 def _counting_grouping(calls):

@@ -79,7 +79,7 @@ def make_inputs(B, H, N, D, kind, seed=0):
     return q.to(torch.bfloat16), k.to(torch.bfloat16), v.to(torch.bfloat16)
 
 
-def cpu_baseline(q, k, v, smooth, rows, budget_s, qk="int8"):
+def cpu_baseline(q, k, v, smooth, rows, budget_s, qk="int8", rotate=False):
     """The CPU oracle (C restatement, OpenMP over rows) on the box's host cores:
     full preprocessing of the same workload plus attention for `rows` evenly
     spaced query rows of every head against all keys, extrapolated to all rows."""
@@ -91,7 +91,7 @@ def cpu_baseline(q, k, v, smooth, rows, budget_s, qk="int8"):
     B, H, N, D = q.shape
     qb, kb, vb = bits(q), bits(k), bits(v)
     t0 = time.perf_counter()
-    st = o.prepare_fp8(qb, kb, vb) if qk == "fp8" else o.prepare(qb, kb, vb, v_smooth=smooth)
+    st = o.prepare_fp8(qb, kb, vb) if qk == "fp8" else o.prepare(qb, kb, vb, v_smooth=smooth, qk_hadamard=rotate)
     prep_s = time.perf_counter() - t0
     # Without smoothing the GPU path uses the folded ExpCast encode, whose fallback is decided
     # per 16-row group: sample whole groups so the oracle's group pass covers only them.
@@ -131,6 +131,8 @@ def main():
     ap.add_argument("--config", default="main", choices=sorted(CONFIGS))
     ap.add_argument("--cpu-rows", type=int, default=2048, help="query rows per head for the CPU baseline")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--qk-hadamard", action="store_true",
+                    help="rotate Q and the centred K (normalized Hadamard) inside the INT8 quantizers")
     ap.add_argument("--qk", default="int8", choices=("int8", "fp8"),
                     help="int8: the sageattn_vc path (headline); fp8: the block-scaled FP8 QK variant")
     ap.add_argument("--mode", default="full", choices=("full", "kernel", "copy"),
@@ -148,6 +150,9 @@ def main():
 
     B, H, N, D, kind, smooth, desc = CONFIGS[args.config]
     fp8 = args.qk == "fp8"
+    if fp8 and args.qk_hadamard:
+        print("bench.py: --qk-hadamard applies to the INT8 path", file=sys.stderr)
+        sys.exit(2)
     if fp8 and smooth:
         print(f"bench.py: --qk fp8 has no V smoothing; config {args.config!r} needs it", file=sys.stderr)
         sys.exit(2)
@@ -175,7 +180,7 @@ def main():
             v8, vs, means = vcx.prepare_v(v, None, smooth=False, channel_scale=True)
             return q8, qs, k8, ks, v8, vs, means
         perm = vcx.group_values(v, clusters, iterations) if smooth else None
-        q8, qs, k8, ks, _ = vcx.prepare_qk(q, k, perm)
+        q8, qs, k8, ks, _ = vcx.prepare_qk(q, k, perm, hadamard=args.qk_hadamard)
         v8, vs, means = vcx.prepare_v(v, perm, smooth=smooth, channel_scale=True)
         return q8, qs, k8, ks, v8, vs, means
 
@@ -243,6 +248,7 @@ def main():
         "data": "synthetic (seeded torch.Generator on CPU, cast to bf16, copied to HBM before timing)",
         "config": {"workload": desc, "shape_bnsd": [B, H, N, D], "config_name": args.config,
                    "v_smooth": smooth, "expcast": True, "qk_format": "fp8_block" if fp8 else "int8",
+                   "qk_hadamard": args.qk_hadamard,
                    "expcast_encode": "unfused (block values)" if smooth else "folded (the reference's default kernel mode)"},
         "kernel_ms": round(kernel_ms, 4),
         "prep_ms": round(prep_med, 4),
@@ -256,7 +262,8 @@ def main():
                           "frac": round(prep_gbs / PEAK_HBM_GBS, 4), "algorithmic_bytes": prep_bytes},
     }
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(qc, kc, vc_, smooth, args.cpu_rows, 30.0, args.qk)
+        result["cpu_baseline"] = cpu_baseline(qc, kc, vc_, smooth, args.cpu_rows, 30.0, args.qk,
+                                              args.qk_hadamard)
     print(json.dumps(result), flush=True)
 
 

@@ -15,8 +15,8 @@
 // the V payload is stored in the matching order (vcx_value_token).
 //
 // K and V^T tiles stream through LDS with gfx950 direct-to-LDS loads
-// (global_load_lds_dwordx4), double buffered, XOR-swizzled so that the 16
-// lanes of a lane group hit 16 distinct 16-byte bank groups.
+// (global_load_lds_dwordx4), double buffered, placed so that the operand reads
+// run at the conflict-free ds_read_b128 rate (key_row / chunk_xor below).
 //
 // Numerical contract (reference sal/csrc/vc/vc_sm90.cu:284-612, vc_math.cuh:268-474):
 //   tiles before the last: logit = RN(float(acc) * RN(sm * RN(qs*ks)))
@@ -74,25 +74,32 @@ struct AttnArgs {
   int64_t prow0, prow1;
 };
 
-// XOR swizzles of the 16-byte chunk index inside an LDS row. A lane group
-// (16 lanes) of the QK A operand reads rows 16j + kr(l), kr = 0..15, at one
-// logical chunk; of the PV A operand rows 16cb + l. Both maps are bijective on
-// every 8-lane half (one 128-byte LDS pass) and on the whole 16-lane group (one
-// 256-byte pass), so neither reading model has bank conflicts.
-template <int D>
-__device__ inline int swz_k(int row) {
-  if constexpr (D == 128) return ((row >> 1) & 1) | (((row >> 3) & 1) << 1) | (((row ^ (row >> 2)) & 1) << 2);
-  else return (((row >> 1) ^ (row >> 2)) & 1) | (((row >> 3) & 1) << 1);
+// LDS placement of the K and V^T tiles. Both operands are read as lane (G = l/16,
+// li = l%16) -> LDS row 16b + li, physical 16-byte chunk X ^ x(li), where X is what the
+// lane group needs (QK: 4ds + G; PV: 4h + G) and x(li) = li & 7 for 128-byte rows,
+// (li >> 1) & 3 for the 64-byte K rows of D64. On gfx950 this read pattern runs at the
+// conflict-free ds_read_b128 rate (4.55 clocks per wave instruction per CU, measured);
+// XORs keyed on the key row instead of the reading lane ran 2-way conflicted (8.2).
+//  K:   LDS row p holds key 16(p/16) + kr(p%16) (kr: the MFMA row order, whose lane
+//       group G gets Sage K-scale group (key%8)/2 == G); chunk q holds channel chunk
+//       q ^ x(p).
+//  V^T: LDS row = channel; physical chunk q holds token chunk 2(q' & 3) + q'/4 with
+//       q' = q ^ (channel & 7), so lane group G finds its chunks 2G, 2G + 1 at 4h + G.
+__device__ inline int key_row(int p) {
+  const int r = p & 15;
+  return (p & ~15) + 8 * ((r & 3) >> 1) + 2 * (r >> 2) + (r & 1);
 }
-__device__ inline int swz_v(int row) { return ((row >> 1) & 3) | (((row ^ (row >> 3)) & 1) << 2); }
+template <int D>
+__device__ inline int chunk_xor(int p) { return D == 128 ? (p & 7) : ((p >> 1) & 3); }
 
 typedef __attribute__((address_space(3))) void lds_void;
 typedef const __attribute__((address_space(1))) void global_void;
 
 // Direct-to-LDS loads of one key tile. Each of the 4 waves issues D/32
 // instructions for K and D/32 for V^T; instruction n of wave w fills the 64
-// consecutive 16-byte slots (w*(D/32) + n)*64 + lane. A slot holds row
-// s/(D/16) (K) or s/8 (V^T) and the 16-byte chunk given by the XOR swizzle.
+// consecutive 16-byte slots (w*(D/32) + n)*64 + lane. Slot s is LDS row s/(D/16) (K)
+// or s/8 (V^T) at physical chunk s%(D/16) or s%8; the source row and chunk follow the
+// placement above.
 // Lane-constant parts of the addresses are precomputed once per kernel.
 // Raw buffer resource over [base, base + bytes): out-of-range lanes read zeros.
 __device__ inline __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
@@ -128,10 +135,10 @@ struct TileLoader {
 #pragma unroll
     for (int n = 0; n < N; ++n) {
       const int s = (wave * N + n) * 64 + lane;
-      const int row = s / (D / 16), phys = s % (D / 16);
-      koff[n] = static_cast<uint32_t>(row * D + ((phys ^ swz_k<D>(row)) * 16));
-      const int ch = s >> 3, vphys = s & 7;
-      voff[n] = static_cast<uint32_t>(ch * static_cast<int>(npad) + ((vphys ^ swz_v(ch)) * 16));
+      const int p = s / (D / 16), phys = s % (D / 16);
+      koff[n] = static_cast<uint32_t>(key_row(p) * D + ((phys ^ chunk_xor<D>(p)) * 16));
+      const int ch = s >> 3, q = (s & 7) ^ (ch & 7);
+      voff[n] = static_cast<uint32_t>(ch * static_cast<int>(npad) + (2 * (q & 3) + (q >> 2)) * 16);
     }
     // Per-head resources. K rows past Nk read zeros (their logits are masked anyway).
     rk = make_rsrc(a.k8 + bh * a.Nk * D, static_cast<uint32_t>(a.Nk * D));
@@ -538,12 +545,10 @@ __global__ __launch_bounds__(kThreadsPerBlock, 2) void attn_kernel(AttnArgs a) {
   w.li = lane & 15;
   w.bh_ = bh;
   // Lane-constant LDS offsets.
-  const int kr = 8 * ((w.li & 3) >> 1) + 2 * (w.li >> 2) + (w.li & 1);
 #pragma unroll
-  for (int ds = 0; ds < W::DS; ++ds)
-    w.koff[ds] = kr * D + ((((D == 128) ? 4 * ds : 0) + w.G) ^ swz_k<D>(kr)) * 16;
+  for (int ds = 0; ds < W::DS; ++ds) w.koff[ds] = w.li * D + ((((D == 128) ? 4 * ds : 0) + w.G) ^ chunk_xor<D>(w.li)) * 16;
 #pragma unroll
-  for (int h = 0; h < 2; ++h) w.voff[h] = w.li * kTile + (((2 * w.G + h) ^ swz_v(w.li)) * 16);
+  for (int h = 0; h < 2; ++h) w.voff[h] = w.li * kTile + (((4 * h + w.G) ^ (w.li & 7)) * 16);
 
   // Q fragments (B operand) and per-row scales.
 #pragma unroll

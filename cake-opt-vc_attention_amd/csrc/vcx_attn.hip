@@ -25,7 +25,9 @@
 //   alpha = exp2((m - m') * log2(e)) (hardware exp2; alpha == 1 exactly when m' == m)
 //   O = alpha*O + PV (+ mass*mean), den = alpha*den + mass, out = O/den * vs.
 // The P bytes follow the contract exactly; alpha, O and den only feed the
-// bf16/fp16 output, whose tolerance covers the exp2 approximation.
+// bf16/fp16 output, whose tolerance covers the exp2 approximation. With per-channel
+// V scales (VM 1) the mass*mean term is deferred: every 16 tiles one f16 MFMA per
+// channel block adds sum_t mean_t (x) w_t, w_t the tile mass rescaled with O.
 //
 // PM = 2 (expcast = 2, no block values) is the folded encode of the reference's default
 // kernel modes (vc_math.cuh:16-111): code = sat_u8(RNE(fmaf(base, RN(scale*A), fmaf(-m', A, B))))
@@ -109,14 +111,20 @@ __device__ inline __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t by
 // Value modes: VM 0 = no smoothing (per-channel V scale in the epilogue),
 // 1 = block-mean smoothing with per-channel scales, 2 = block-mean smoothing
 // with per-block scales (applied to every tile's contribution).
+// VM 1 defers the block-mean restore: the fp16 means of tile t land in slot t % kRing of
+// an LDS ring, and every kChunk tiles one f16 MFMA per channel block adds
+// sum_t mean_t (x) w_t to O (w_t: the row's tile mass, rescaled like O).
+constexpr int kChunk = 16, kRing = 32;
+
 template <int D, int VM, int QF = 0>
 struct TileLoader {
-  static constexpr bool SMOOTH = VM >= 1, BSCALE = VM == 2;
-  // Meta region of a buffer: SMOOTH ? fp16 means of the tile (2*D bytes) : nothing,
+  static constexpr bool SMOOTH = VM >= 1, BSCALE = VM == 2, RING = VM == 1;
+  // Meta region of a buffer: BSCALE ? fp16 means of the tile (2*D bytes) : nothing,
   // then BSCALE ? the tile's fp32 V scales (4*D bytes) : nothing, then the tile's
   // K scales (INT8: 4 Sage key-group scales, 16 bytes; FP8 block: one scale, 4 bytes).
-  // Means and K scales are loaded by wave 0, V scales by wave 1.
-  static constexpr int ML = SMOOTH ? (2 * D) / 16 : 0;
+  // Means (meta or ring) and K scales are loaded by wave 0, V scales by wave 1.
+  static constexpr int MR = SMOOTH ? (2 * D) / 16 : 0;  // lanes that load the tile's means
+  static constexpr int ML = BSCALE ? MR : 0;
   static constexpr int VL = BSCALE ? (4 * D) / 16 : 0;
   static constexpr int VS_OFF = 16 * ML;
   static constexpr int KS_OFF = 16 * (ML + VL);
@@ -126,6 +134,7 @@ struct TileLoader {
   uint32_t voff[N];                 // lane byte offset inside the V^T tile columns
   uint32_t moff;                    // lane byte offset of the meta load (wave 0)
   __amdgpu_buffer_rsrc_t rk, rv, rm, rs, rb;
+  uint8_t* ring;                    // RING: LDS ring of kRing tiles x D fp16 means
   int wave;
 
   __device__ inline void init(const AttnArgs& a, int64_t bh) {
@@ -156,8 +165,9 @@ struct TileLoader {
     const int lane = threadIdx.x & 63;
     if (wave == 0) {
       if constexpr (SMOOTH) {
-        if (lane < ML)
-          __builtin_amdgcn_raw_ptr_buffer_load_lds(rm, (lds_void*)lm, 16, moff, static_cast<int>(t * D * 2), 0, 0);
+        uint8_t* dst = RING ? ring + (t % kRing) * (2 * D) : lm;
+        if (lane < MR)
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(rm, (lds_void*)dst, 16, moff, static_cast<int>(t * D * 2), 0, 0);
       }
       if (lane == 0) {
         if constexpr (QF == 1)
@@ -230,6 +240,7 @@ struct Wave {
   int64_t row[2];
   float m[2], den[2];
   v4f O[2][CB];
+  float wts[2][4];  // VM 1: pending mean weights of chunk tiles 4G..4G+3 (row li)
   int koff[DS], voff[2];
   int G, li;
   int64_t bh_;
@@ -452,6 +463,10 @@ struct Wave {
       if (__any(alpha[qg] != 1.0f)) {
 #pragma unroll
         for (int cb = 0; cb < CB; ++cb) O[qg][cb] *= alpha[qg];
+        if constexpr (VM == 1) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) wts[qg][j] *= alpha[qg];
+        }
       }
     }
 
@@ -507,19 +522,45 @@ struct Wave {
       else mass[qg] = tmass[qg];
       den[qg] = den[qg] * alpha[qg] + mass[qg];
     }
-    if constexpr (SMOOTH) {
+    if constexpr (VM == 1) {
+      // Deferred block-mean restore: tile t is position c of its chunk; lane group
+      // G = c / 4 keeps the row's mass in slot c % 4 (the MFMA's k = c). At the chunk's
+      // end (or the last tile) O^T[ch][row] += sum_k mean_k[ch] * w_k[row] over the
+      // chunk, as v_mfma_f32_16x16x16f16 (A: means from the ring, exact in fp16;
+      // B: the weights rounded to fp16). Slots of tiles past the last hold w = 0.
+      const int c = static_cast<int>(t & (kChunk - 1));
 #pragma unroll
-      for (int cb = 0; cb < CB; ++cb) {
-        const uint2 hm = *reinterpret_cast<const uint2*>(lm + 32 * cb + 8 * G);
-        const float mean[4] = {f16_bits_to_f32(hm.x & 0xffffu), f16_bits_to_f32(hm.x >> 16),
-                               f16_bits_to_f32(hm.y & 0xffffu), f16_bits_to_f32(hm.y >> 16)};
+      for (int qg = 0; qg < 2; ++qg)
 #pragma unroll
-        for (int qg = 0; qg < 2; ++qg)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) O[qg][cb][r] = __builtin_fmaf(mass[qg], mean[r], O[qg][cb][r]);
-      }
+        for (int j = 0; j < 4; ++j) wts[qg][j] = (G == (c >> 2) && j == (c & 3)) ? mass[qg] : wts[qg][j];
+      if (LAST || c == kChunk - 1) flush_means(ring, t - c);
     }
   }
+
+  // O += means (x) weights over the chunk that starts at tile `base` (VM 1).
+  __device__ inline void flush_means(const uint8_t* ring, int64_t base) {
+    typedef _Float16 v4h __attribute__((ext_vector_type(4)));
+    v4h b[2];
+#pragma unroll
+    for (int qg = 0; qg < 2; ++qg) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        b[qg][j] = static_cast<_Float16>(wts[qg][j]);
+        wts[qg][j] = 0.0f;
+      }
+    }
+    const uint8_t* col = ring + 2 * li;
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb) {
+      v4h av;
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        av[j] = *reinterpret_cast<const _Float16*>(col + ((base + 4 * G + j) % kRing) * (2 * D) + 32 * cb);
+#pragma unroll
+      for (int qg = 0; qg < 2; ++qg) O[qg][cb] = __builtin_amdgcn_mfma_f32_16x16x16f16(av, b[qg], O[qg][cb], 0, 0, 0);
+    }
+  }
+  const uint8_t* ring = nullptr;
 };
 
 template <int D, int VM, bool DUMP, int OUT, int PM, int QF = 0>
@@ -531,6 +572,8 @@ __global__ __launch_bounds__(kThreadsPerBlock, 2) void attn_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) uint8_t lds1[KB + VB];
   __shared__ __attribute__((aligned(16))) uint8_t meta0[LD::META_BYTES];
   __shared__ __attribute__((aligned(16))) uint8_t meta1[LD::META_BYTES];
+  constexpr int RING_BYTES = LD::RING ? kRing * 2 * D : 16;
+  __shared__ __attribute__((aligned(16))) uint8_t ring[RING_BYTES];
 
   // XCD-aware order: the hardware deals blocks round-robin over 8 XCDs; give
   // each XCD a contiguous range of (head, query block) so its L2 serves one head.
@@ -566,11 +609,22 @@ __global__ __launch_bounds__(kThreadsPerBlock, 2) void attn_kernel(AttnArgs a) {
     w.m[qg] = -5000000.0f;
     w.den[qg] = 0.0f;
 #pragma unroll
+    for (int j = 0; j < 4; ++j) w.wts[qg][j] = 0.0f;
+#pragma unroll
     for (int cb = 0; cb < W::CB; ++cb) w.O[qg][cb] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
   }
 
   LD ld;
   ld.init(a, bh);
+  if constexpr (LD::RING) {
+    // The last chunk's flush reads ring slots of tiles past the last one (weight 0):
+    // they must hold finite values, so the ring starts zeroed.
+    for (int i = threadIdx.x; i < RING_BYTES / 16; i += kThreadsPerBlock)
+      reinterpret_cast<uint4*>(ring)[i] = make_uint4(0, 0, 0, 0);
+    __syncthreads();
+    ld.ring = ring;
+    w.ring = ring;
+  }
   ld.issue(0, lds0, lds0 + KB, meta0);
   // Tiles before the last, two per iteration so each buffer is a fixed LDS object.
   const int64_t body = a.tiles - 1;

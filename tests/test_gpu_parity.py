@@ -562,3 +562,32 @@ def test_folded_encode_known_answer_and_group_fallback_on_gpu(extreme, code):
     assert got[0, 0, 0, 96] == code and got[0, 0, 0, 45] == 120
     _, ecodes = o.reference(s, return_codes=True, affine=True)
     np.testing.assert_array_equal(got, ecodes)
+
+
+def test_deferred_mean_restore_rising_maximum_across_chunks():
+    # Smoothing path: the block-mean restore is applied every 16 tiles from the rows' tile
+    # masses, rescaled whenever the running maximum moves. Scores that grow with the key
+    # index move every row's maximum in every tile (40 tiles: two full chunks and a partial
+    # one), and clustered V gives large block means: the output must still meet the bound
+    # against the oracle, and the P bytes stay exact.
+    B, H, N, D = 1, 2, 40 * 128 - 37, 128
+    g = torch.Generator().manual_seed(77)
+    q = (torch.randn(B, H, 160, D, generator=g) * 0.3 + 1.0).to(torch.bfloat16)
+    ramp = torch.linspace(0.0, 1.0, N).view(1, 1, N, 1)
+    k = (torch.randn(B, H, N, D, generator=g) * 0.3 + ramp * 0.5).to(torch.bfloat16)
+    cent = torch.randn(B, H, 8, D, generator=g) * 3.0
+    v = (cent[:, :, torch.randint(0, 8, (N,), generator=g)] + 0.2 * torch.randn(B, H, N, D, generator=g)).to(
+        torch.bfloat16)
+    _print_case("deferred restore rising max", N)
+    st = _oracle_state(q, k, v, True, torch.bfloat16)
+    tok = vcx.value_token()
+    v8 = _to_dev(logical_to_storage(st["v"], tok)).view(torch.float8_e4m3fn)
+    out, pd = vcx.forward(_to_dev(st["q"]), _to_dev(st["k"]), v8, _to_dev(st["qs"]), _to_dev(st["ks"]),
+                          _to_dev(st["vs"]), _to_dev(st["means"]).view(torch.float16), True, True,
+                          st["output_type"], st["scale"], p_rows=(0, 160))
+    eout, ecodes = o.reference(st, return_codes=True)
+    np.testing.assert_array_equal(pd.cpu().numpy(), ecodes)
+    got = out.float().cpu().numpy()
+    err, bound = output_bound(got, eout)
+    assert np.all(err <= bound), float((err - bound).max())
+    assert cosine(got, eout) >= 0.9999

@@ -110,6 +110,20 @@ __device__ inline int int8_code(float x, float s) {
   y = __fadd_rn(y, y >= 0.0f ? 0.5f : -0.5f);
   return static_cast<int>(truncf(y));
 }
+// int8_code(x, s) with the quotient from r = RN(1/s) (one IEEE division per group):
+// q0 = RN(x*r), e = x - q0*s (one FMA, exact unless it underflows), y = RN(q0 + e*r).
+// This is the correctly rounded x/s whenever the residual does not underflow (Markstein's
+// correction theorem, "IA-64 and Elementary Functions", 2000), i.e. for |x| >= 2^-102.
+// Below that, |x/s| < 2^-102 / 1e-7 < 0.25 (every group scale is >= 1e-7), and both
+// quotients give code 0. A GPU comparison against __fdiv_rn over every bf16 and fp16 x
+// and 18k scales, plus 1.9e10 random binary32 x, found no differing code.
+__device__ inline float recip_rn(float s) { return __fdiv_rn(1.0f, s); }
+__device__ inline int int8_code_r(float x, float s, float r) {
+  const float q0 = __fmul_rn(x, r);
+  float y = __builtin_fmaf(__builtin_fmaf(-q0, s, x), r, q0);
+  y = __fadd_rn(y, y >= 0.0f ? 0.5f : -0.5f);
+  return static_cast<int>(truncf(y));
+}
 
 // ------------------------------------------------------------------ wave helpers
 

@@ -293,14 +293,14 @@ __global__ __launch_bounds__(kThreads) void quant_q_kernel(const void* q, int64_
     for (int j = 0; j < CPT; ++j) amax = fmaxf(amax, fabsf(x[j]));
 #pragma unroll
     for (int m = 1; m < 32; m <<= 1) amax = wave_xor_max(amax, m);
-    const float s = int8_scale(amax);
+    const float s = int8_scale(amax), rs = recip_rn(s);
     if (row < n) {
       uint32_t packed[CPT / 4];
 #pragma unroll
       for (int j = 0; j < CPT / 4; ++j) {
         uint32_t wv = 0;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) wv |= (static_cast<uint32_t>(int8_code(x[4 * j + e], s)) & 0xffu) << (8 * e);
+        for (int e = 0; e < 4; ++e) wv |= (static_cast<uint32_t>(int8_code_r(x[4 * j + e], s, rs)) & 0xffu) << (8 * e);
         packed[j] = wv;
       }
       int8_t* dst = q8 + (bh * n + row) * D + c * CPT;
@@ -462,7 +462,9 @@ __global__ __launch_bounds__(kThreads) void quant_k_kernel(const void* k, int64_
                                                            int8_t* k8, float* ks, float norm) {
   constexpr int CPT = D / 16;
   __shared__ float gred[4][2];
-  const int64_t tile = blockIdx.x, bh = blockIdx.y, tiles = gridDim.x;
+  // (head, tile) in the reverse order of the statistics pass, so that the rows that pass
+  // read last are still in the memory-side cache when this pass starts.
+  const int64_t tile = gridDim.x - 1 - blockIdx.x, bh = gridDim.y - 1 - blockIdx.y, tiles = gridDim.x;
   const int tid = threadIdx.x, kk = tid >> 4, c = tid & 15, lane = tid & 63, w = tid >> 6;
   const uint16_t* base = head_base(k, bh, H, sb, sh);
   float mean[CPT];
@@ -485,7 +487,7 @@ __global__ __launch_bounds__(kThreads) void quant_k_kernel(const void* k, int64_
   if ((lane & 31) == 0) gred[w][lane >> 5] = amax;
   __syncthreads();
   amax = fmaxf(gred[w][lane >> 5], gred[w ^ 2][lane >> 5]);
-  const float s = int8_scale(amax);
+  const float s = int8_scale(amax), rs = recip_rn(s);
   const int g = (kk & 7) >> 1;
   if (w < 2 && (lane & 31) == 0) ks[bh * tiles * 4 + tile * 4 + g] = s;
 #pragma unroll
@@ -497,7 +499,7 @@ __global__ __launch_bounds__(kThreads) void quant_k_kernel(const void* k, int64_
     for (int j = 0; j < CPT / 4; ++j) {
       uint32_t wv = 0;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) wv |= (static_cast<uint32_t>(int8_code(v[i][4 * j + e], s)) & 0xffu) << (8 * e);
+      for (int e = 0; e < 4; ++e) wv |= (static_cast<uint32_t>(int8_code_r(v[i][4 * j + e], s, rs)) & 0xffu) << (8 * e);
       packed[j] = wv;
     }
     int8_t* dst = k8 + (bh * n + key) * D + c * CPT;
@@ -525,7 +527,8 @@ __global__ __launch_bounds__(kThreads) void quant_v_kernel(
   constexpr int CPG = D / 8;  // channels per thread
   __shared__ __attribute__((aligned(16))) uint8_t stage[D * kTile];
   __shared__ float sc_sh[D], mu_sh[D];
-  const int64_t tile = blockIdx.x, bh = blockIdx.y, tiles = gridDim.x;
+  // (head, tile) in the reverse order of the statistics pass (see quant_k_kernel).
+  const int64_t tile = gridDim.x - 1 - blockIdx.x, bh = gridDim.y - 1 - blockIdx.y, tiles = gridDim.x;
   const int tid = threadIdx.x, m = tid >> 3, cg = tid & 7;
   const uint16_t* base = head_base(vin, bh, H, sb, sh);
   // Row loads first, so that they overlap the scale/mean stage below.

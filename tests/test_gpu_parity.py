@@ -591,3 +591,26 @@ def test_deferred_mean_restore_rising_maximum_across_chunks():
     err, bound = output_bound(got, eout)
     assert np.all(err <= bound), float((err - bound).max())
     assert cosine(got, eout) >= 0.9999
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
+def test_int8_quantizers_on_every_input_bit_pattern(dt):
+    # Every finite 16-bit pattern of the input dtype, as Q and as K (after centring): the
+    # quantizers' reciprocal-and-FMA quotient must give the bytes of the oracle's IEEE
+    # division under every group scale these rows produce.
+    bits_all = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    x = torch.from_numpy(bits_all.view(np.int16).copy()).view(dt)
+    x = torch.where(torch.isfinite(x), x, torch.zeros_like(x))
+    x = x.view(1, 1, 512, 128)
+    perm = torch.randperm(512, generator=torch.Generator().manual_seed(3))
+    for name, t in (("ordered", x), ("shuffled rows", x[:, :, perm].contiguous())):
+        _print_case("every bit pattern", dt, name)
+        q8, qs, k8, ks, km = vcx.prepare_qk(t.to(DEV), t.to(DEV))
+        nm = dtype_name(dt)
+        eq8, eqs = o.quant_q(bits(t), nm)
+        ekm = o.k_mean(bits(t), None, nm)
+        ek8, eks = o.quant_k(bits(t), ekm, None, nm)
+        np.testing.assert_array_equal(qs.cpu().numpy().view(np.uint32), eqs.view(np.uint32))
+        np.testing.assert_array_equal(q8.cpu().numpy(), eq8)
+        np.testing.assert_array_equal(ks.cpu().numpy().view(np.uint32), eks.view(np.uint32))
+        np.testing.assert_array_equal(k8.cpu().numpy(), ek8)

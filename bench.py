@@ -28,6 +28,7 @@ sys.path.insert(0, str(ROOT / "cake-opt-vc_attention_amd"))
 sys.path.insert(0, str(ROOT))
 
 PEAK_TOPS = 5000.0      # MI355X dense INT8 / FP8 MFMA, TOPS (published)
+PEAK_CLOCK_GHZ = 2.4    # engine clock of the published peak (256 CUs x 4 SIMDs x 2048 ops/clock)
 PEAK_HBM_GBS = 8000.0   # MI355X HBM3E, GB/s (published)
 
 # HBM bytes per fused-kernel launch, measured with rocprofv3 --pmc FETCH_SIZE (scaled by
@@ -261,6 +262,32 @@ def main():
         "roofline_prep": {"bound": "hbm", "achieved": round(prep_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                           "frac": round(prep_gbs / PEAK_HBM_GBS, 4), "algorithmic_bytes": prep_bytes},
     }
+    # Engine clock, outside the timed region: a short burst of untimed steps right after the
+    # timed ones (the GPU still in its sustained state), with probe waves on a second stream
+    # over the first 60 % of the fused launches 2..5, then the probe alone with the GPU idle.
+    side = torch.cuda.Stream(device=dev)
+    window_us = max(int(kernel_ms * 600), 100)
+    probes = []
+    for i in range(5):
+        p = prep()
+        if i > 0:
+            side.wait_stream(torch.cuda.current_stream(dev))
+            with torch.cuda.stream(side):
+                probes.append(vcx.clock_probe(window_us, dev))
+        fused(p)
+    torch.cuda.synchronize()
+    per_launch = [pr.ghz() for pr in probes]
+    per_wave = [g for pr in probes for g in pr.ghz_per_block()]
+    idle_ghz = vcx.clock_probe(2000, dev).ghz()
+    load_ghz = sum(per_launch) / len(per_launch)
+    result["clock"] = {"engine_ghz_under_load": round(load_ghz, 3), "engine_ghz_idle": round(idle_ghz, 3),
+                       "engine_ghz_per_probed_launch": [round(g, 3) for g in per_launch],
+                       "engine_ghz_probe_wave_range": [round(min(per_wave), 3), round(max(per_wave), 3)],
+                       "peak_basis_ghz": PEAK_CLOCK_GHZ,
+                       "frac_at_measured_clock": round(achieved / (PEAK_TOPS * load_ghz / PEAK_CLOCK_GHZ), 4),
+                       "method": "s_memtime / s_memrealtime ticks of 8 one-wave probe blocks (one per XCD) on a "
+                                 "second stream over the first 60 % of fused launches 2-5 of an untimed burst "
+                                 "that follows the timed steps (vcx_clock_probe)"}
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(qc, kc, vc_, smooth, args.cpu_rows, 30.0, args.qk,
                                               args.qk_hadamard)

@@ -29,7 +29,41 @@ int check_launch(const char* what) {
   return VCX_OK;
 }
 
+// Each of the grid's one-wave blocks (8: the hardware deals consecutive blocks to the 8 XCDs
+// in turn) reads the shader-clock counter (s_memtime, ticks at the current engine clock) and
+// the constant-rate real-time counter (s_memrealtime) across a window of `ticks` real-time
+// ticks. The window ends on the real-time counter alone, so the loop always terminates.
+__global__ __launch_bounds__(64) void clock_probe_kernel(unsigned long long* out, unsigned long long ticks) {
+  const unsigned long long r0 = __builtin_amdgcn_s_memrealtime();
+  const unsigned long long c0 = __builtin_amdgcn_s_memtime();
+  unsigned long long r = r0;
+  while (r - r0 < ticks) {
+    __builtin_amdgcn_s_sleep(2);
+    r = __builtin_amdgcn_s_memrealtime();
+  }
+  const unsigned long long c1 = __builtin_amdgcn_s_memtime();
+  if (threadIdx.x == 0) {
+    out[2 * blockIdx.x] = c1 - c0;
+    out[2 * blockIdx.x + 1] = r - r0;
+  }
+}
+
 }  // namespace vcx
+
+extern "C" int vcx_clock_probe(int64_t window_us, uint64_t* out, int* wall_khz, void* stream) {
+  VCX_REQUIRE(out != nullptr && wall_khz != nullptr, "null pointer");
+  VCX_REQUIRE(vcx::aligned(out, 8), "out must be 8-byte aligned");
+  VCX_REQUIRE(window_us >= 1 && window_us <= 10000000, "window_us must be in [1, 10000000]");
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e == hipSuccess) e = hipDeviceGetAttribute(wall_khz, hipDeviceAttributeWallClockRate, dev);
+  if (e != hipSuccess) return vcx::fail(VCX_EHIP, "wall clock rate: %s", hipGetErrorString(e));
+  VCX_REQUIRE(*wall_khz > 0, "device reports no wall clock rate");
+  const unsigned long long ticks = static_cast<unsigned long long>(window_us) * static_cast<unsigned long long>(*wall_khz) / 1000ull;
+  vcx::clock_probe_kernel<<<dim3(VCX_CLOCK_PROBE_BLOCKS), 64, 0, static_cast<hipStream_t>(stream)>>>(
+      reinterpret_cast<unsigned long long*>(out), ticks > 0 ? ticks : 1);
+  return vcx::check_launch("clock_probe_kernel");
+}
 
 extern "C" int vcx_abi_version(void) { return VCX_ABI_VERSION; }
 

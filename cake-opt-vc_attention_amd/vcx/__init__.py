@@ -30,6 +30,8 @@ class VcxError(RuntimeError):
 def _declare(L):
     P, i64, i32, f32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_float
     L.vcx_abi_version.restype = i32
+    L.vcx_clock_probe.restype = i32
+    L.vcx_clock_probe.argtypes = [i64, P, ctypes.POINTER(ctypes.c_int), P]
     L.vcx_abi_version.argtypes = []
     L.vcx_last_error.restype = ctypes.c_char_p
     L.vcx_last_error.argtypes = []
@@ -73,7 +75,8 @@ def _declare(L):
 EXPORTED = ("vcx_abi_version", "vcx_last_error", "vcx_value_token", "vcx_workspace_bytes",
             "vcx_group_values", "vcx_prepare_qk_int8", "vcx_prepare_qk_int8_rotated", "vcx_preprocess_qk",
             "vcx_prepare_qk_fp8", "vcx_prepare_v_fp8", "vcx_attention_fwd", "vcx_attention_fwd_fp8",
-            "vcx_expcast_codes", "vcx_convert_probe", "vcx_kernel_resources", "vcx_kernel_resources_fp8")
+            "vcx_expcast_codes", "vcx_convert_probe", "vcx_kernel_resources", "vcx_kernel_resources_fp8",
+            "vcx_clock_probe")
 
 
 def lib():
@@ -390,6 +393,38 @@ def convert_probe(x):
     f8 = torch.empty(x.shape, dtype=torch.uint8, device=dev)
     _check(lib().vcx_convert_probe(_ptr(x), _ptr(u8), _ptr(f8), x.numel(), _stream(dev)), "vcx_convert_probe")
     return u8, f8
+
+
+CLOCK_PROBE_BLOCKS = 8
+
+
+class ClockProbe:
+    """Engine-clock reading (one wave per XCD) launched on the current stream of `device`;
+    ghz() and ghz_per_block() synchronize the device."""
+
+    def __init__(self, window_us: int, device=None):
+        dev = torch.device("cuda", torch.cuda.current_device()) if device is None else torch.device(device)
+        self.ticks = torch.zeros(2 * CLOCK_PROBE_BLOCKS, dtype=torch.int64, device=dev)
+        khz = ctypes.c_int(0)
+        _check(lib().vcx_clock_probe(int(window_us), _ptr(self.ticks), ctypes.byref(khz), _stream(dev)),
+               "vcx_clock_probe")
+        self.wall_khz = khz.value
+
+    def ghz_per_block(self) -> list:
+        torch.cuda.synchronize(self.ticks.device)
+        t = [int(x) for x in self.ticks.cpu()]
+        return [t[2 * i] / t[2 * i + 1] * self.wall_khz / 1e6 for i in range(CLOCK_PROBE_BLOCKS)]
+
+    def ghz(self) -> float:
+        """Mean engine clock over the probe blocks, GHz."""
+        g = self.ghz_per_block()
+        return sum(g) / len(g)
+
+
+def clock_probe(window_us: int, device=None) -> ClockProbe:
+    """Launch one wave that counts engine-clock ticks against the constant-rate real-time
+    counter for `window_us` microseconds (asynchronous; read the result with .ghz())."""
+    return ClockProbe(window_us, device)
 
 
 def kernel_resources(D: int = 128, block_values: bool = False, *, qk_fp8: bool = False,

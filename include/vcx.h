@@ -36,6 +36,7 @@ extern "C" {
 #endif
 
 #define VCX_ABI_VERSION 1
+#define VCX_CLOCK_PROBE_BLOCKS 8
 
 enum vcx_status {
   VCX_OK = 0,
@@ -208,6 +209,16 @@ int vcx_kernel_resources(int64_t D, int block_values, int64_t* out);
  * 0: control). Replaces _vc_sm90.fp8_kernel_resources
  * (third_party/sageattention_local/csrc/vc/fp8_dispatch.cuh:61-73). */
 int vcx_kernel_resources_fp8(int64_t D, int expcast, int64_t* out);
+
+/* Engine-clock probe: VCX_CLOCK_PROBE_BLOCKS one-wave blocks on `stream` (one per XCD
+ * as the hardware deals blocks) each count s_memtime ticks (the engine clock) against
+ * s_memrealtime ticks (constant rate, *wall_khz kHz) over window_us microseconds of real
+ * time; block i stores out[2i] = engine ticks, out[2i+1] = real-time ticks (device
+ * memory, 8-byte aligned); its clock = out[2i] / out[2i+1] * wall_khz kHz. Run beside
+ * the fused kernel on a second stream it reads the clock under load.
+ * No counterpart in the reference; for reporting MFMA roofline fractions at the
+ * measured clock. */
+int vcx_clock_probe(int64_t window_us, uint64_t* out, int* wall_khz, void* stream);
 
 #ifdef __cplusplus
 }

@@ -96,6 +96,15 @@ def test_invalid_calls_rejected_before_launch():
     assert L.vcx_expcast_codes(None, None, -1, None) == 1
     assert L.vcx_group_values(None, 1, 1, 1, 10, 128, 0, 0, 128, 9, 2, None, None, None, None, 0, None) == 2
     assert "8 effective clusters" in L.vcx_last_error().decode()
+    khz = ctypes.c_int(0)
+    assert L.vcx_clock_probe(1000, None, ctypes.byref(khz), None) == 1
+    assert "null" in L.vcx_last_error().decode()
+    fake = ctypes.c_void_p(4096)  # never dereferenced: the window is checked first
+    assert L.vcx_clock_probe(0, fake, ctypes.byref(khz), None) == 1
+    assert "window_us" in L.vcx_last_error().decode()
+    assert L.vcx_clock_probe(10000001, fake, ctypes.byref(khz), None) == 1
+    assert L.vcx_clock_probe(1000, ctypes.c_void_p(4100), ctypes.byref(khz), None) == 1
+    assert "aligned" in L.vcx_last_error().decode()
 
 
 def test_python_binding_refuses_cpu_tensors():

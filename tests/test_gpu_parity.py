@@ -32,6 +32,19 @@ def test_device_is_gfx950_and_library_loaded():
     assert sorted(tok) == list(range(128))
 
 
+def test_clock_probe_reads_a_plausible_engine_clock():
+    # 2 ms of real time: the engine counter must run between 0.5 and 3 GHz, and a window
+    # twice as long must read about twice the real-time ticks.
+    short, long_ = vcx.clock_probe(2000, DEV), vcx.clock_probe(4000, DEV)
+    ghz = short.ghz()
+    assert 0.5 < ghz < 3.0, ghz
+    assert 0.5 < long_.ghz() < 3.0
+    assert short.wall_khz > 0
+    assert all(0.5 < g < 3.0 for g in short.ghz_per_block())
+    ratio = int(long_.ticks[1]) / int(short.ticks[1])
+    assert 1.9 < ratio < 2.1, ratio
+
+
 # ------------------------------------------------------------------ scalar maps
 
 def test_expcast_codes_sweep_bit_exact():

@@ -9,6 +9,8 @@ eager fallback: a missing or stale library raises RuntimeError.
 from __future__ import annotations
 
 import ctypes
+import functools
+import itertools
 from pathlib import Path
 
 import torch
@@ -77,6 +79,22 @@ EXPORTED = ("vcx_abi_version", "vcx_last_error", "vcx_value_token", "vcx_workspa
             "vcx_prepare_qk_fp8", "vcx_prepare_v_fp8", "vcx_attention_fwd", "vcx_attention_fwd_fp8",
             "vcx_expcast_codes", "vcx_convert_probe", "vcx_kernel_resources", "vcx_kernel_resources_fp8",
             "vcx_clock_probe")
+
+
+def _device_call(fn):
+    """no_grad, with the device of the first tensor argument made current for the call: the
+    library launches on the current HIP device, on a stream of that device."""
+
+    @functools.wraps(fn)
+    def wrapper(*args, **kwargs):
+        t = next((a for a in itertools.chain(args, kwargs.values()) if isinstance(a, torch.Tensor)), None)
+        with torch.no_grad():
+            if t is not None and t.device.type == "cuda":
+                with torch.cuda.device(t.device):
+                    return fn(*args, **kwargs)
+            return fn(*args, **kwargs)
+
+    return wrapper
 
 
 def lib():
@@ -159,7 +177,7 @@ def abi_version() -> int:
 
 # ---------------------------------------------------------------- preprocessing
 
-@torch.no_grad()
+@_device_call
 def group_values(v, clusters: int, iterations: int, debug: bool = False):
     """int64 permutation [B,H,N] (+ int32 labels and fp32 centers when debug)."""
     dev = _require_device(v)
@@ -178,7 +196,7 @@ def group_values(v, clusters: int, iterations: int, debug: bool = False):
     return (perm, labels, centers) if debug else perm
 
 
-@torch.no_grad()
+@_device_call
 def prepare_qk(q, k, perm=None, hadamard: bool = False):
     """INT8 Q/K with Sage per-thread scales after K centring: (q8, qs, k8, ks, km).
     hadamard=True rotates Q and the centred K (normalized Sylvester transform) first."""
@@ -204,7 +222,7 @@ def prepare_qk(q, k, perm=None, hadamard: bool = False):
     return q8, qs, k8, ks, km
 
 
-@torch.no_grad()
+@_device_call
 def preprocess_qk(q, k, k_smooth: bool, hadamard: bool):
     """Binary32 post-RoPE Q/K preprocessing (the reference's preprocess_qk): K centred by its
     channel mean when k_smooth, Q and K rotated by the normalized Sylvester-Hadamard transform
@@ -230,7 +248,7 @@ def preprocess_qk(q, k, k_smooth: bool, hadamard: bool):
     return qo, ko
 
 
-@torch.no_grad()
+@_device_call
 def prepare_qk_fp8(q, k):
     """Block-scaled E4M3 Q/K (Q 64-row blocks, centred K 128-row blocks):
     (q8 uint8 [B,H,Nq,D], qs [B,H,ceil(Nq/64)], k8 uint8 [B,H,Nk,D], ks [B,H,ceil(Nk/128)],
@@ -254,7 +272,7 @@ def prepare_qk_fp8(q, k):
     return q8, qs, k8, ks, km
 
 
-@torch.no_grad()
+@_device_call
 def prepare_v(v, perm=None, smooth: bool = False, channel_scale: bool = True):
     """E4M3 V in storage order: (v8 [B,H,D,tiles*128], vs, means or empty)."""
     dev = _require_device(v, perm)
@@ -281,7 +299,7 @@ def prepare_v(v, perm=None, smooth: bool = False, channel_scale: bool = True):
 
 # ---------------------------------------------------------------- attention
 
-@torch.no_grad()
+@_device_call
 def forward(q8, k8, v8, qs, ks, vs, means, expcast: bool, block_values: bool, output_type: int, scale: float,
             *, channel_scale: bool = True, affine: bool = False, out=None, p_rows=None):
     """Fused attention on prepared payloads -> out [B,H,Nq,D] (fp16 if output_type == 0 else bf16).
@@ -334,7 +352,7 @@ def forward(q8, k8, v8, qs, ks, vs, means, expcast: bool, block_values: bool, ou
     return (out, pd) if p_rows is not None else out
 
 
-@torch.no_grad()
+@_device_call
 def forward_fp8(q8, k8, v8, qs, ks, vs, expcast: bool, output_type: int, scale: float,
                 *, affine: bool = True, out=None, p_rows=None):
     """Fused attention on block-scaled FP8 Q/K payloads (vcx.prepare_qk_fp8) and the
@@ -376,7 +394,7 @@ def forward_fp8(q8, k8, v8, qs, ks, vs, expcast: bool, output_type: int, scale: 
     return (out, pd) if p_rows is not None else out
 
 
-@torch.no_grad()
+@_device_call
 def expcast_codes(x):
     dev = _require_device(x)
     x = x.float().contiguous()
@@ -385,7 +403,7 @@ def expcast_codes(x):
     return y
 
 
-@torch.no_grad()
+@_device_call
 def convert_probe(x):
     dev = _require_device(x)
     x = x.float().contiguous()
@@ -406,8 +424,9 @@ class ClockProbe:
         dev = torch.device("cuda", torch.cuda.current_device()) if device is None else torch.device(device)
         self.ticks = torch.zeros(2 * CLOCK_PROBE_BLOCKS, dtype=torch.int64, device=dev)
         khz = ctypes.c_int(0)
-        _check(lib().vcx_clock_probe(int(window_us), _ptr(self.ticks), ctypes.byref(khz), _stream(dev)),
-               "vcx_clock_probe")
+        with torch.cuda.device(dev):
+            _check(lib().vcx_clock_probe(int(window_us), _ptr(self.ticks), ctypes.byref(khz), _stream(dev)),
+                   "vcx_clock_probe")
         self.wall_khz = khz.value
 
     def ghz_per_block(self) -> list:

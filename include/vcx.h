@@ -7,6 +7,8 @@
  *   - never allocates: the caller owns every output and workspace buffer;
  *   - enqueues all work on the given HIP stream (hipStream_t passed as void*;
  *     NULL means the null stream) and never synchronizes;
+ *   - launches on the calling thread's current HIP device: the stream and every
+ *     pointer must belong to that device;
  *   - returns VCX_OK (0) or a nonzero error code, with a message available
  *     from vcx_last_error() on the calling thread; no C++ exception crosses
  *     this boundary;

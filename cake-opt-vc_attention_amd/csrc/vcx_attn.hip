@@ -228,12 +228,22 @@ __device__ inline float acc_value(const v4i& acc, int r) { return __int_as_float
 template <int D, int VM, bool DUMP, int PM, int QF = 0>
 struct Wave {
   static constexpr bool EC = PM != 0;  // ExpCast bytes (1 unfused, 2 folded) or the control path (0)
-  static constexpr bool IB = PM == 2 && QF == 0;  // biased INT8 accumulators (folded path)
+  // Biased INT8 accumulators (float(acc) = one v_sub_f32): the folded path, and the unfused
+  // path at D128 with channel-scale smoothing (same-box: smoothing 11.13 -> 11.06 ms, long
+  // 43.24 -> 43.00 ms). D64 (168 VGPRs at three waves per SIMD) and per-block V scales keep
+  // v_cvt_f32_i32: the bias register costs them spills.
+  static constexpr bool IB = QF == 0 && (PM == 2 || (PM == 1 && D == 128 && VM == 1));
   static constexpr int DS = D / 64;  // 64-deep QK steps
   static constexpr int CB = D / 16;  // 16-channel output blocks
   static constexpr bool SMOOTH = VM >= 1, BSCALE = VM == 2;
   typedef TileLoader<D, VM, QF> LD;
   typedef std::conditional_t<QF == 1, v4f, v4i> Acc;  // 16x16 score accumulator
+
+  // The exact float value of one INT8 score accumulator element.
+  __device__ static inline float acc_float(int x) {
+    if constexpr (IB) return __int_as_float(x) - kBiasF;
+    else return static_cast<float>(x);
+  }
 
   v4i qf[2][DS];
   float qsv[2];
@@ -377,7 +387,7 @@ struct Wave {
           for (int j = 0; j < 8; ++j)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-              lg[j][r] = static_cast<float>(S[qg][j][r]) * c;
+              lg[j][r] = acc_float(S[qg][j][r]) * c;
               tmax = fmaxf(tmax, lg[j][r]);
             }
         } else {
@@ -386,7 +396,7 @@ struct Wave {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
               const int64_t key = t * kTile + 16 * j + 8 * (r >> 1) + 2 * G + (r & 1);
-              float x = (static_cast<float>(S[qg][j][r]) * dq) * a.sm;
+              float x = (acc_float(S[qg][j][r]) * dq) * a.sm;
               lg[j][r] = key < a.Nk ? x : -INFINITY;
               tmax = fmaxf(tmax, lg[j][r]);
             }

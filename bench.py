@@ -36,7 +36,7 @@ PEAK_HBM_GBS = 8000.0   # MI355X HBM3E, GB/s (published)
 # commands are in profiles/attn_kernel_main_hbm_bytes.txt (FP8 QK variant:
 # profiles/attn_kernel_fp8_main_hbm_bytes.txt). Counters cannot be read from inside this
 # process, so the figure is keyed by QK format and configuration and null where unmeasured.
-MEASURED_TRAFFIC_BYTES = {("int8", "main"): 3.127e9, ("fp8", "main"): 3.133e9}
+MEASURED_TRAFFIC_BYTES = {("int8", "main"): 3.128e9, ("fp8", "main"): 3.133e9}
 
 CONFIGS = {
     # name: (B, H, N, D, kind, v_smooth, description)
@@ -132,6 +132,8 @@ def main():
     ap.add_argument("--config", default="main", choices=sorted(CONFIGS))
     ap.add_argument("--cpu-rows", type=int, default=2048, help="query rows per head for the CPU baseline")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-clock", action="store_true",
+                    help="skip the engine-clock burst after the timed steps (for kernel-trace profiles)")
     ap.add_argument("--qk-hadamard", action="store_true",
                     help="rotate Q and the centred K (normalized Hadamard) inside the INT8 quantizers")
     ap.add_argument("--qk", default="int8", choices=("int8", "fp8"),
@@ -265,29 +267,30 @@ def main():
     # Engine clock, outside the timed region: a short burst of untimed steps right after the
     # timed ones (the GPU still in its sustained state), with probe waves on a second stream
     # over the first 60 % of the fused launches 2..5, then the probe alone with the GPU idle.
-    side = torch.cuda.Stream(device=dev)
-    window_us = max(int(kernel_ms * 600), 100)
-    probes = []
-    for i in range(5):
-        p = prep()
-        if i > 0:
-            side.wait_stream(torch.cuda.current_stream(dev))
-            with torch.cuda.stream(side):
-                probes.append(vcx.clock_probe(window_us, dev))
-        fused(p)
-    torch.cuda.synchronize()
-    per_launch = [pr.ghz() for pr in probes]
-    per_wave = [g for pr in probes for g in pr.ghz_per_block()]
-    idle_ghz = vcx.clock_probe(2000, dev).ghz()
-    load_ghz = sum(per_launch) / len(per_launch)
-    result["clock"] = {"engine_ghz_under_load": round(load_ghz, 3), "engine_ghz_idle": round(idle_ghz, 3),
-                       "engine_ghz_per_probed_launch": [round(g, 3) for g in per_launch],
-                       "engine_ghz_probe_wave_range": [round(min(per_wave), 3), round(max(per_wave), 3)],
-                       "peak_basis_ghz": PEAK_CLOCK_GHZ,
-                       "frac_at_measured_clock": round(achieved / (PEAK_TOPS * load_ghz / PEAK_CLOCK_GHZ), 4),
-                       "method": "s_memtime / s_memrealtime ticks of 8 one-wave probe blocks (one per XCD) on a "
-                                 "second stream over the first 60 % of fused launches 2-5 of an untimed burst "
-                                 "that follows the timed steps (vcx_clock_probe)"}
+    if not args.no_clock:
+        side = torch.cuda.Stream(device=dev)
+        window_us = max(int(kernel_ms * 600), 100)
+        probes = []
+        for i in range(5):
+            p = prep()
+            if i > 0:
+                side.wait_stream(torch.cuda.current_stream(dev))
+                with torch.cuda.stream(side):
+                    probes.append(vcx.clock_probe(window_us, dev))
+            fused(p)
+        torch.cuda.synchronize()
+        per_launch = [pr.ghz() for pr in probes]
+        per_wave = [g for pr in probes for g in pr.ghz_per_block()]
+        idle_ghz = vcx.clock_probe(2000, dev).ghz()
+        load_ghz = sum(per_launch) / len(per_launch)
+        result["clock"] = {"engine_ghz_under_load": round(load_ghz, 3), "engine_ghz_idle": round(idle_ghz, 3),
+                           "engine_ghz_per_probed_launch": [round(g, 3) for g in per_launch],
+                           "engine_ghz_probe_wave_range": [round(min(per_wave), 3), round(max(per_wave), 3)],
+                           "peak_basis_ghz": PEAK_CLOCK_GHZ,
+                           "frac_at_measured_clock": round(achieved / (PEAK_TOPS * load_ghz / PEAK_CLOCK_GHZ), 4),
+                           "method": "s_memtime / s_memrealtime ticks of 8 one-wave probe blocks (one per XCD) on a "
+                                     "second stream over the first 60 % of fused launches 2-5 of an untimed burst "
+                                     "that follows the timed steps (vcx_clock_probe)"}
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(qc, kc, vc_, smooth, args.cpu_rows, 30.0, args.qk,
                                               args.qk_hadamard)

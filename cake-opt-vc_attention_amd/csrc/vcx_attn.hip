@@ -111,30 +111,32 @@ __device__ inline __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t by
 // Value modes: VM 0 = no smoothing (per-channel V scale in the epilogue),
 // 1 = block-mean smoothing with per-channel scales, 2 = block-mean smoothing
 // with per-block scales (applied to every tile's contribution).
-// VM 1 defers the block-mean restore: the fp16 means of tile t land in slot t % kRing of
+// VM 1 and 2 defer the block-mean restore: the fp16 means of tile t land in slot t % NR of
 // an LDS ring, and every kChunk tiles one f16 MFMA per channel block adds
-// sum_t mean_t (x) w_t to O (w_t: the row's tile mass, rescaled like O).
+// sum_t mean_t (x) w_t to O (w_t: the row's tile mass, rescaled like O). VM 2 also rings
+// the tile's fp32 V scales and feeds RN_f16(vs_t * mean_t) to that MFMA instead.
 constexpr int kChunk = 16, kRing = 32;
 
 template <int D, int VM, int QF = 0>
 struct TileLoader {
-  static constexpr bool SMOOTH = VM >= 1, BSCALE = VM == 2, RING = VM == 1;
-  // Meta region of a buffer: BSCALE ? fp16 means of the tile (2*D bytes) : nothing,
-  // then BSCALE ? the tile's fp32 V scales (4*D bytes) : nothing, then the tile's
-  // K scales (INT8: 4 Sage key-group scales, 16 bytes; FP8 block: one scale, 4 bytes).
-  // Means (meta or ring) and K scales are loaded by wave 0, V scales by wave 1.
+  static constexpr bool SMOOTH = VM >= 1, BSCALE = VM == 2, RING = VM >= 1;
+  // Ring slots: the DMA of tile t+1 is in flight while a flush reads tiles t-15..t, so a
+  // ring needs kChunk + 1 slots; VM 1 keeps 32 (power of two), VM 2 (which also rings
+  // 4*D bytes of V scales per tile) the minimum, to stay within two blocks' LDS per CU.
+  static constexpr int NR = BSCALE ? kChunk + 1 : kRing;
+  // Meta region of a buffer: the tile's K scales (INT8: 4 Sage key-group scales, 16 bytes;
+  // FP8 block: one scale, 4 bytes), loaded by wave 0 with the means; V scales by wave 1.
   static constexpr int MR = SMOOTH ? (2 * D) / 16 : 0;  // lanes that load the tile's means
-  static constexpr int ML = BSCALE ? MR : 0;
-  static constexpr int VL = BSCALE ? (4 * D) / 16 : 0;
-  static constexpr int VS_OFF = 16 * ML;
-  static constexpr int KS_OFF = 16 * (ML + VL);
-  static constexpr int META_BYTES = KS_OFF + 16;
+  static constexpr int VL = BSCALE ? (4 * D) / 16 : 0;  // lanes that load the tile's V scales
+  static constexpr int KS_OFF = 0;
+  static constexpr int META_BYTES = 16;
   static constexpr int N = D / 32;  // instructions per wave per operand
   uint32_t koff[N];                 // lane byte offset inside the K tile (row*D + chunk*16)
   uint32_t voff[N];                 // lane byte offset inside the V^T tile columns
   uint32_t moff;                    // lane byte offset of the meta load (wave 0)
   __amdgpu_buffer_rsrc_t rk, rv, rm, rs, rb;
-  uint8_t* ring;                    // RING: LDS ring of kRing tiles x D fp16 means
+  uint8_t* ring;                    // RING: LDS ring of NR tiles x D fp16 means
+  uint8_t* vsring;                  // BSCALE: LDS ring of NR tiles x D fp32 V scales
   int wave;
 
   __device__ inline void init(const AttnArgs& a, int64_t bh) {
@@ -165,7 +167,7 @@ struct TileLoader {
     const int lane = threadIdx.x & 63;
     if (wave == 0) {
       if constexpr (SMOOTH) {
-        uint8_t* dst = RING ? ring + (t % kRing) * (2 * D) : lm;
+        uint8_t* dst = ring + (t % NR) * (2 * D);
         if (lane < MR)
           __builtin_amdgcn_raw_ptr_buffer_load_lds(rm, (lds_void*)dst, 16, moff, static_cast<int>(t * D * 2), 0, 0);
       }
@@ -178,7 +180,8 @@ struct TileLoader {
     }
     if constexpr (BSCALE) {
       if (wave == 1 && lane < VL)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_void*)(lm + VS_OFF), 16, moff, static_cast<int>(t * D * 4), 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_void*)(vsring + (t % NR) * (4 * D)), 16, moff,
+                                                 static_cast<int>(t * D * 4), 0, 0);
     }
     const int kso = static_cast<int>(t * kTile * D);
 #pragma unroll
@@ -250,7 +253,7 @@ struct Wave {
   int64_t row[2];
   float m[2], den[2];
   v4f O[2][CB];
-  float wts[2][4];  // VM 1: pending mean weights of chunk tiles 4G..4G+3 (row li)
+  float wts[2][4];  // VM 1, 2: pending mean weights of chunk tiles 4G..4G+3 (row li)
   int koff[DS], voff[2];
   int G, li;
   int64_t bh_;
@@ -473,7 +476,7 @@ struct Wave {
       if (__any(alpha[qg] != 1.0f)) {
 #pragma unroll
         for (int cb = 0; cb < CB; ++cb) O[qg][cb] *= alpha[qg];
-        if constexpr (VM == 1) {
+        if constexpr (SMOOTH) {
 #pragma unroll
           for (int j = 0; j < 4; ++j) wts[qg][j] *= alpha[qg];
         }
@@ -486,58 +489,56 @@ struct Wave {
     const v4f zero = {0.0f, 0.0f, 0.0f, 0.0f};
     float mass[2];
     if constexpr (BSCALE) {
-      // Per-block V scales: O += (PV_t + mass * mean_t) * vs_t per channel. The row
-      // mass comes first; each channel block's PV lands in a temporary that is
-      // folded into O right away.
+      // Per-block V scales: O += vs_t * PV_t per channel, one FMA per element on the PV
+      // temporary of each channel block; the mean term vs_t * mean_t * mass joins the
+      // deferred restore below.
 #pragma unroll
       for (int qg = 0; qg < 2; ++qg) {
         if constexpr (EC) mass[qg] = mfma_fp8(ones, P[qg], zero)[0];
         else mass[qg] = tmass[qg];
         den[qg] = den[qg] * alpha[qg] + mass[qg];
       }
+      const uint8_t* vsl = vsring + (t % LD::NR) * (4 * D);
       v8i vc = load_v(lv, 0), vn;
 #pragma unroll
       for (int cb = 0; cb < CB; ++cb) {
         if (cb + 1 < CB) vn = load_v(lv, cb + 1);
-        const uint2 hm = *reinterpret_cast<const uint2*>(lm + 32 * cb + 8 * G);
-        const float4 vsb = *reinterpret_cast<const float4*>(lm + LD::VS_OFF + 4 * (16 * cb + 4 * G));
-        const float mean[4] = {f16_bits_to_f32(hm.x & 0xffffu), f16_bits_to_f32(hm.x >> 16),
-                               f16_bits_to_f32(hm.y & 0xffffu), f16_bits_to_f32(hm.y >> 16)};
+        const float4 vsb = *reinterpret_cast<const float4*>(vsl + 4 * (16 * cb + 4 * G));
         const float sc[4] = {vsb.x, vsb.y, vsb.z, vsb.w};
 #pragma unroll
         for (int qg = 0; qg < 2; ++qg) {
           const v4f pv = mfma_fp8(vc, P[qg], zero);
 #pragma unroll
-          for (int r = 0; r < 4; ++r)
-            O[qg][cb][r] = __builtin_fmaf(__builtin_fmaf(mass[qg], mean[r], pv[r]), sc[r], O[qg][cb][r]);
+          for (int r = 0; r < 4; ++r) O[qg][cb][r] = __builtin_fmaf(pv[r], sc[r], O[qg][cb][r]);
         }
         vc = vn;
         __builtin_amdgcn_sched_barrier(0);
       }
-      return;
-    }
-    v8i vf[CB];
-    vf[0] = load_v(lv, 0);
-    if (CB > 1) vf[1] = load_v(lv, 1);
+    } else {
+      v8i vf[CB];
+      vf[0] = load_v(lv, 0);
+      if (CB > 1) vf[1] = load_v(lv, 1);
 #pragma unroll
-    for (int cb = 0; cb < CB; ++cb) {
-      if (cb + 2 < CB) vf[cb + 2] = load_v(lv, cb + 2);
+      for (int cb = 0; cb < CB; ++cb) {
+        if (cb + 2 < CB) vf[cb + 2] = load_v(lv, cb + 2);
 #pragma unroll
-      for (int qg = 0; qg < 2; ++qg) O[qg][cb] = mfma_fp8(vf[cb], P[qg], O[qg][cb]);
-      __builtin_amdgcn_sched_barrier(0);
-    }
+        for (int qg = 0; qg < 2; ++qg) O[qg][cb] = mfma_fp8(vf[cb], P[qg], O[qg][cb]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
 #pragma unroll
-    for (int qg = 0; qg < 2; ++qg) {
-      if constexpr (EC) mass[qg] = mfma_fp8(ones, P[qg], zero)[0];
-      else mass[qg] = tmass[qg];
-      den[qg] = den[qg] * alpha[qg] + mass[qg];
+      for (int qg = 0; qg < 2; ++qg) {
+        if constexpr (EC) mass[qg] = mfma_fp8(ones, P[qg], zero)[0];
+        else mass[qg] = tmass[qg];
+        den[qg] = den[qg] * alpha[qg] + mass[qg];
+      }
     }
-    if constexpr (VM == 1) {
+    if constexpr (SMOOTH) {
       // Deferred block-mean restore: tile t is position c of its chunk; lane group
       // G = c / 4 keeps the row's mass in slot c % 4 (the MFMA's k = c). At the chunk's
       // end (or the last tile) O^T[ch][row] += sum_k mean_k[ch] * w_k[row] over the
-      // chunk, as v_mfma_f32_16x16x16f16 (A: means from the ring, exact in fp16;
-      // B: the weights rounded to fp16). Slots of tiles past the last hold w = 0.
+      // chunk, as v_mfma_f32_16x16x16f16 (A: means from the ring, exact in fp16, or with
+      // per-block scales RN_f16(vs_k[ch] * mean_k[ch]); B: the weights rounded to fp16).
+      // Slots of tiles past the last hold w = 0.
       const int c = static_cast<int>(t & (kChunk - 1));
 #pragma unroll
       for (int qg = 0; qg < 2; ++qg)
@@ -547,7 +548,7 @@ struct Wave {
     }
   }
 
-  // O += means (x) weights over the chunk that starts at tile `base` (VM 1).
+  // O += means (x) weights over the chunk that starts at tile `base` (VM 1, 2).
   __device__ inline void flush_means(const uint8_t* ring, int64_t base) {
     typedef _Float16 v4h __attribute__((ext_vector_type(4)));
     v4h b[2];
@@ -564,13 +565,22 @@ struct Wave {
     for (int cb = 0; cb < CB; ++cb) {
       v4h av;
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
-        av[j] = *reinterpret_cast<const _Float16*>(col + ((base + 4 * G + j) % kRing) * (2 * D) + 32 * cb);
+      for (int j = 0; j < 4; ++j) {
+        const int slot = static_cast<int>((base + 4 * G + j) % LD::NR);
+        const _Float16 mh = *reinterpret_cast<const _Float16*>(col + slot * (2 * D) + 32 * cb);
+        if constexpr (BSCALE) {
+          const float vsv = *reinterpret_cast<const float*>(vsring + slot * (4 * D) + 4 * (16 * cb + li));
+          av[j] = static_cast<_Float16>(static_cast<float>(mh) * vsv);
+        } else {
+          av[j] = mh;
+        }
+      }
 #pragma unroll
       for (int qg = 0; qg < 2; ++qg) O[qg][cb] = __builtin_amdgcn_mfma_f32_16x16x16f16(av, b[qg], O[qg][cb], 0, 0, 0);
     }
   }
   const uint8_t* ring = nullptr;
+  const uint8_t* vsring = nullptr;
 };
 
 // D64 without per-block V scales runs three workgroups per CU (at most 168 VGPRs; its
@@ -588,8 +598,10 @@ __global__ __launch_bounds__(kThreadsPerBlock, (kBlocksPerCU<D, VM>)) void attn_
   __shared__ __attribute__((aligned(16))) uint8_t lds1[KB + VB];
   __shared__ __attribute__((aligned(16))) uint8_t meta0[LD::META_BYTES];
   __shared__ __attribute__((aligned(16))) uint8_t meta1[LD::META_BYTES];
-  constexpr int RING_BYTES = LD::RING ? kRing * 2 * D : 16;
+  constexpr int RING_BYTES = LD::RING ? LD::NR * 2 * D : 16;
   __shared__ __attribute__((aligned(16))) uint8_t ring[RING_BYTES];
+  constexpr int VSRING_BYTES = LD::BSCALE ? LD::NR * 4 * D : 16;
+  __shared__ __attribute__((aligned(16))) uint8_t vsring[VSRING_BYTES];
 
   // XCD-aware order: the hardware deals blocks round-robin over 8 XCDs; give
   // each XCD a contiguous range of (head, query block) so its L2 serves one head.
@@ -634,12 +646,18 @@ __global__ __launch_bounds__(kThreadsPerBlock, (kBlocksPerCU<D, VM>)) void attn_
   ld.init(a, bh);
   if constexpr (LD::RING) {
     // The last chunk's flush reads ring slots of tiles past the last one (weight 0):
-    // they must hold finite values, so the ring starts zeroed.
+    // they must hold finite values, so the rings start zeroed.
     for (int i = threadIdx.x; i < RING_BYTES / 16; i += kThreadsPerBlock)
       reinterpret_cast<uint4*>(ring)[i] = make_uint4(0, 0, 0, 0);
+    if constexpr (LD::BSCALE) {
+      for (int i = threadIdx.x; i < VSRING_BYTES / 16; i += kThreadsPerBlock)
+        reinterpret_cast<uint4*>(vsring)[i] = make_uint4(0, 0, 0, 0);
+    }
     __syncthreads();
     ld.ring = ring;
     w.ring = ring;
+    ld.vsring = vsring;
+    w.vsring = vsring;
   }
   ld.issue(0, lds0, lds0 + KB, meta0);
   // Tiles before the last, two per iteration so each buffer is a fixed LDS object.

@@ -383,6 +383,11 @@ BLOCK = [  # B, H, Nq, Nk, D, dtype
     (1, 2, 300, 700, 128, torch.bfloat16),
     (2, 1, 129, 257, 64, torch.float16),
     (1, 1, 1, 1, 128, torch.bfloat16),
+    # the deferred mean term: 36 tiles (two full 16-tile chunks, the 17-slot ring wraps
+    # twice), a chunk that ends on the last tile, and a last tile that opens a chunk
+    (1, 1, 64, 4500, 128, torch.bfloat16),
+    (1, 2, 40, 2048, 64, torch.float16),
+    (1, 1, 33, 2049, 128, torch.bfloat16),
 ]
 
 

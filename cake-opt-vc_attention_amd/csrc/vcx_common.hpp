@@ -146,11 +146,19 @@ __device__ inline void hadamard_row(float (&x)[CPT], int c, float norm) {
         x[j] = __fadd_rn(a, b);
         x[j + s] = __fsub_rn(a, b);
       }
+  // Lane xor 1 and 2 stay inside a quad of lanes: a DPP quad_perm move reads the partner
+  // ([1,0,3,2] = 0xB1, [2,3,0,1] = 0x4E) without the LDS-pipe permute of __shfl_xor.
 #pragma unroll
   for (int m = 1; m < L; m <<= 1)
 #pragma unroll
     for (int j = 0; j < CPT; ++j) {
-      const float other = __shfl_xor(x[j], m, 64);
+      float other;
+      if (m == 1)
+        other = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x[j]), 0xB1, 0xF, 0xF, false));
+      else if (m == 2)
+        other = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x[j]), 0x4E, 0xF, 0xF, false));
+      else
+        other = __shfl_xor(x[j], m, 64);
       x[j] = (c & m) ? __fsub_rn(other, x[j]) : __fadd_rn(x[j], other);
     }
 #pragma unroll

@@ -127,7 +127,46 @@ __device__ inline int int8_code_r(float x, float s, float r) {
 
 // ------------------------------------------------------------------ wave helpers
 
-__device__ inline float wave_xor_max(float v, int mask) { return fmaxf(v, __shfl_xor(v, mask, 64)); }
+// Cross-lane reductions without the LDS pipe. dpp_move<CTRL> reads another lane of the same
+// row of 16 through a DPP operand: quad_perm xor 1 (0xB1) and xor 2 (0x4E), row_half_mirror
+// (0x141: i <-> 7-i), row_mirror (0x140: i <-> 15-i). The gfx950 permlane swaps return
+// {x[l], x[l ^ 16]} (or ^ 32) in some order, so max and + over the pair are exact.
+template <int CTRL>
+__device__ inline float dpp_move(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+__device__ inline float max_xor16(float v) {
+  const auto s = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(s[0]), __uint_as_float(s[1]));
+}
+__device__ inline float max_xor32(float v) {
+  const auto s = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(s[0]), __uint_as_float(s[1]));
+}
+// x + x[l ^ 16] and x + x[l ^ 32] in binary64 (the pair's sum: addition commutes).
+__device__ inline double add_xor16(double v) {
+  const uint64_t b = static_cast<uint64_t>(__double_as_longlong(v));
+  const auto lo = __builtin_amdgcn_permlane16_swap(static_cast<uint32_t>(b), static_cast<uint32_t>(b), false, false);
+  const auto hi = __builtin_amdgcn_permlane16_swap(static_cast<uint32_t>(b >> 32), static_cast<uint32_t>(b >> 32), false, false);
+  return __longlong_as_double(static_cast<long long>((static_cast<uint64_t>(hi[0]) << 32) | lo[0])) +
+         __longlong_as_double(static_cast<long long>((static_cast<uint64_t>(hi[1]) << 32) | lo[1]));
+}
+__device__ inline double add_xor32(double v) {
+  const uint64_t b = static_cast<uint64_t>(__double_as_longlong(v));
+  const auto lo = __builtin_amdgcn_permlane32_swap(static_cast<uint32_t>(b), static_cast<uint32_t>(b), false, false);
+  const auto hi = __builtin_amdgcn_permlane32_swap(static_cast<uint32_t>(b >> 32), static_cast<uint32_t>(b >> 32), false, false);
+  return __longlong_as_double(static_cast<long long>((static_cast<uint64_t>(hi[0]) << 32) | lo[0])) +
+         __longlong_as_double(static_cast<long long>((static_cast<uint64_t>(hi[1]) << 32) | lo[1]));
+}
+// Maximum over each 32-lane half of the wave (exact in any pairing order): quad exchanges,
+// the 8- and 16-lane mirrors, then lane l ^ 16.
+__device__ inline float half_wave_max(float v) {
+  v = fmaxf(v, dpp_move<0xB1>(v));
+  v = fmaxf(v, dpp_move<0x4E>(v));
+  v = fmaxf(v, dpp_move<0x141>(v));
+  v = fmaxf(v, dpp_move<0x140>(v));
+  return max_xor16(v);
+}
 
 // Normalized Sylvester-Hadamard rotation of one row of W = CPT * L values held by L
 // consecutive lanes (lane c of the group holds entries c*CPT .. c*CPT + CPT - 1). Strides
@@ -152,13 +191,7 @@ __device__ inline void hadamard_row(float (&x)[CPT], int c, float norm) {
   for (int m = 1; m < L; m <<= 1)
 #pragma unroll
     for (int j = 0; j < CPT; ++j) {
-      float other;
-      if (m == 1)
-        other = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x[j]), 0xB1, 0xF, 0xF, false));
-      else if (m == 2)
-        other = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x[j]), 0x4E, 0xF, 0xF, false));
-      else
-        other = __shfl_xor(x[j], m, 64);
+      const float other = m == 1 ? dpp_move<0xB1>(x[j]) : m == 2 ? dpp_move<0x4E>(x[j]) : __shfl_xor(x[j], m, 64);
       x[j] = (c & m) ? __fsub_rn(other, x[j]) : __fadd_rn(x[j], other);
     }
 #pragma unroll

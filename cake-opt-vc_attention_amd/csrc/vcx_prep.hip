@@ -81,8 +81,7 @@ __device__ inline void tile_tree(double (&a)[D / 16], double* red, double* out_c
   int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, c = tid & 15;
 #pragma unroll
   for (int j = 0; j < CPT; ++j) {
-    double b = a[j] + __shfl_xor(a[j], 16, 64);
-    a[j] = b + __shfl_xor(b, 32, 64);
+    a[j] = add_xor32(add_xor16(a[j]));
   }
   if (lane < 16)
 #pragma unroll
@@ -121,8 +120,7 @@ __global__ __launch_bounds__(kThreads) void tile_stats_kernel(
       m[j] = 0.0f;
 #pragma unroll
       for (int i = 0; i < 8; ++i) m[j] = fmaxf(m[j], fabsf(v[i][j]));
-      m[j] = wave_xor_max(m[j], 16);
-      m[j] = wave_xor_max(m[j], 32);
+      m[j] = max_xor32(max_xor16(m[j]));
     }
     if (lane < 16)
 #pragma unroll
@@ -159,8 +157,7 @@ __global__ __launch_bounds__(kThreads) void tile_stats_kernel(
 #pragma unroll
         for (int i = 0; i < 8; ++i)
           if (tile * kTile + kk + 16 * i < n) pk[j] = fmaxf(pk[j], fabsf(__fsub_rn(v[i][j], mu)));
-        pk[j] = wave_xor_max(pk[j], 16);
-        pk[j] = wave_xor_max(pk[j], 32);
+        pk[j] = max_xor32(max_xor16(pk[j]));
       }
       if (lane < 16)
 #pragma unroll
@@ -291,8 +288,7 @@ __global__ __launch_bounds__(kThreads) void quant_q_kernel(const void* q, int64_
     float amax = 0.0f;
 #pragma unroll
     for (int j = 0; j < CPT; ++j) amax = fmaxf(amax, fabsf(x[j]));
-#pragma unroll
-    for (int m = 1; m < 32; m <<= 1) amax = wave_xor_max(amax, m);
+    amax = half_wave_max(amax);
     const float s = int8_scale(amax), rs = recip_rn(s);
     if (row < n) {
       uint32_t packed[CPT / 4];
@@ -350,8 +346,7 @@ __global__ __launch_bounds__(kThreads) void quant_fp8_kernel(const void* x, int6
       amax = fmaxf(amax, fabsf(y));
     }
   }
-#pragma unroll
-  for (int m = 1; m < 64; m <<= 1) amax = wave_xor_max(amax, m);
+  amax = max_xor32(half_wave_max(amax));
   if (lane == 0) wmax[w] = amax;
   __syncthreads();
   amax = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
@@ -482,8 +477,7 @@ __global__ __launch_bounds__(kThreads) void quant_k_kernel(const void* k, int64_
 #pragma unroll
     for (int j = 0; j < CPT; ++j) amax = fmaxf(amax, fabsf(v[i][j]));
   }
-#pragma unroll
-  for (int m = 1; m < 32; m <<= 1) amax = wave_xor_max(amax, m);
+  amax = half_wave_max(amax);
   if ((lane & 31) == 0) gred[w][lane >> 5] = amax;
   __syncthreads();
   amax = fmaxf(gred[w][lane >> 5], gred[w ^ 2][lane >> 5]);

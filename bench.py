@@ -107,6 +107,7 @@ def cpu_baseline(q, k, v, smooth, rows, budget_s, qk="int8", rotate=False):
     attn_s = time.perf_counter() - t0
     ops = 4.0 * B * H * len(ids) * N * D
     threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    full_s = prep_s + attn_s * N / len(ids)
     return {
         "value": ops / attn_s / 1e12,
         "unit": "TOPS",
@@ -117,11 +118,29 @@ def cpu_baseline(q, k, v, smooth, rows, budget_s, qk="int8", rotate=False):
                   f"{', FP8 block QK' if qk == 'fp8' else ''}) "
                   f"x all {N} keys x {B * H} heads (P bytes + decoded-payload fp64 accumulation), OpenMP over rows; "
                   f"value = 4*B*H*rows*N*D / time. Full preprocessing of the same inputs (single thread) "
-                  f"took {prep_s:.2f} s; extrapolated full forward = {prep_s + attn_s * N / len(ids):.1f} s",
+                  f"took {prep_s:.2f} s; extrapolated full forward = {full_s:.1f} s",
         "attention_s": attn_s,
         "prep_s": prep_s,
-        "cpu_model": platform.processor() or platform.machine(),
+        "sample_rows_per_head": int(len(ids)),
+        "extrapolated_full_forward_s": full_s,
+        "extrapolation": "linear in query rows (attention) + full preprocessing",
+        "cpu_model": cpu_model(),
+        "os_cpu_count": os.cpu_count(),
+        "omp_threads": threads,
+        "torch_threads": torch.get_num_threads(),
     }
+
+
+def cpu_model():
+    """CPU model name from /proc/cpuinfo (platform.processor() is empty on the GPU box)."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
 
 
 def main():

@@ -145,6 +145,26 @@ def _strides4(x):
     return x.stride(0), x.stride(1), x.stride(2)
 
 
+def _check_qk_pair(q, k):
+    """Q and K must agree in batch, heads and head dim: the C ABI takes one B/H/D for both."""
+    if q.dim() != 4 or k.dim() != 4:
+        raise VcxError("Q/K must be [B,H,N,D]")
+    if q.shape[0] != k.shape[0] or q.shape[1] != k.shape[1] or q.shape[3] != k.shape[3]:
+        raise VcxError(f"Q {tuple(q.shape)} and K {tuple(k.shape)} must match in batch, heads and head dim")
+    if q.numel() == 0 or k.numel() == 0:
+        raise VcxError("Q/K must be nonempty")
+
+
+def _output(out, shape, dtype, device):
+    """The caller's output buffer (checked against what the kernel writes) or a new one."""
+    if out is None:
+        return torch.empty(shape, dtype=dtype, device=device)
+    if tuple(out.shape) != tuple(shape) or out.dtype != dtype or out.device != device:
+        raise VcxError(f"out must be {dtype} {tuple(shape)} on {device}; got {out.dtype} "
+                       f"{tuple(out.shape)} on {out.device}")
+    return out
+
+
 def workspace_bytes(op: int, B: int, H: int, N: int, D: int, smooth: bool = False, clusters: int = 8) -> int:
     out = ctypes.c_size_t(0)
     _check(lib().vcx_workspace_bytes(op, B, H, N, D, int(smooth), clusters, ctypes.byref(out)),
@@ -200,9 +220,10 @@ def group_values(v, clusters: int, iterations: int, debug: bool = False):
 def prepare_qk(q, k, perm=None, hadamard: bool = False):
     """INT8 Q/K with Sage per-thread scales after K centring: (q8, qs, k8, ks, km).
     hadamard=True rotates Q and the centred K (normalized Sylvester transform) first."""
-    dev = _require_device(q, k, perm)
     if q.dtype not in _DTYPE or k.dtype != q.dtype:
         raise VcxError("Q/K require matching float16/bfloat16")
+    _check_qk_pair(q, k)
+    dev = _require_device(q, k, perm)
     B, H, Nq, D = q.shape
     Nk = k.shape[2]
     qsb, qsh, qsn = _strides4(q)
@@ -253,9 +274,10 @@ def prepare_qk_fp8(q, k):
     """Block-scaled E4M3 Q/K (Q 64-row blocks, centred K 128-row blocks):
     (q8 uint8 [B,H,Nq,D], qs [B,H,ceil(Nq/64)], k8 uint8 [B,H,Nk,D], ks [B,H,ceil(Nk/128)],
     km fp32 [B,H,D])."""
-    dev = _require_device(q, k)
     if q.dtype not in _DTYPE or k.dtype != q.dtype:
         raise VcxError("Q/K require matching float16/bfloat16")
+    _check_qk_pair(q, k)
+    dev = _require_device(q, k)
     B, H, Nq, D = q.shape
     Nk = k.shape[2]
     qsb, qsh, qsn = _strides4(q)
@@ -313,7 +335,8 @@ def forward(q8, k8, v8, qs, ks, vs, means, expcast: bool, block_values: bool, ou
     """
     if affine and (not expcast or block_values):
         raise VcxError("the folded ExpCast encode applies to ExpCast without block values")
-    dev = _require_device(q8, k8, v8, qs, ks, vs)
+    if q8.dim() != 4:
+        raise VcxError("q must be [B,H,Nq,D]")
     B, H, Nq, D = q8.shape
     Nk = k8.shape[2]
     tiles = (Nk + 127) // 128
@@ -335,8 +358,8 @@ def forward(q8, k8, v8, qs, ks, vs, means, expcast: bool, block_values: bool, ou
     if tuple(vs.shape) != vs_shape:
         raise VcxError(f"vs must have shape {vs_shape}")
     out_dtype = torch.float16 if output_type == 0 else torch.bfloat16
-    if out is None:
-        out = torch.empty((B, H, Nq, D), dtype=out_dtype, device=dev)
+    out = _output(out, (B, H, Nq, D), out_dtype, q8.device)
+    dev = _require_device(q8, k8, v8, qs, ks, vs, means if block_values else None, out)
     osb, osh, osn = _strides4(out)
     pd = None
     r0 = r1 = 0
@@ -362,7 +385,8 @@ def forward_fp8(q8, k8, v8, qs, ks, vs, expcast: bool, output_type: int, scale: 
     runs the unfused encode (affine=False); expcast=False runs the Sage FP8 control
     probabilities. p_rows as in forward().
     """
-    dev = _require_device(q8, k8, v8, qs, ks, vs)
+    if q8.dim() != 4:
+        raise VcxError("q must be [B,H,Nq,D]")
     B, H, Nq, D = q8.shape
     Nk = k8.shape[2]
     tiles = (Nk + 127) // 128
@@ -378,8 +402,8 @@ def forward_fp8(q8, k8, v8, qs, ks, vs, expcast: bool, output_type: int, scale: 
             or tuple(vs.shape) != (B, H, D):
         raise VcxError("Incorrect FP8 block scales")
     out_dtype = torch.float16 if output_type == 0 else torch.bfloat16
-    if out is None:
-        out = torch.empty((B, H, Nq, D), dtype=out_dtype, device=dev)
+    out = _output(out, (B, H, Nq, D), out_dtype, q8.device)
+    dev = _require_device(q8, k8, v8, qs, ks, vs, out)
     osb, osh, osn = _strides4(out)
     pd = None
     r0 = r1 = 0

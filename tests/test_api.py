@@ -110,3 +110,46 @@ def test_forward_prepared_rejections(monkeypatch):
         api.forward_prepared(payload(True, vs_ndim=4), kernel_mode="vc31_unified")
     with pytest.raises(ValueError, match="v_smooth=False"):
         api.forward_prepared(payload(True), kernel_mode="vc16")
+
+
+# ---- binding-level checks (vcx): raised before the library is touched, so no kernel runs
+
+import vcx  # noqa: E402
+
+
+@pytest.fixture
+def no_native(monkeypatch):
+    def forbidden():
+        raise AssertionError("libvcx must not be called")
+    monkeypatch.setattr(vcx, "lib", forbidden)
+
+
+@pytest.mark.parametrize("bad", ["short", "dtype", "wide"])
+def test_forward_rejects_a_mismatched_out_buffer(no_native, bad):
+    st = payload(False)
+    B, H, Nq, D = st["q"].shape
+    out = {"short": torch.empty(B, H, Nq - 1, D, dtype=torch.bfloat16),
+           "dtype": torch.empty(B, H, Nq, D, dtype=torch.uint8),
+           "wide": torch.empty(B, H, Nq, D, dtype=torch.float32)}[bad]
+    with pytest.raises(vcx.VcxError, match="out must be"):
+        vcx.forward(*(st[x] for x in ("q", "k", "v", "qs", "ks", "vs", "means")), True, False, 1, 0.125, out=out)
+
+
+def test_forward_fp8_rejects_a_mismatched_out_buffer(no_native):
+    q8 = torch.zeros(1, 1, 65, 64, dtype=torch.uint8)
+    k8 = torch.zeros(1, 1, 129, 64, dtype=torch.uint8)
+    v8 = torch.zeros(1, 1, 64, 256, dtype=torch.uint8)
+    qs, ks, vs = torch.ones(1, 1, 2), torch.ones(1, 1, 2), torch.ones(1, 1, 64)
+    with pytest.raises(vcx.VcxError, match="out must be"):
+        vcx.forward_fp8(q8, k8, v8, qs, ks, vs, True, 1, 0.125, out=torch.empty(1, 1, 64, 64, dtype=torch.bfloat16))
+    with pytest.raises(vcx.VcxError, match="out must be"):
+        vcx.forward_fp8(q8, k8, v8, qs, ks, vs, True, 0, 0.125, out=torch.empty(1, 1, 65, 64, dtype=torch.bfloat16))
+
+
+@pytest.mark.parametrize("kshape", [(1, 1, 40, 128), (2, 2, 40, 128), (1, 2, 40, 64)])
+@pytest.mark.parametrize("fn", ["prepare_qk", "prepare_qk_fp8"])
+def test_prepare_qk_rejects_k_that_does_not_match_q(no_native, fn, kshape):
+    q = torch.zeros(1, 2, 33, 128, dtype=torch.bfloat16)
+    k = torch.zeros(*kshape, dtype=torch.bfloat16)
+    with pytest.raises(vcx.VcxError, match="must match in batch, heads and head dim"):
+        getattr(vcx, fn)(q, k)

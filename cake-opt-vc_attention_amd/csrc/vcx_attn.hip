@@ -198,15 +198,33 @@ __device__ inline v4f mfma_fp8(const v8i& a, const v8i& b, const v4f& c) {
   return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
 }
 
+// v_max_f32 / v_max3_f32 as single instructions: fmaxf lowers to maxnum, around which the
+// compiler inserts NaN-quieting copies of values coming out of the permlane swaps. The
+// operands here are finite or -inf.
+__device__ inline float vmax(float a, float b) {
+  float r;
+  asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
+__device__ inline float vmax3(float a, float b, float c) {
+  float r;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+
 // Row reductions over the four lane groups that hold one query row: gfx950
 // permlane swaps give each lane the values of lanes l^16 and l^32 without an LDS
 // round trip. Every lane of the row ends with the same value (the adds commute).
-__device__ inline float row_max(float x) {
+// running_max returns max(m, row maximum of x).
+__device__ inline float running_max(float m, float x) {
   const auto x16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  x = fmaxf(__uint_as_float(x16[0]), __uint_as_float(x16[1]));
+  x = vmax(__uint_as_float(x16[0]), __uint_as_float(x16[1]));
   const auto x32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return fmaxf(__uint_as_float(x32[0]), __uint_as_float(x32[1]));
+  return vmax3(m, __uint_as_float(x32[0]), __uint_as_float(x32[1]));
 }
+
+// Whether `pred` holds on some active lane (a scalar test of the lane mask).
+__device__ inline bool wave_any(bool pred) { return __builtin_amdgcn_ballot_w64(pred) != 0; }
 
 __device__ inline float row_sum(float x) {
   const auto x16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
@@ -255,6 +273,7 @@ struct Wave {
   v4f O[2][CB];
   float wts[2][4];  // VM 1, 2: pending mean weights of chunk tiles 4G..4G+3 (row li)
   int koff[DS], voff[2];
+  v8i ones;  // all-ones E4M3 A operand of the row-mass MFMA, kept in registers
   int G, li;
   int64_t bh_;
 
@@ -305,7 +324,7 @@ struct Wave {
 
     // ---- logits, online max, P bytes (ExpCast codes, or E4M3 probabilities on the control path)
     v8i P[2];
-    float alpha[2], tmass[2];
+    float mold[2], tmass[2];
 #pragma unroll
     for (int qg = 0; qg < 2; ++qg) {
       if constexpr (PM == 2) {
@@ -339,7 +358,8 @@ struct Wave {
               im = im > S[qg][j][r] ? im : S[qg][j][r];
               bs[j][r] = __int_as_float(S[qg][j][r]) - kBiasF;
             }
-          tmax = static_cast<float>(im - kBias) * scale;
+          // the biased bits read as 12582912 + max: one exact subtraction gives float(max)
+          tmax = (__int_as_float(im) - kBiasF) * scale;
         } else {
           float bm = -INFINITY;
 #pragma unroll
@@ -353,13 +373,16 @@ struct Wave {
             }
           tmax = bm * scale;
         }
-        tmax = row_max(tmax);
-        const float mn = fmaxf(m[qg], tmax);
-        alpha[qg] = __builtin_amdgcn_exp2f((m[qg] - mn) * 1.44269504088896341f);
+        const float mn = running_max(m[qg], tmax);
+        mold[qg] = m[qg];
         m[qg] = mn;
         const float gain = scale * kExpA;
-        const bool safe = scale >= 1.1754943508222875e-38f && __builtin_isfinite(gain) && fabsf(mn) <= 128.0f;
-        if (__all(safe)) {
+        // every lane admits the fold: scale normal, gain finite, |m'| <= 128 (lane masks
+        // combined on the scalar unit)
+        const uint64_t safe = __builtin_amdgcn_ballot_w64(scale >= 1.1754943508222875e-38f) &
+                              __builtin_amdgcn_ballot_w64(__builtin_isfinite(gain)) &
+                              __builtin_amdgcn_ballot_w64(fabsf(mn) <= 128.0f);
+        if (safe == __builtin_amdgcn_read_exec()) {
           const float bias = __builtin_fmaf(-mn, kExpA, kExpB);
 #pragma unroll
           for (int j = 0; j < 8; ++j) {
@@ -404,9 +427,8 @@ struct Wave {
               tmax = fmaxf(tmax, lg[j][r]);
             }
         }
-        tmax = row_max(tmax);
-        const float mn = fmaxf(m[qg], tmax);
-        alpha[qg] = __builtin_amdgcn_exp2f((m[qg] - mn) * 1.44269504088896341f);
+        const float mn = running_max(m[qg], tmax);
+        mold[qg] = m[qg];
         m[qg] = mn;
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
@@ -438,9 +460,8 @@ struct Wave {
             bs[j][r] = b;
             tmax = fmaxf(tmax, __builtin_fmaf(b, f, -kFp8Offset));
           }
-        tmax = row_max(tmax);
-        const float mn = fmaxf(m[qg], tmax);
-        alpha[qg] = __builtin_amdgcn_exp2f(m[qg] - mn);
+        const float mn = running_max(m[qg], tmax);
+        mold[qg] = m[qg];
         m[qg] = mn;
         float ls = 0.0f;
 #pragma unroll
@@ -470,22 +491,25 @@ struct Wave {
       }
     }
 
-    // ---- rescale the history only when some row maximum moved
+    // ---- rescale the history only when some row maximum moved: alpha = exp(m - m')
+    // (exp2 of the log2-domain difference on the control path) is exactly 1 on the other
+    // lanes, and O, den (and the pending mean weights) are scaled before this tile adds in.
 #pragma unroll
     for (int qg = 0; qg < 2; ++qg) {
-      if (__any(alpha[qg] != 1.0f)) {
+      if (wave_any(mold[qg] != m[qg])) {
+        const float alpha = EC ? __builtin_amdgcn_exp2f((mold[qg] - m[qg]) * 1.44269504088896341f)
+                               : __builtin_amdgcn_exp2f(mold[qg] - m[qg]);
 #pragma unroll
-        for (int cb = 0; cb < CB; ++cb) O[qg][cb] *= alpha[qg];
+        for (int cb = 0; cb < CB; ++cb) O[qg][cb] *= alpha;
+        den[qg] *= alpha;
         if constexpr (SMOOTH) {
 #pragma unroll
-          for (int j = 0; j < 4; ++j) wts[qg][j] *= alpha[qg];
+          for (int j = 0; j < 4; ++j) wts[qg][j] *= alpha;
         }
       }
     }
 
     // ---- O^T += V^T P^T, mass = 1^T P^T
-    const v8i ones = {0x38383838, 0x38383838, 0x38383838, 0x38383838,
-                      0x38383838, 0x38383838, 0x38383838, 0x38383838};
     const v4f zero = {0.0f, 0.0f, 0.0f, 0.0f};
     float mass[2];
     if constexpr (BSCALE) {
@@ -496,7 +520,7 @@ struct Wave {
       for (int qg = 0; qg < 2; ++qg) {
         if constexpr (EC) mass[qg] = mfma_fp8(ones, P[qg], zero)[0];
         else mass[qg] = tmass[qg];
-        den[qg] = den[qg] * alpha[qg] + mass[qg];
+        den[qg] += mass[qg];
       }
       const uint8_t* vsl = vsring + (t % LD::NR) * (4 * D);
       v8i vc = load_v(lv, 0), vn;
@@ -529,7 +553,7 @@ struct Wave {
       for (int qg = 0; qg < 2; ++qg) {
         if constexpr (EC) mass[qg] = mfma_fp8(ones, P[qg], zero)[0];
         else mass[qg] = tmass[qg];
-        den[qg] = den[qg] * alpha[qg] + mass[qg];
+        den[qg] += mass[qg];
       }
     }
     if constexpr (SMOOTH) {
@@ -641,6 +665,10 @@ __global__ __launch_bounds__(kThreadsPerBlock, (kBlocksPerCU<D, VM>)) void attn_
 #pragma unroll
     for (int cb = 0; cb < W::CB; ++cb) w.O[qg][cb] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
   }
+
+  // The opaque copy keeps the compiler from rebuilding the constant operand every tile.
+  w.ones = v8i{0x38383838, 0x38383838, 0x38383838, 0x38383838, 0x38383838, 0x38383838, 0x38383838, 0x38383838};
+  asm volatile("" : "+v"(w.ones));
 
   LD ld;
   ld.init(a, bh);

@@ -6,7 +6,7 @@ namespace vcx {
 size_t ws_prepare_qk(int64_t BH, int64_t N, int64_t D);
 size_t ws_prepare_v(int64_t BH, int64_t N, int64_t D);
 size_t ws_preprocess_qk(int64_t BH, int64_t N, int64_t D);
-size_t ws_group(int64_t BH, int64_t N, int64_t D);
+size_t ws_group(int64_t BH, int64_t N, int64_t D, int clusters);
 
 std::string& last_error() {
   static thread_local std::string msg;
@@ -77,7 +77,6 @@ extern "C" int vcx_value_token(int p) {
 extern "C" int vcx_workspace_bytes(int op, int64_t B, int64_t H, int64_t N, int64_t D, int smooth,
                                    int clusters, size_t* bytes) {
   (void)smooth;
-  (void)clusters;
   VCX_REQUIRE(bytes != nullptr, "bytes is null");
   VCX_REQUIRE(B >= 1 && H >= 1 && N >= 1 && D >= 1 && D <= 128, "invalid shape");
   VCX_REQUIRE(op == VCX_WS_PREPROCESS_QK || D == 64 || D == 128, "invalid shape");
@@ -86,7 +85,10 @@ extern "C" int vcx_workspace_bytes(int op, int64_t B, int64_t H, int64_t N, int6
     case VCX_WS_PREPROCESS_QK: *bytes = vcx::ws_preprocess_qk(BH, N, D); return VCX_OK;
     case VCX_WS_PREPARE_QK: *bytes = vcx::ws_prepare_qk(BH, N, D); return VCX_OK;
     case VCX_WS_PREPARE_V: *bytes = vcx::ws_prepare_v(BH, N, D); return VCX_OK;
-    case VCX_WS_GROUP: *bytes = vcx::ws_group(BH, N, D); return VCX_OK;
+    case VCX_WS_GROUP:
+      VCX_REQUIRE(clusters >= 1 && clusters <= 256, "clusters must be in [1, 256]");
+      *bytes = vcx::ws_group(BH, N, D, clusters);
+      return VCX_OK;
     default: return vcx::fail(VCX_EINVAL, "unknown workspace op %d", op);
   }
 }

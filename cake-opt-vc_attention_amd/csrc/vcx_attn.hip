@@ -43,9 +43,9 @@
 //
 // PM = 0 is the Sage FP8 control path (expcast=False; vc_sm90.cu:177,
 // attn_utils.cuh:355-455): a.sm = RN(sm * RN(log2 e)), base/factor as above,
-// m' = max(m, max fmaf(base, factor, -8.807)), P = E4M3(exp2(fmaf(base, factor, -m'))),
-// den and the mean restore use the unrounded sum of P. exp2 is v_exp_f32, so a P
-// byte can differ by one code from an exactly rounded exp2 next to a midpoint.
+// m' = max(m, max fmaf(base, factor, -8.807)), P = E4M3(exp2(fmaf(base, factor, -m'))) with
+// the correctly rounded binary32 exp2 (fp8_exp2_word: v_exp_f32, rechecked in binary64 next
+// to an E4M3 rounding midpoint); den and the mean restore use the unrounded sum of P.
 #include "vcx_common.hpp"
 
 #include <type_traits>
@@ -466,15 +466,15 @@ struct Wave {
         float ls = 0.0f;
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-          float pr[4];
+          float xs[4], pr[4];
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            pr[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(bs[j][r], f, -mn));
-            ls += pr[r];
+            xs[r] = __builtin_fmaf(bs[j][r], f, -mn);
+            pr[r] = __builtin_amdgcn_exp2f(xs[r]);
           }
-          int w = __builtin_amdgcn_cvt_pk_fp8_f32(pr[0], pr[1], 0, false);
-          w = __builtin_amdgcn_cvt_pk_fp8_f32(pr[2], pr[3], w, true);
-          P[qg][j] = w;
+          P[qg][j] = static_cast<int>(fp8_exp2_word<LAST>(xs, pr));
+#pragma unroll
+          for (int r = 0; r < 4; ++r) ls += pr[r];
         }
         tmass[qg] = row_sum(ls);
       }
@@ -939,6 +939,40 @@ extern "C" int vcx_attention_fwd_fp8(const uint8_t* q8, const uint8_t* k8, const
   const bool dump = p_dump != nullptr;
   return D == 128 ? launch_mode<128, 0, 1>(a, nblocks, dump, out_dtype, expcast, st)
                   : launch_mode<64, 0, 1>(a, nblocks, dump, out_dtype, expcast, st);
+}
+
+namespace vcx {
+namespace {
+// One thread per four inputs: the control path's probability bytes via fp8_exp2_word
+// (SAT: the form of the tiles with masked keys).
+template <bool SAT>
+__global__ void fp8_exp2_probe_kernel(const float* x, uint8_t* y, int64_t n) {
+  const int64_t i = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) * 4;
+  if (i >= n) return;
+  float xs[4], pr[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    xs[r] = i + r < n ? x[i + r] : -INFINITY;
+    pr[r] = __builtin_amdgcn_exp2f(xs[r]);
+  }
+  const uint32_t w = fp8_exp2_word<SAT>(xs, pr);
+#pragma unroll
+  for (int r = 0; r < 4; ++r)
+    if (i + r < n) y[i + r] = static_cast<uint8_t>(w >> (8 * r));
+}
+}  // namespace
+}  // namespace vcx
+
+extern "C" int vcx_fp8_exp2_codes(const float* x, uint8_t* y, int64_t n, int form, void* stream) {
+  VCX_REQUIRE(n >= 0 && (n == 0 || (x != nullptr && y != nullptr)), "invalid probe arguments");
+  VCX_REQUIRE(form == 0 || form == 1, "form must be 0 or 1");
+  VCX_REQUIRE(aligned(x, 4), "x must be 4-byte aligned");
+  if (n == 0) return VCX_OK;
+  const int64_t threads = cdiv(n, 4), blocks = cdiv(threads, 256);
+  VCX_REQUIRE(blocks < (int64_t(1) << 31), "n too large");
+  if (form) fp8_exp2_probe_kernel<true><<<dim3(static_cast<unsigned>(blocks)), 256, 0, static_cast<hipStream_t>(stream)>>>(x, y, n);
+  else fp8_exp2_probe_kernel<false><<<dim3(static_cast<unsigned>(blocks)), 256, 0, static_cast<hipStream_t>(stream)>>>(x, y, n);
+  return check_launch("fp8_exp2_probe_kernel");
 }
 
 namespace {

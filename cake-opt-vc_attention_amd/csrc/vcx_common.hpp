@@ -3,6 +3,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdarg>
 #include <cstdint>
@@ -97,6 +98,53 @@ __device__ inline float round_in(float f) { return in_to_f32<DT>(f32_to_in<DT>(f
 __device__ inline uint32_t e4m3_sat(float x) {
   float y = fminf(448.0f, fmaxf(-448.0f, x));
   return static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(y, 0.0f, 0, false)) & 0xffu;
+}
+
+// E4M3 bytes (packed, element 0 in the low byte) of four Sage FP8 control-path probabilities
+// p = exp2(x), equal to E4M3_RNE(RN_f32(exp2(x))) with a correctly rounded binary32 exp2.
+// On entry p holds the hardware exp2 (v_exp_f32, within one ulp of exp2 on every binary32
+// input). The bytes of p - 2 ulps and p + 2 ulps agree unless an E4M3 rounding midpoint lies
+// within two ulps of p; only then does the lane recompute exp2 in binary64 and round it once
+// to binary32 (p is updated to that value). The +-2 ulp neighbours of two probabilities come
+// from one 64-bit add each way (v_lshl_add_u64); a borrow out of a low half below 2 ulps (p
+// = 0 or nearly) only widens the window or yields a NaN byte, i.e. a needless recheck.
+// SAT = true forms the lower neighbours with a saturating subtraction instead, for tiles
+// with masked keys (p = exp2(-inf) = 0). Reference: the probability byte of
+// sal/sageattention_local/vc_reference.py:68-75 and sal/csrc/qattn/attn_utils.cuh:355-455.
+// Binary64 exp2 rounded once to binary32: one out-of-line copy for the rare recheck.
+__device__ __noinline__ inline float exp2_via_f64(float x) { return static_cast<float>(exp2(static_cast<double>(x))); }
+
+template <bool SAT = false>
+__device__ inline uint32_t fp8_exp2_word(const float (&x)[4], float (&p)[4]) {
+  constexpr uint64_t kTwoUlps = 0x0000000200000002ull;
+  float dn[4], up[4];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const uint64_t pr = (static_cast<uint64_t>(__float_as_uint(p[2 * h + 1])) << 32) | __float_as_uint(p[2 * h]);
+    const uint64_t u = pr + kTwoUlps;
+    up[2 * h] = __uint_as_float(static_cast<uint32_t>(u));
+    up[2 * h + 1] = __uint_as_float(static_cast<uint32_t>(u >> 32));
+    if constexpr (SAT) {
+#pragma unroll
+      for (int r = 2 * h; r < 2 * h + 2; ++r)
+        dn[r] = __uint_as_float(__builtin_elementwise_sub_sat(__float_as_uint(p[r]), 2u));  // p >= 0: stops at +0
+    } else {
+      const uint64_t d = pr - kTwoUlps;
+      dn[2 * h] = __uint_as_float(static_cast<uint32_t>(d));
+      dn[2 * h + 1] = __uint_as_float(static_cast<uint32_t>(d >> 32));
+    }
+  }
+  uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(dn[0], dn[1], 0, false));
+  lo = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(dn[2], dn[3], static_cast<int>(lo), true));
+  uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(up[0], up[1], 0, false));
+  hi = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(up[2], up[3], static_cast<int>(hi), true));
+  if (__builtin_expect(lo != hi, 0)) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) p[r] = exp2_via_f64(x[r]);
+    lo = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(p[0], p[1], 0, false));
+    lo = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(p[2], p[3], static_cast<int>(lo), true));
+  }
+  return lo;
 }
 
 // ExpCast constants (exact fp32 values of the reference, expcast.cuh:7).

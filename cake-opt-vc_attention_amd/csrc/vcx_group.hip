@@ -1,56 +1,76 @@
-// V grouping on gfx950: deterministic Lloyd clustering (<= 8 centers per head)
-// and a stable counting sort of the labels, as in the reference's fused
-// grouping (third_party/sageattention_local/csrc/vc/clustering.cu:21-167).
+// V grouping on gfx950: deterministic Lloyd clustering (1..256 centers per head) and a
+// stable counting sort of the labels, as in the reference's grouping
+// (third_party/sageattention_local/csrc/vc/clustering.cu:21-167 for at most 8 clusters,
+// pybind.cpp:6-44 for the wider range and the legacy entry point).
 //
-// Contract (identical in oracle/vc_oracle.c vco_group_values):
-//   ids = trunc(fp32 linspace(0, n-1, count)), centers = V[ids] as fp32;
+// Contract (identical in oracle/vc_oracle.c vco_group_values_ex):
+//   count = min(clusters, n); centers = centers_in, or V[ids] as fp32 with
+//   ids = trunc(fp32 linspace(0, n-1, count));
 //   distance = sum over d (sequential) of fma(x_d - c_d, x_d - c_d, acc) in fp64,
-//   argmin with ties to the lowest id; all but the last iteration replace every
-//   non-empty center by RN_f32(fp64 sum / count), the sum taken sequentially
-//   over tokens inside each 128-token tile and then sequentially over tiles;
-//   perm = stable sort of tokens by label.
+//   argmin with ties to the lowest id; every iteration but the last replaces every
+//   non-empty center by RN_f32(fp64 sum / count), the sum taken sequentially over the
+//   cluster's tokens inside each 128-token tile and then sequentially over tiles;
+//   perm = stable sort of tokens by label; centers_next = that same update applied to
+//   the final labels (the warm start of the next refresh).
+//
+// Two schedules, bit-identical where both apply:
+//   fused   (count <= 8): the assignment kernel also forms per-(tile, cluster) fp64 sums
+//           over ballot-built token lists; a second kernel adds them over tiles.
+//   general (any count, and every count under mode 1): the assignment kernel counts
+//           labels per tile in LDS; the labels are sorted, and the update walks each
+//           cluster's sorted token list (tokens ascending), closing a partial sum at each
+//           tile boundary. Tiles without the cluster contribute +0.0 to the fused sum,
+//           which leaves it unchanged (partial sums start at +0.0 and are never -0.0), so
+//           both schedules add the same values in the same order.
 #include "vcx_common.hpp"
+
+#include <type_traits>
 
 namespace vcx {
 namespace {
 
-constexpr int kMaxClusters = 8;
+constexpr int kFusedClusters = 8;  // the fused schedule's center slots per head
+constexpr int kMaxClusters = 256;
 constexpr int kGroupThreads = 128;  // one thread per token of a 128-token tile
 
 struct Ids {
-  int64_t v[kMaxClusters];
+  int32_t v[kMaxClusters];
 };
 
 __device__ inline const uint16_t* head_ptr(const void* x, int64_t bh, int64_t H, int64_t sb, int64_t sh) {
   return reinterpret_cast<const uint16_t*>(x) + (bh / H) * sb + (bh % H) * sh;
 }
 
-// Centers are kept as fp32 (the contract's values) and as their exact fp64
-// widening, which the assignment reads with wave-uniform (scalar) loads; unused
-// slots of the fp64 copy are zero.
+// Centers are kept as fp32 (the contract's values) and as their exact fp64 widening,
+// which the assignment reads with wave-uniform (scalar) loads. Slots are CS per head
+// (CS = 8 for the fused schedule, count rounded up to 8 for the general one); slots at or
+// past count hold zeros. Initial values: centers_in [BH][count][D], else V[ids].
 template <int DT>
 __global__ void grp_init_kernel(const void* v, int64_t H, int64_t sb, int64_t sh, int64_t sn, Ids ids,
-                                int count, int D, float* centers, double* centers64) {
+                                int count, int CS, int D, const float* centers_in, float* centers,
+                                double* centers64) {
   const int64_t bh = blockIdx.x;
   const uint16_t* base = head_ptr(v, bh, H, sb, sh);
   const int d = threadIdx.x;
-  for (int c = 0; c < kMaxClusters; ++c) {
-    const float x = c < count ? in_to_f32<DT>(base[ids.v[c] * sn + d]) : 0.0f;
-    if (c < count) centers[(bh * kMaxClusters + c) * D + d] = x;
-    centers64[(bh * kMaxClusters + c) * D + d] = static_cast<double>(x);
+  for (int c = 0; c < CS; ++c) {
+    float x = 0.0f;
+    if (c < count) x = centers_in ? centers_in[(bh * count + c) * D + d] : in_to_f32<DT>(base[ids.v[c] * sn + d]);
+    centers[(bh * CS + c) * D + d] = x;
+    centers64[(bh * CS + c) * D + d] = static_cast<double>(x);
   }
 }
 
-// grid (tiles, B*H), 128 threads. Assign every token of the tile; with STATS
-// also write the tile's per-cluster fp64 channel sums; always write the tile's
-// per-cluster counts (used by the center update and by the sort).
-// The tile is staged through LDS with coalesced loads; each thread then reads
-// its token's row 16 bytes at a time and runs the distance chains of all
-// clusters side by side (d outermost); the fp64 centers are wave-uniform and
-// come through scalar loads.
-template <int DT, int D, bool STATS, bool WIDE>
+// grid (tiles, B*H), 128 threads. Assign every token of the tile and write the tile's
+// per-cluster counts (pcnt, CS slots per tile). Fused schedule (!GENERAL, count <= 8):
+// with STATS also the tile's per-cluster fp64 channel sums. General schedule: counts from
+// an LDS histogram.
+// The tile is staged through LDS with coalesced loads; each thread then reads its token's
+// row 16 bytes at a time and runs the distance chains of 8 clusters side by side (d
+// outermost), chunk after chunk of 8 centers; the fp64 centers are wave-uniform and come
+// through scalar loads.
+template <int DT, int D, bool STATS, bool WIDE, bool GENERAL>
 __global__ __launch_bounds__(kGroupThreads) void grp_assign_kernel(
-    const void* v, int64_t H, int64_t n, int64_t sb, int64_t sh, int64_t sn, int count,
+    const void* v, int64_t H, int64_t n, int64_t sb, int64_t sh, int64_t sn, int count, int CS,
     const double* __restrict__ centers64, int32_t* labels, double* psum, int32_t* pcnt) {
   constexpr int kStride = D + 8;  // 16-bit elements per staged row (16-byte aligned rows)
   __shared__ __attribute__((aligned(16))) uint16_t xs[kTile * kStride];
@@ -89,88 +109,102 @@ __global__ __launch_bounds__(kGroupThreads) void grp_assign_kernel(
       *reinterpret_cast<uint32_t*>(&xs[row * kStride + 2 * part]) = val[k];
     }
   }
-  const double* cen = centers64 + bh * kMaxClusters * D;  // wave-uniform: scalar loads
+  __shared__ int hist[GENERAL ? kMaxClusters : 1];
+  if constexpr (GENERAL) {
+    for (int c = tid; c < count; c += kGroupThreads) hist[c] = 0;
+  }
   __syncthreads();
   const int64_t tok = tile * kTile + tid;
   int best = 0;
   if (tok < n) {
-    // distance_c = sum over d (in order) of fma(x_d - c_d, x_d - c_d, acc) in fp64
-    double acc[kMaxClusters];
+    double best_d = 0.0;
+    for (int c0 = 0; c0 < count; c0 += 8) {
+      const double* cen = centers64 + (bh * CS + c0) * D;  // wave-uniform: scalar loads
+      // distance_c = sum over d (in order) of fma(x_d - c_d, x_d - c_d, acc) in fp64
+      double acc[8];
 #pragma unroll
-    for (int c = 0; c < kMaxClusters; ++c) acc[c] = 0.0;
+      for (int c = 0; c < 8; ++c) acc[c] = 0.0;
 #pragma unroll 2
-    for (int i = 0; i < D / 8; ++i) {
-      const uint4 q = *reinterpret_cast<const uint4*>(&xs[tid * kStride + 8 * i]);
-      const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+      for (int i = 0; i < D / 8; ++i) {
+        const uint4 q = *reinterpret_cast<const uint4*>(&xs[tid * kStride + 8 * i]);
+        const uint32_t w[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const int d = 8 * i + 2 * k;
-        const double x0 = static_cast<double>(in_to_f32<DT>(w[k] & 0xffffu));
-        const double x1 = static_cast<double>(in_to_f32<DT>(w[k] >> 16));
+        for (int k = 0; k < 4; ++k) {
+          const int d = 8 * i + 2 * k;
+          const double x0 = static_cast<double>(in_to_f32<DT>(w[k] & 0xffffu));
+          const double x1 = static_cast<double>(in_to_f32<DT>(w[k] >> 16));
 #pragma unroll
-        for (int c = 0; c < kMaxClusters; ++c) {
-          const double d0 = __dsub_rn(x0, cen[c * D + d]);
-          acc[c] = __fma_rn(d0, d0, acc[c]);
-          const double d1 = __dsub_rn(x1, cen[c * D + d + 1]);
-          acc[c] = __fma_rn(d1, d1, acc[c]);
+          for (int c = 0; c < 8; ++c) {
+            const double d0 = __dsub_rn(x0, cen[c * D + d]);
+            acc[c] = __fma_rn(d0, d0, acc[c]);
+            const double d1 = __dsub_rn(x1, cen[c * D + d + 1]);
+            acc[c] = __fma_rn(d1, d1, acc[c]);
+          }
         }
       }
-    }
-    double best_d = acc[0];
 #pragma unroll
-    for (int c = 1; c < kMaxClusters; ++c)
-      if (c < count && acc[c] < best_d) {  // ties keep the lowest id
-        best_d = acc[c];
-        best = c;
-      }
+      for (int c = 0; c < 8; ++c)
+        if (c0 + c < count && ((c0 == 0 && c == 0) || acc[c] < best_d)) {  // ties keep the lowest id
+          best_d = acc[c];
+          best = c0 + c;
+        }
+    }
     labels[bh * n + tok] = best;
   }
-  // Stable order of the tile's tokens by label: wave ballots give each token its
-  // rank among the earlier tokens with the same label.
-  __shared__ int wcount[2][kMaxClusters];
-  __shared__ int start[kMaxClusters + 1];
-  __shared__ uint8_t order[kTile];
-  const int L = tok < n ? best : -1;
-  const int lane = tid & 63, wv = tid >> 6;
-  int rank = 0;
-#pragma unroll
-  for (int c = 0; c < kMaxClusters; ++c) {
-    const uint64_t m = __ballot(L == c);
-    if (L == c) rank = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m >> 32), __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m), 0));
-    if (lane == 0) wcount[wv][c] = __popcll(m);
-  }
-  __syncthreads();
-  if (tid == 0) {
-    int acc = 0;
-    for (int c = 0; c < kMaxClusters; ++c) {
-      start[c] = acc;
-      acc += wcount[0][c] + wcount[1][c];
-    }
-    start[kMaxClusters] = acc;
-  }
-  __syncthreads();
-  if (L >= 0) order[start[L] + (wv ? wcount[0][L] : 0) + rank] = static_cast<uint8_t>(tid);
-  const int64_t meta = (bh * tiles + tile) * kMaxClusters;
-  if (tid < count) pcnt[meta + tid] = wcount[0][tid] + wcount[1][tid];
-  if constexpr (STATS) {
+  const int64_t meta = (bh * tiles + tile) * CS;
+  if constexpr (GENERAL) {
+    if (tok < n) atomicAdd(&hist[best], 1);
     __syncthreads();
-    if (tid < D) {
-      // per-cluster sums over the tile's tokens in token order
-      for (int c = 0; c < count; ++c) {
-        double acc = 0.0;
-        const int e = start[c + 1];
-        for (int k = start[c]; k < e; ++k) {
-          const int t = order[k];
-          acc = __dadd_rn(acc, static_cast<double>(in_to_f32<DT>(xs[t * kStride + tid])));
+    for (int c = tid; c < count; c += kGroupThreads) pcnt[meta + c] = hist[c];
+    return;
+  } else {
+    // Stable order of the tile's tokens by label: wave ballots give each token its
+    // rank among the earlier tokens with the same label.
+    __shared__ int wcount[2][kFusedClusters];
+    __shared__ int start[kFusedClusters + 1];
+    __shared__ uint8_t order[kTile];
+    const int L = tok < n ? best : -1;
+    const int lane = tid & 63, wv = tid >> 6;
+    int rank = 0;
+#pragma unroll
+    for (int c = 0; c < kFusedClusters; ++c) {
+      const uint64_t m = __ballot(L == c);
+      if (L == c)
+        rank = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m >> 32), __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m), 0));
+      if (lane == 0) wcount[wv][c] = __popcll(m);
+    }
+    __syncthreads();
+    if (tid == 0) {
+      int acc = 0;
+      for (int c = 0; c < kFusedClusters; ++c) {
+        start[c] = acc;
+        acc += wcount[0][c] + wcount[1][c];
+      }
+      start[kFusedClusters] = acc;
+    }
+    __syncthreads();
+    if (L >= 0) order[start[L] + (wv ? wcount[0][L] : 0) + rank] = static_cast<uint8_t>(tid);
+    if (tid < count) pcnt[meta + tid] = wcount[0][tid] + wcount[1][tid];
+    if constexpr (STATS) {
+      __syncthreads();
+      if (tid < D) {
+        // per-cluster sums over the tile's tokens in token order
+        for (int c = 0; c < count; ++c) {
+          double acc = 0.0;
+          const int e = start[c + 1];
+          for (int k = start[c]; k < e; ++k) {
+            const int t = order[k];
+            acc = __dadd_rn(acc, static_cast<double>(in_to_f32<DT>(xs[t * kStride + tid])));
+          }
+          psum[(meta + c) * D + tid] = acc;
         }
-        psum[(meta + c) * D + tid] = acc;
       }
     }
   }
 }
 
-// grid (B*H, count), D threads: new center = RN_f32(sum / n) for a non-empty
-// cluster, the fp64 sum taken over tiles in order (loads batched).
+// Fused schedule. grid (B*H, count), D threads: new center = RN_f32(sum / n) for a
+// non-empty cluster, the fp64 sum taken over tiles in order (loads batched).
 __global__ void grp_update_kernel(float* centers, double* centers64, const double* psum, const int32_t* pcnt,
                                   int64_t tiles, int D) {
   const int64_t bh = blockIdx.x;
@@ -184,7 +218,7 @@ __global__ void grp_update_kernel(float* centers, double* centers64, const doubl
     int cnt[kBatch];
 #pragma unroll
     for (int i = 0; i < kBatch; ++i) {
-      const int64_t meta = (bh * tiles + t + i) * kMaxClusters + c;
+      const int64_t meta = (bh * tiles + t + i) * kFusedClusters + c;
       v[i] = psum[meta * D + d];
       cnt[i] = pcnt[meta];
     }
@@ -195,63 +229,108 @@ __global__ void grp_update_kernel(float* centers, double* centers64, const doubl
     }
   }
   for (; t < tiles; ++t) {
-    const int64_t meta = (bh * tiles + t) * kMaxClusters + c;
+    const int64_t meta = (bh * tiles + t) * kFusedClusters + c;
     s = __dadd_rn(s, psum[meta * D + d]);
     total += pcnt[meta];
   }
   if (total > 0) {
     const float x = static_cast<float>(__ddiv_rn(s, static_cast<double>(total)));
-    centers[(bh * kMaxClusters + c) * D + d] = x;
-    centers64[(bh * kMaxClusters + c) * D + d] = static_cast<double>(x);
+    centers[(bh * kFusedClusters + c) * D + d] = x;
+    centers64[(bh * kFusedClusters + c) * D + d] = static_cast<double>(x);
   }
 }
 
-// grid (B*H), 64 threads: start offset of each (tile, label) in the sorted order
-// (integer counts, so the batched loads do not change the result).
-__global__ void grp_offsets_kernel(const int32_t* pcnt, int64_t tiles, int count, int64_t* offsets) {
+// General schedule. grid (B*H, count), D threads: cluster c's tokens are
+// perm[offsets[tile 0][c] .. + n_c) in ascending order; each thread sums its channel,
+// closing the tile partial whenever the token's tile changes (loads batched, order kept).
+template <int DT>
+__global__ void grp_update_sorted_kernel(const void* v, int64_t H, int64_t n, int64_t sb, int64_t sh, int64_t sn,
+                                         int count, int CS, const int64_t* perm, const int64_t* offsets,
+                                         const int32_t* pcnt, int64_t tiles, int D, float* centers,
+                                         double* centers64) {
+  const int64_t bh = blockIdx.x;
+  const int c = blockIdx.y, d = threadIdx.x;
+  const uint16_t* base = head_ptr(v, bh, H, sb, sh);
+  const int64_t begin = offsets[bh * tiles * CS + c];
+  const int64_t end = offsets[(bh * tiles + tiles - 1) * CS + c] + pcnt[(bh * tiles + tiles - 1) * CS + c];
+  const int64_t* p = perm + bh * n;
+  constexpr int kBatch = 16;
+  double s = 0.0, part = 0.0;
+  int64_t cur = -1;
+  for (int64_t i = begin; i < end; i += kBatch) {
+    int64_t tk[kBatch];
+    float x[kBatch];
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) tk[j] = i + j < end ? p[i + j] : -1;
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) x[j] = tk[j] >= 0 ? in_to_f32<DT>(base[tk[j] * sn + d]) : 0.0f;
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) {
+      if (tk[j] < 0) break;
+      const int64_t tl = tk[j] >> 7;
+      if (tl != cur) {
+        s = __dadd_rn(s, part);
+        part = 0.0;
+        cur = tl;
+      }
+      part = __dadd_rn(part, static_cast<double>(x[j]));
+    }
+  }
+  s = __dadd_rn(s, part);
+  const int64_t total = end - begin;
+  if (total > 0) {
+    const float x = static_cast<float>(__ddiv_rn(s, static_cast<double>(total)));
+    centers[(bh * CS + c) * D + d] = x;
+    centers64[(bh * CS + c) * D + d] = static_cast<double>(x);
+  }
+}
+
+// grid (B*H), max(64, count rounded up to 64) threads: start offset of each (tile, label)
+// in the sorted order (integer counts, so the batched loads do not change the result).
+__global__ void grp_offsets_kernel(const int32_t* pcnt, int64_t tiles, int count, int CS, int64_t* offsets) {
   __shared__ int64_t total[kMaxClusters];
   const int64_t bh = blockIdx.x;
   const int c = threadIdx.x;
   constexpr int kBatch = 16;
-  const int32_t* col = pcnt + bh * tiles * kMaxClusters + c;
+  const int32_t* col = pcnt + bh * tiles * CS + c;
   if (c < count) {
     int64_t s = 0;
     int64_t t = 0;
     for (; t + kBatch <= tiles; t += kBatch) {
       int v[kBatch];
 #pragma unroll
-      for (int i = 0; i < kBatch; ++i) v[i] = col[(t + i) * kMaxClusters];
+      for (int i = 0; i < kBatch; ++i) v[i] = col[(t + i) * CS];
 #pragma unroll
       for (int i = 0; i < kBatch; ++i) s += v[i];
     }
-    for (; t < tiles; ++t) s += col[t * kMaxClusters];
+    for (; t < tiles; ++t) s += col[t * CS];
     total[c] = s;
   }
   __syncthreads();
   if (c < count) {
     int64_t off = 0;
     for (int i = 0; i < c; ++i) off += total[i];
-    int64_t* out = offsets + bh * tiles * kMaxClusters + c;
+    int64_t* out = offsets + bh * tiles * CS + c;
     int64_t t = 0;
     for (; t + kBatch <= tiles; t += kBatch) {
       int v[kBatch];
 #pragma unroll
-      for (int i = 0; i < kBatch; ++i) v[i] = col[(t + i) * kMaxClusters];
+      for (int i = 0; i < kBatch; ++i) v[i] = col[(t + i) * CS];
 #pragma unroll
       for (int i = 0; i < kBatch; ++i) {
-        out[(t + i) * kMaxClusters] = off;
+        out[(t + i) * CS] = off;
         off += v[i];
       }
     }
     for (; t < tiles; ++t) {
-      out[t * kMaxClusters] = off;
-      off += col[t * kMaxClusters];
+      out[t * CS] = off;
+      off += col[t * CS];
     }
   }
 }
 
 // grid (tiles, B*H), 128 threads: stable scatter of token indices.
-__global__ __launch_bounds__(kGroupThreads) void grp_scatter_kernel(const int32_t* labels, int64_t n,
+__global__ __launch_bounds__(kGroupThreads) void grp_scatter_kernel(const int32_t* labels, int64_t n, int CS,
                                                                     const int64_t* offsets, int64_t* perm) {
   __shared__ int lab[kTile];
   const int64_t tile = blockIdx.x, bh = blockIdx.y, tiles = gridDim.x;
@@ -263,7 +342,7 @@ __global__ __launch_bounds__(kGroupThreads) void grp_scatter_kernel(const int32_
   if (tok >= n) return;
   int rank = 0;
   for (int t = 0; t < tid; ++t) rank += lab[t] == L;
-  perm[bh * n + offsets[(bh * tiles + tile) * kMaxClusters + L] + rank] = tok;
+  perm[bh * n + offsets[(bh * tiles + tile) * CS + L] + rank] = tok;
 }
 
 size_t align_up(size_t x) { return (x + 255) & ~size_t(255); }
@@ -278,17 +357,21 @@ struct GroupWs {
   size_t bytes;
 };
 
-GroupWs group_ws(void* base, int64_t BH, int64_t N, int64_t D) {
+// Slots per head: 8 for the fused schedule, count rounded up to 8 for the general one
+// (the assignment reads centers in chunks of 8).
+int center_slots(int count, bool general) { return general ? (count + 7) / 8 * 8 : kFusedClusters; }
+
+GroupWs group_ws(void* base, int64_t BH, int64_t N, int64_t D, int CS, bool general) {
   const int64_t tiles = cdiv(N, kTile);
   GroupWs w{};
   size_t off = 0;
   auto take = [&](size_t bytes) { char* p = static_cast<char*>(base) + off; off += align_up(bytes); return p; };
-  w.centers = reinterpret_cast<float*>(take(sizeof(float) * BH * kMaxClusters * D));
-  w.centers64 = reinterpret_cast<double*>(take(sizeof(double) * BH * kMaxClusters * D));
-  w.psum = reinterpret_cast<double*>(take(sizeof(double) * BH * tiles * kMaxClusters * D));
-  w.pcnt = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * BH * tiles * kMaxClusters));
+  w.centers = reinterpret_cast<float*>(take(sizeof(float) * BH * CS * D));
+  w.centers64 = reinterpret_cast<double*>(take(sizeof(double) * BH * CS * D));
+  w.psum = general ? nullptr : reinterpret_cast<double*>(take(sizeof(double) * BH * tiles * CS * D));
+  w.pcnt = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * BH * tiles * CS));
   w.labels = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * BH * N));
-  w.offsets = reinterpret_cast<int64_t*>(take(sizeof(int64_t) * BH * tiles * kMaxClusters));
+  w.offsets = reinterpret_cast<int64_t*>(take(sizeof(int64_t) * BH * tiles * CS));
   w.bytes = off;
   return w;
 }
@@ -303,79 +386,113 @@ void linspace_ids(int64_t n, int count, Ids& ids) {
     float v;
     if (i < half) { const float t = step * static_cast<float>(i); v = start + t; }
     else { const float t = step * static_cast<float>(count - 1 - i); v = end - t; }
-    ids.v[i] = static_cast<int64_t>(v);
+    ids.v[i] = static_cast<int32_t>(v);
   }
 }
 
 }  // namespace
 
-size_t ws_group(int64_t BH, int64_t N, int64_t D) { return group_ws(nullptr, BH, N, D).bytes; }
+// Workspace of one grouping call: the larger of the two schedules' needs for this count
+// (count = min(clusters, N)); clusters <= 0 means the fused schedule's 8.
+size_t ws_group(int64_t BH, int64_t N, int64_t D, int clusters) {
+  const int count = static_cast<int>(std::min<int64_t>(clusters > 0 ? clusters : kFusedClusters, N));
+  size_t bytes = group_ws(nullptr, BH, N, D, center_slots(count, true), true).bytes;
+  if (count <= kFusedClusters) bytes = std::max(bytes, group_ws(nullptr, BH, N, D, kFusedClusters, false).bytes);
+  return bytes;
+}
 
 }  // namespace vcx
 
 using namespace vcx;
 
 extern "C" int vcx_group_values(const void* v, int dtype, int64_t B, int64_t H, int64_t N, int64_t D,
-                                int64_t v_sb, int64_t v_sh, int64_t v_sn, int clusters, int iterations,
-                                int64_t* perm, int32_t* labels, float* centers, void* workspace,
-                                size_t workspace_bytes, void* stream) {
+                                int64_t v_sb, int64_t v_sh, int64_t v_sn, int clusters, int iterations, int mode,
+                                const float* centers_in, int64_t* perm, int32_t* labels, float* centers,
+                                float* centers_next, void* workspace, size_t workspace_bytes, void* stream) {
   VCX_REQUIRE(B >= 1 && H >= 1 && N >= 1, "B, H, N must be positive");
   VCX_REQUIRE(D == 64 || D == 128, "D must be 64 or 128");
   VCX_REQUIRE(B * H <= 65535 && N < (int64_t(1) << 30), "shape exceeds launch bounds");
   VCX_REQUIRE(dtype == VCX_FLOAT16 || dtype == VCX_BFLOAT16, "dtype must be float16 or bfloat16");
-  VCX_REQUIRE(clusters >= 1 && clusters <= 256 && iterations >= 1 && iterations <= 100,
+  VCX_REQUIRE(clusters >= 1 && clusters <= kMaxClusters && iterations >= 1 && iterations <= 100,
               "clusters must be in [1, 256] and iterations in [1, 100]");
+  VCX_REQUIRE(mode == VCX_GROUP_AUTO || mode == VCX_GROUP_GENERAL, "mode must be VCX_GROUP_AUTO or VCX_GROUP_GENERAL");
   const int count = static_cast<int>(clusters < N ? clusters : N);
-  if (count > kMaxClusters)
-    return fail(VCX_EUNSUPPORTED, "grouping supports at most %d effective clusters (got %d)", kMaxClusters, count);
+  const bool general = mode == VCX_GROUP_GENERAL || count > kFusedClusters;
   VCX_REQUIRE(v != nullptr && aligned(v, 4), "v must be non-null and 4-byte aligned");
   VCX_REQUIRE(v_sb % 2 == 0 && v_sh % 2 == 0 && v_sn % 2 == 0 && v_sn >= D && v_sb >= 0 && v_sh >= 0,
               "v strides must be even, non-negative, with sn >= D");
   VCX_REQUIRE(perm != nullptr && aligned(perm, 8), "perm must be non-null and 8-byte aligned");
-  VCX_REQUIRE(aligned(labels, 4) && aligned(centers, 4), "labels/centers misaligned");
+  VCX_REQUIRE(aligned(labels, 4) && aligned(centers, 4) && aligned(centers_in, 4) && aligned(centers_next, 4),
+              "labels/centers misaligned");
   const int64_t BH = B * H, tiles = cdiv(N, kTile);
+  const int CS = center_slots(count, general);
   VCX_REQUIRE(workspace != nullptr && aligned(workspace, 256), "workspace must be non-null and 256-byte aligned");
-  GroupWs ws = group_ws(workspace, BH, N, D);
+  GroupWs ws = group_ws(workspace, BH, N, D, CS, general);
   VCX_REQUIRE(workspace_bytes >= ws.bytes, "workspace too small: need %zu bytes", ws.bytes);
   int32_t* lab = labels ? labels : ws.labels;
   Ids ids{};
   linspace_ids(N, count, ids);
   hipStream_t st = static_cast<hipStream_t>(stream);
   const bool wide = aligned(v, 16) && v_sb % 8 == 0 && v_sh % 8 == 0 && v_sn % 8 == 0;
+  const int offset_threads = std::max(64, (count + 63) / 64 * 64);
+  auto copy_centers = [&](float* dst) -> int {
+    hipError_t e = hipMemcpy2DAsync(dst, sizeof(float) * count * D, ws.centers, sizeof(float) * CS * D,
+                                    sizeof(float) * count * D, BH, hipMemcpyDeviceToDevice, st);
+    if (e != hipSuccess) return fail(VCX_EHIP, "hipMemcpy2DAsync: %s", hipGetErrorString(e));
+    return VCX_OK;
+  };
   auto run = [&](auto dt, auto dd) -> int {
     constexpr int DT = decltype(dt)::value, DD = decltype(dd)::value;
-    auto assign = [&](auto stats, double* psum) {
-      constexpr bool ST = decltype(stats)::value;
+    auto assign = [&](auto stats, auto gen, double* psum) {
+      constexpr bool ST = decltype(stats)::value, GE = decltype(gen)::value;
       if (wide)
-        grp_assign_kernel<DT, DD, ST, true><<<dim3(tiles, BH), kGroupThreads, 0, st>>>(
-            v, H, N, v_sb, v_sh, v_sn, count, ws.centers64, lab, psum, ws.pcnt);
+        grp_assign_kernel<DT, DD, ST, true, GE><<<dim3(tiles, BH), kGroupThreads, 0, st>>>(
+            v, H, N, v_sb, v_sh, v_sn, count, CS, ws.centers64, lab, psum, ws.pcnt);
       else
-        grp_assign_kernel<DT, DD, ST, false><<<dim3(tiles, BH), kGroupThreads, 0, st>>>(
-            v, H, N, v_sb, v_sh, v_sn, count, ws.centers64, lab, psum, ws.pcnt);
+        grp_assign_kernel<DT, DD, ST, false, GE><<<dim3(tiles, BH), kGroupThreads, 0, st>>>(
+            v, H, N, v_sb, v_sh, v_sn, count, CS, ws.centers64, lab, psum, ws.pcnt);
     };
-    grp_init_kernel<DT><<<dim3(BH), DD, 0, st>>>(v, H, v_sb, v_sh, v_sn, ids, count, DD, ws.centers, ws.centers64);
+    auto sort = [&]() -> int {
+      grp_offsets_kernel<<<dim3(BH), offset_threads, 0, st>>>(ws.pcnt, tiles, count, CS, ws.offsets);
+      VCX_LAUNCHED("grp_offsets_kernel");
+      grp_scatter_kernel<<<dim3(tiles, BH), kGroupThreads, 0, st>>>(lab, N, CS, ws.offsets, perm);
+      VCX_LAUNCHED("grp_scatter_kernel");
+      return VCX_OK;
+    };
+    grp_init_kernel<DT><<<dim3(BH), DD, 0, st>>>(v, H, v_sb, v_sh, v_sn, ids, count, CS, DD, centers_in,
+                                                  ws.centers, ws.centers64);
     VCX_LAUNCHED("grp_init_kernel");
     for (int it = 0; it < iterations; ++it) {
-      if (it + 1 < iterations) {
-        assign(std::true_type(), ws.psum);
-        VCX_LAUNCHED("grp_assign_kernel<stats>");
-        grp_update_kernel<<<dim3(BH, count), DD, 0, st>>>(ws.centers, ws.centers64, ws.psum, ws.pcnt, tiles, DD);
-        VCX_LAUNCHED("grp_update_kernel");
-      } else {
-        assign(std::false_type(), nullptr);
+      const bool last = it + 1 == iterations, update = !last || centers_next != nullptr;
+      if (!general) {
+        if (update) assign(std::true_type(), std::false_type(), ws.psum);
+        else assign(std::false_type(), std::false_type(), nullptr);
         VCX_LAUNCHED("grp_assign_kernel");
+        if (last) {
+          if (int rc = sort()) return rc;
+          if (centers)
+            if (int rc = copy_centers(centers)) return rc;
+        }
+        if (update) {
+          grp_update_kernel<<<dim3(BH, count), DD, 0, st>>>(ws.centers, ws.centers64, ws.psum, ws.pcnt, tiles, DD);
+          VCX_LAUNCHED("grp_update_kernel");
+        }
+      } else {
+        assign(std::false_type(), std::true_type(), nullptr);
+        VCX_LAUNCHED("grp_assign_kernel<general>");
+        if (int rc = sort()) return rc;
+        if (last && centers)
+          if (int rc = copy_centers(centers)) return rc;
+        if (update) {
+          grp_update_sorted_kernel<DT><<<dim3(BH, count), DD, 0, st>>>(v, H, N, v_sb, v_sh, v_sn, count, CS, perm,
+                                                                       ws.offsets, ws.pcnt, tiles, DD, ws.centers,
+                                                                       ws.centers64);
+          VCX_LAUNCHED("grp_update_sorted_kernel");
+        }
       }
     }
-    grp_offsets_kernel<<<dim3(BH), 64, 0, st>>>(ws.pcnt, tiles, count, ws.offsets);
-    VCX_LAUNCHED("grp_offsets_kernel");
-    grp_scatter_kernel<<<dim3(tiles, BH), kGroupThreads, 0, st>>>(lab, N, ws.offsets, perm);
-    VCX_LAUNCHED("grp_scatter_kernel");
-    if (centers) {
-      hipError_t e = hipMemcpy2DAsync(centers, sizeof(float) * count * DD, ws.centers,
-                                      sizeof(float) * kMaxClusters * DD, sizeof(float) * count * DD, BH,
-                                      hipMemcpyDeviceToDevice, st);
-      if (e != hipSuccess) return fail(VCX_EHIP, "hipMemcpy2DAsync: %s", hipGetErrorString(e));
-    }
+    if (centers_next)
+      if (int rc = copy_centers(centers_next)) return rc;
     return VCX_OK;
   };
   if (dtype == VCX_BFLOAT16) {

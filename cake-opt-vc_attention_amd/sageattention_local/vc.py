@@ -126,13 +126,17 @@ def prepare(q, k, v, *, expcast=True, v_smooth=True, clusters=8, iterations=2, s
 
     Grouping produces the permutation; K and V are gathered inside the
     quantizers (no permuted copies). ``v`` is in gfx950 tile storage order.
+    grouping_mode="fused" is the reference's group_values (the fused schedule for at most
+    8 effective clusters, the general one above); "legacy" runs the general schedule for
+    every count, as group_values_legacy does (vc.py:153). Both follow one arithmetic
+    contract, so they return the same permutation.
     """
     if v_scale_mode not in ("channel", "block"):
         raise ValueError("v_scale_mode must be 'channel' or 'block'")
     if grouping_mode not in ("fused", "legacy"):
         raise ValueError("grouping_mode must be 'fused' or 'legacy'")
     ext = _extension()
-    permutation = ext.group_values(v, clusters, iterations) if v_smooth else None
+    permutation = ext.group_values(v, clusters, iterations, legacy=grouping_mode == "legacy") if v_smooth else None
     q8, qs, k8, ks, km = ext.prepare_qk(q, k, permutation)
     v8, vs, means = ext.prepare_v(v, permutation, smooth=v_smooth, channel_scale=v_scale_mode == "channel")
     return {"q": q8, "k": k8, "v": v8, "qs": qs, "ks": ks, "vs": vs, "means": means, "km": km,
@@ -207,7 +211,9 @@ def sage_vc_build_info():
     return {"vc_extension": str(ext.LIB_PATH), "abi_version": ext.abi_version(), "arch": "gfx950",
             "algorithm": "Sage per-thread INT8 QK + VC block V residual/mean + ExpCast",
             "qk_hadamard": False, "v_block": 128, "mean_dtype": "float16",
-            "clustering": "<=8 clusters, Lloyd with fp64 distances, stable counting sort; fresh every call",
+            "clustering": "1..256 clusters, Lloyd with fp64 distances and tile-ordered fp64 center sums, stable "
+                          "counting sort; fused schedule for <= 8 clusters, general schedule above or with "
+                          "grouping_mode='legacy'; fresh every call",
             "expcast_probability": "without block values (default modes): folded encode RNE(fmaf(score, RN(scale*A), "
                                    "fmaf(-m, A, B))) with the 16-row |m| <= 128 fallback; otherwise exact FP32 RN "
                                    "multiply/subtract + single-rounding FMA + saturating RNE byte",

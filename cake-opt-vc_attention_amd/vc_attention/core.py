@@ -2,8 +2,8 @@
 
 Mirrors the reference's src/vc_attention/core.py: a frozen ``Config`` with
 validation (core.py:15-65), the request-scoped ``LayoutCache`` of the
-denoising-step schedule (core.py:181-226) and ``attention(...) -> (out,
-counters)`` with backend dispatch (core.py:263-371).
+denoising-step schedule with warm-started regrouping (core.py:153-226) and
+``attention(...) -> (out, counters)`` with backend dispatch (core.py:263-371).
 
 Backends of this build:
 * ``"hip"``: the gfx950 sageattn_vc path (Sage per-thread INT8 QK, ExpCast or
@@ -84,30 +84,58 @@ class Config:
             bad = [f"{k}={v!r}" for k, v in required.items() if getattr(self, k) != v]
             if bad:
                 raise ValueError("hip backend implements the sageattn_vc contract; it requires " + ", ".join(bad))
-            if self.clusters > 8:
-                raise ValueError("hip backend groups V into at most 8 clusters")
+            if self.clusters > 256:
+                raise ValueError("hip backend groups V into at most 256 clusters")
+
+
+@dataclass
+class _LayerLayout:
+    """What a layer keeps between denoising steps: the permutation and the grouping's next
+    centers (the warm start of its next refresh), keyed by the V signature."""
+    signature: tuple
+    permutation: object
+    centers: object
+    refreshed_at: int
+    last_step: int
 
 
 class LayoutCache:
-    """Request-scoped layout state (reference core.py:181-226).
+    """Request-scoped V layout of the denoising-step schedule (reference core.py:181-226).
 
-    Only the permutation is cached; means and residuals are recomputed on every
-    call. Grouping always starts from the linspace initialisation (the fused
-    sageattn_vc grouping), so cached centers are not reused as a warm start.
+    Within one request, a layer regroups V at the first step of its smoothing window and
+    then every ``refresh_interval`` steps while smoothing is active (steps below
+    ceil(total_steps * active_fraction)); between refreshes it reuses the permutation, while
+    means and residuals are recomputed from the current V on every call. A refresh starts
+    the grouping from the centers the previous refresh produced (the reference passes
+    state["centers"] back, core.py:216-221). A new request id, a changed V shape / device /
+    dtype / total_steps, or a step earlier than the layer's last one discards the layer's
+    layout. ``layout`` returns (permutation or None, smoothing active, refreshed now).
     """
 
     def __init__(self, config):
         self.config = config
         self._request_id = None
-        self._states = {}
+        self._layers = {}
 
     @property
     def entries(self):
-        return len(self._states)
+        return len(self._layers)
 
     def reset(self):
         self._request_id = None
-        self._states.clear()
+        self._layers.clear()
+
+    def _window(self, total_steps):
+        """Number of leading steps with smoothing active."""
+        return math.ceil(total_steps * self.config.active_fraction) if self.config.v_smooth else 0
+
+    def _entry(self, layer_id, signature, step):
+        """The layer's layout if it is still valid for this call, else None (and dropped)."""
+        entry = self._layers.get(layer_id)
+        if entry is not None and (entry.signature != signature or step < entry.last_step):
+            del self._layers[layer_id]
+            entry = None
+        return entry
 
     def layout(self, v, *, step, total_steps, request_id, layer_id, grouping=None):
         if request_id is None:
@@ -117,28 +145,25 @@ class LayoutCache:
         if request_id != self._request_id:
             self.reset()
             self._request_id = request_id
-        signature = (tuple(v.shape), str(v.device), v.dtype, total_steps)
-        state = self._states.get(layer_id)
-        if state is not None and (state["signature"] != signature or step < state["step"]):
-            state = None
-            self._states.pop(layer_id, None)
-        active = self.config.v_smooth and step < math.ceil(total_steps * self.config.active_fraction)
-        refresh = active and (state is None or step - state["refresh_step"] >= self.config.refresh_interval)
-        if refresh:
-            if grouping is None:
-                grouping = _hip_grouping(self.config)
-            pi = grouping(v)
-            state = {"signature": signature, "pi": pi, "refresh_step": step, "step": step}
-            self._states[layer_id] = state
-        if state is not None:
-            state["step"] = step
-        return (None if state is None else state["pi"]), active, refresh
+        entry = self._entry(layer_id, (tuple(v.shape), str(v.device), v.dtype, total_steps), step)
+        active = step < self._window(total_steps)
+        due = active and (entry is None or step - entry.refreshed_at >= self.config.refresh_interval)
+        if due:
+            group = grouping if grouping is not None else _hip_grouping(self.config)
+            perm, centers = group(v, None if entry is None else entry.centers)
+            entry = _LayerLayout((tuple(v.shape), str(v.device), v.dtype, total_steps), perm, centers, step, step)
+            self._layers[layer_id] = entry
+        elif entry is not None:
+            entry.last_step = step
+        return (entry.permutation if entry is not None else None), active, due
 
 
 def _hip_grouping(cfg):
+    """grouping(v, centers or None) -> (permutation, next centers) on the GPU."""
     import vcx
 
-    return lambda v: vcx.group_values(v, cfg.clusters, cfg.iterations)
+    return lambda v, centers: vcx.group_values(v, cfg.clusters, cfg.iterations, centers=centers,
+                                               return_centers=True)
 
 
 def _validate(q, k, v, causal, mask):

@@ -15,7 +15,7 @@ from pathlib import Path
 
 import torch
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 LIB_PATH = Path(__file__).resolve().parents[1] / "lib" / "libvcx.so"
 
 _OK, _EINVAL, _EUNSUPPORTED, _EHIP = 0, 1, 2, 3
@@ -42,7 +42,7 @@ def _declare(L):
     L.vcx_workspace_bytes.restype = i32
     L.vcx_workspace_bytes.argtypes = [i32, i64, i64, i64, i64, i32, i32, ctypes.POINTER(ctypes.c_size_t)]
     L.vcx_group_values.restype = i32
-    L.vcx_group_values.argtypes = [P, i32, i64, i64, i64, i64, i64, i64, i64, i32, i32, P, P, P, P,
+    L.vcx_group_values.argtypes = [P, i32, i64, i64, i64, i64, i64, i64, i64, i32, i32, i32, P, P, P, P, P, P,
                                    ctypes.c_size_t, P]
     L.vcx_prepare_qk_int8.restype = i32
     L.vcx_prepare_qk_int8.argtypes = [P, P, i32, i64, i64, i64, i64, i64, i64, i64, i64, i64, i64, i64,
@@ -66,6 +66,8 @@ def _declare(L):
                                         P, i64, i64, i64, P, i64, i64, P]
     L.vcx_expcast_codes.restype = i32
     L.vcx_expcast_codes.argtypes = [P, P, i64, P]
+    L.vcx_fp8_exp2_codes.restype = i32
+    L.vcx_fp8_exp2_codes.argtypes = [P, P, i64, i32, P]
     L.vcx_convert_probe.restype = i32
     L.vcx_convert_probe.argtypes = [P, P, P, i64, P]
     L.vcx_kernel_resources.restype = i32
@@ -77,7 +79,7 @@ def _declare(L):
 EXPORTED = ("vcx_abi_version", "vcx_last_error", "vcx_value_token", "vcx_workspace_bytes",
             "vcx_group_values", "vcx_prepare_qk_int8", "vcx_prepare_qk_int8_rotated", "vcx_preprocess_qk",
             "vcx_prepare_qk_fp8", "vcx_prepare_v_fp8", "vcx_attention_fwd", "vcx_attention_fwd_fp8",
-            "vcx_expcast_codes", "vcx_convert_probe", "vcx_kernel_resources", "vcx_kernel_resources_fp8",
+            "vcx_expcast_codes", "vcx_fp8_exp2_codes", "vcx_convert_probe", "vcx_kernel_resources", "vcx_kernel_resources_fp8",
             "vcx_clock_probe")
 
 
@@ -197,23 +199,44 @@ def abi_version() -> int:
 
 # ---------------------------------------------------------------- preprocessing
 
+GROUP_AUTO, GROUP_GENERAL = 0, 1
+
+
 @_device_call
-def group_values(v, clusters: int, iterations: int, debug: bool = False):
-    """int64 permutation [B,H,N] (+ int32 labels and fp32 centers when debug)."""
-    dev = _require_device(v)
+def group_values(v, clusters: int, iterations: int, debug: bool = False, *, legacy: bool = False,
+                 centers=None, return_centers: bool = False):
+    """Lloyd grouping of V tokens -> int64 permutation [B,H,N].
+
+    debug=True also returns int32 labels and the final assignment's fp32 centers
+    [B,H,count,D]; return_centers=True appends centers_next, the update of the final labels
+    (pass it back as `centers` to warm-start the next call). legacy=True runs the general
+    schedule for every count (the reference's group_values_legacy); otherwise counts above 8
+    take it and the rest the fused one. Results are identical between the two.
+    """
     if v.dtype not in _DTYPE:
         raise VcxError("grouping requires float16/bfloat16 V")
+    if v.dim() != 4:
+        raise VcxError("V must be [B,H,N,D]")
     B, H, N, D = v.shape
-    sb, sh, sn = _strides4(v)
     count = min(clusters, N)
+    if centers is not None and (centers.dtype != torch.float32 or tuple(centers.shape) != (B, H, count, D)
+                                or not centers.is_contiguous()):
+        raise VcxError(f"centers must be contiguous float32 {(B, H, count, D)}")
+    dev = _require_device(v, centers)
+    sb, sh, sn = _strides4(v)
     perm = torch.empty((B, H, N), dtype=torch.int64, device=dev)
     labels = torch.empty((B, H, N), dtype=torch.int32, device=dev) if debug else None
-    centers = torch.empty((B, H, count, D), dtype=torch.float32, device=dev) if debug else None
+    cen = torch.empty((B, H, count, D), dtype=torch.float32, device=dev) if debug else None
+    nxt = torch.empty((B, H, count, D), dtype=torch.float32, device=dev) if return_centers else None
     ws = _workspace(workspace_bytes(WS_GROUP, B, H, N, D, clusters=clusters), dev)
     _check(lib().vcx_group_values(_ptr(v), _DTYPE[v.dtype], B, H, N, D, sb, sh, sn, clusters, iterations,
-                                  _ptr(perm), _ptr(labels), _ptr(centers), _ptr(ws), ws.numel(), _stream(dev)),
+                                  GROUP_GENERAL if legacy else GROUP_AUTO, _ptr(centers), _ptr(perm),
+                                  _ptr(labels), _ptr(cen), _ptr(nxt), _ptr(ws), ws.numel(), _stream(dev)),
            "vcx_group_values")
-    return (perm, labels, centers) if debug else perm
+    out = (perm, labels, cen) if debug else (perm,)
+    if return_centers:
+        out = out + (nxt,)
+    return out if len(out) > 1 else perm
 
 
 @_device_call
@@ -424,6 +447,18 @@ def expcast_codes(x):
     x = x.float().contiguous()
     y = torch.empty(x.shape, dtype=torch.uint8, device=dev)
     _check(lib().vcx_expcast_codes(_ptr(x), _ptr(y), x.numel(), _stream(dev)), "vcx_expcast_codes")
+    return y
+
+
+@_device_call
+def fp8_exp2_codes(x, last_tile: bool = False):
+    """E4M3 bytes of the control path's probabilities exp2(x), from the fused kernel's device
+    code (last_tile: the variant of the tile with masked keys)."""
+    dev = _require_device(x)
+    x = x.float().contiguous()
+    y = torch.empty(x.shape, dtype=torch.uint8, device=dev)
+    _check(lib().vcx_fp8_exp2_codes(_ptr(x), _ptr(y), x.numel(), int(last_tile), _stream(dev)),
+           "vcx_fp8_exp2_codes")
     return y
 
 

@@ -37,7 +37,7 @@
 extern "C" {
 #endif
 
-#define VCX_ABI_VERSION 1
+#define VCX_ABI_VERSION 2
 #define VCX_CLOCK_PROBE_BLOCKS 8
 
 enum vcx_status {
@@ -48,6 +48,11 @@ enum vcx_status {
 };
 
 enum vcx_dtype { VCX_FLOAT16 = 0, VCX_BFLOAT16 = 1, VCX_FLOAT32 = 2 /* vcx_preprocess_qk only */ };
+
+enum vcx_group_mode {
+  VCX_GROUP_AUTO = 0,   /* fused schedule for <= 8 effective clusters, general above (group_values) */
+  VCX_GROUP_GENERAL = 1 /* general schedule for every count (group_values_legacy) */
+};
 
 enum vcx_workspace_op {
   VCX_WS_PREPARE_QK = 1, /* vcx_prepare_qk_int8 */
@@ -72,21 +77,27 @@ const char* vcx_last_error(void);
 int vcx_value_token(int p);
 
 /* Bytes of caller-provided workspace needed by one call of the given op.
- * clusters/iterations matter for VCX_WS_GROUP only; smooth for VCX_WS_PREPARE_V. */
+ * clusters matters for VCX_WS_GROUP only (either mode); smooth for VCX_WS_PREPARE_V. */
 int vcx_workspace_bytes(int op, int64_t B, int64_t H, int64_t N, int64_t D, int smooth,
                         int clusters, size_t* bytes);
 
-/* V grouping: count = min(clusters, N) <= 8 clusters per head, `iterations`
- * Lloyd passes (fp64 distances, ties to the lowest id, empty clusters keep
- * their center), then a stable counting sort by label.
- * Outputs: perm int64 [B,H,N]; labels int32 [B,H,N] (nullable);
- * centers fp32 [B,H,count,D] used by the final assignment (nullable).
- * Replaces _vc_sm90.group_values / group_values_debug
- * (third_party/sageattention_local/csrc/vc/pybind.cpp:39-44, clustering.cu:140-167). */
+/* V grouping: count = min(clusters, N) in 1..256 clusters per head, `iterations` Lloyd
+ * passes (fp64 distances, ties to the lowest id, empty clusters keep their center, center
+ * sums in fp64 tile order), then a stable counting sort by label. mode VCX_GROUP_AUTO runs
+ * the fused schedule for count <= 8 and the general one above; VCX_GROUP_GENERAL runs the
+ * general one for every count (same results where both apply).
+ * centers_in (nullable, fp32 [B,H,count,D]): initial centers (the warm start of a cached
+ * layout); NULL starts from V[trunc(fp32 linspace(0, N-1, count))].
+ * Outputs: perm int64 [B,H,N]; labels int32 [B,H,N] (nullable); centers fp32
+ * [B,H,count,D] used by the final assignment (nullable); centers_next fp32 [B,H,count,D]
+ * (nullable): the Lloyd update of the final labels, to pass as centers_in next time.
+ * Replaces _vc_sm90.group_values / group_values_debug / group_values_legacy(_debug)
+ * (third_party/sageattention_local/csrc/vc/pybind.cpp:6-44, clustering.cu:140-167) and the
+ * warm-started grouping of src/vc_attention/core.py:153-171 (cuda_backend.py:24-25). */
 int vcx_group_values(const void* v, int dtype, int64_t B, int64_t H, int64_t N, int64_t D,
-                     int64_t v_sb, int64_t v_sh, int64_t v_sn, int clusters, int iterations,
-                     int64_t* perm, int32_t* labels, float* centers, void* workspace,
-                     size_t workspace_bytes, void* stream);
+                     int64_t v_sb, int64_t v_sh, int64_t v_sn, int clusters, int iterations, int mode,
+                     const float* centers_in, int64_t* perm, int32_t* labels, float* centers,
+                     float* centers_next, void* workspace, size_t workspace_bytes, void* stream);
 
 /* Q/K INT8 with Sage per-thread scales, after K channel-mean centring.
  * perm (nullable, int64 [B,H,Nk]) gathers K tokens first. km_out (nullable)
@@ -193,6 +204,14 @@ int vcx_attention_fwd_fp8(const uint8_t* q8, const uint8_t* k8, const uint8_t* v
 /* ExpCast byte probe: y[i] = clamp(RNE(fmaf(x[i], 11.54156, 119.65)), 0, 120).
  * Replaces _vc_sm90.expcast_codes (third_party/sageattention_local/csrc/vc/preprocess.cu:170-179). */
 int vcx_expcast_codes(const float* x, uint8_t* y, int64_t n, void* stream);
+
+/* Control-path probability probe: y[i] = E4M3_RNE(RN_f32(exp2(x[i]))), the P byte of the
+ * Sage FP8 control path (vcx_attention_fwd expcast = 0) computed by the fused kernel's own
+ * device function (hardware exp2, rechecked in binary64 next to an E4M3 rounding midpoint);
+ * form 0 is the variant of the tiles before the last, 1 that of the last tile.
+ * Replaces the probability byte of third_party/sageattention_local/sageattention_local/
+ * vc_reference.py:68-75 (torch.exp2 then float8_e4m3fn), for the parity tests. */
+int vcx_fp8_exp2_codes(const float* x, uint8_t* y, int64_t n, int form, void* stream);
 
 /* Diagnostic probe of the gfx950 conversions the kernels rely on:
  * u8[i] = v_cvt_pk_u8_f32(x[i]) and f8[i] = v_cvt_pk_fp8_f32(clamp(x[i], +-448)).

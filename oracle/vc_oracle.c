@@ -18,6 +18,7 @@
  * Build with -ffp-contract=off so the compiler cannot fuse a*b+c by itself.
  */
 #include <math.h>
+#include <quadmath.h>
 #include <stdint.h>
 #include <stdlib.h>
 #include <string.h>
@@ -133,6 +134,42 @@ VCO_EXPORT void vco_e4m3_decode_array(const uint8_t* x, float* y, int64_t n) {
   for (int64_t i = 0; i < n; ++i) y[i] = vco_e4m3_decode(x[i]);
 }
 
+/* Correctly rounded binary32 exp2(x) (round to nearest, ties to even). The binary64 libm
+ * value (glibc's exp2 is within 0.51 ulp of binary64, i.e. 2^-52 relative) decides the
+ * binary32 rounding unless it lies within 2^-44 (relative) of a binary32 rounding boundary;
+ * then exp2 is evaluated again in binary128 (libquadmath, 113-bit significand) and rounded
+ * once to binary32. This defines the Sage FP8 control path's probability, whose reference
+ * (sal/sageattention_local/vc_reference.py:68-75: torch.exp2 of the binary32 shifted logit,
+ * then float8_e4m3fn) names no rounding for exp2. */
+VCO_EXPORT float vco_exp2_rn(float x) {
+  if (x != x) return x;
+  const double y = exp2((double)x);
+  const float f = (float)y;
+  if (f == INFINITY) return f;
+  const double up = 0.5 * ((double)f + (double)nextafterf(f, INFINITY));
+  const double dn = 0.5 * ((double)f + (double)nextafterf(f, -INFINITY));
+  const double tol = ldexp(y, -44);
+  if (fabs(y - up) <= tol || fabs(y - dn) <= tol) return (float)exp2q((__float128)x);
+  return f;
+}
+
+/* E4M3 byte of the control path's probability p = exp2(x): OCP E4M3 (RN-even, satfinite) of
+ * vco_exp2_rn(x) (sal/csrc/qattn/attn_utils.cuh:355-455 with exp_offset; the byte of
+ * vc_reference.py:75). */
+VCO_EXPORT uint8_t vco_fp8_exp2_code(float x) { return vco_e4m3_encode(vco_exp2_rn(x)); }
+
+VCO_EXPORT void vco_fp8_exp2_codes(const float* x, uint8_t* y, int64_t n) {
+#pragma omp parallel for schedule(static)
+  for (int64_t i = 0; i < n; ++i) y[i] = vco_fp8_exp2_code(x[i]);
+}
+
+/* y[i] = vco_fp8_exp2_code(x) for x with the binary32 bits first + i (an exhaustive sweep of
+ * a bit range without materializing the inputs). */
+VCO_EXPORT void vco_fp8_exp2_sweep(uint32_t first, int64_t n, uint8_t* y) {
+#pragma omp parallel for schedule(static)
+  for (int64_t i = 0; i < n; ++i) y[i] = vco_fp8_exp2_code(u32_as_f32(first + (uint32_t)i));
+}
+
 /* Round-to-nearest-even to an unsigned byte with saturation to [0, 255];
  * this is the documented behaviour of the gfx950 instruction the fused kernel
  * uses to produce ExpCast codes (v_cvt_pk_u8_f32). NaN maps to 0. */
@@ -201,7 +238,7 @@ VCO_EXPORT void vco_linspace_ids(int64_t n, int count, int64_t* ids) {
 }
 
 /* Deterministic Lloyd grouping, per head.
- * Reference policy: sal/csrc/vc/clustering.cu:21-137 and pybind.cpp:39-44
+ * Reference policy: sal/csrc/vc/clustering.cu:21-137 and pybind.cpp:6-44
  * (count = min(clusters, n); centers initialised to V[linspace ids]; each
  * iteration assigns every token to the nearest center with ties to the lowest
  * id; all but the last iteration recompute non-empty centers as the mean of
@@ -211,15 +248,39 @@ VCO_EXPORT void vco_linspace_ids(int64_t n, int count, int64_t* ids) {
  * fp32 |x|^2 + |c|^2 - 2x.c; see the FP64 oracle in
  * tests/test_sage_vc_grouping_cuda.py:8-23). Center sums are fp64: per
  * 128-token tile sequentially over tokens, then sequentially over tiles.
- * v: [BH][n][D]; perm [BH][n]; labels [BH][n]; centers [BH][count][D]. */
-VCO_EXPORT int vco_group_values(const uint16_t* v, int dtype, int64_t BH, int64_t n, int D,
-                                int clusters, int iterations, int64_t* perm, int32_t* labels,
-                                float* centers_out) {
+ * Warm start (src/vc_attention/core.py:153-171, the grouping a LayoutCache refresh
+ * reruns with its cached centers): centers_in (nullable, [BH][count][D]) replaces the
+ * linspace initialisation; centers_next (nullable) receives the same center update
+ * applied once more to the final labels, i.e. the centers core.py returns.
+ * v: [BH][n][D]; perm [BH][n]; labels [BH][n]; centers [BH][count][D] (the final
+ * assignment's centers). */
+static void update_centers(const uint16_t* vh, int dtype, int64_t n, int D, int count, const int32_t* lab,
+                           float* centers, double* tile_sum, double* total, int64_t* cnt) {
+  int64_t tiles = (n + 127) / 128;
+  for (int i = 0; i < count * D; ++i) total[i] = 0.0;
+  for (int c = 0; c < count; ++c) cnt[c] = 0;
+  for (int64_t tile = 0; tile < tiles; ++tile) {
+    for (int i = 0; i < count * D; ++i) tile_sum[i] = 0.0;
+    int64_t end = (tile + 1) * 128 < n ? (tile + 1) * 128 : n;
+    for (int64_t t = tile * 128; t < end; ++t) {
+      int c = lab[t];
+      cnt[c] += 1;
+      for (int d = 0; d < D; ++d) tile_sum[c * D + d] += (double)load_in(vh + t * D + d, dtype);
+    }
+    for (int i = 0; i < count * D; ++i) total[i] += tile_sum[i];
+  }
+  for (int c = 0; c < count; ++c)
+    if (cnt[c] > 0)
+      for (int d = 0; d < D; ++d) centers[c * D + d] = (float)(total[c * D + d] / (double)cnt[c]);
+}
+
+VCO_EXPORT int vco_group_values_ex(const uint16_t* v, int dtype, int64_t BH, int64_t n, int D,
+                                   int clusters, int iterations, const float* centers_in, int64_t* perm,
+                                   int32_t* labels, float* centers_out, float* centers_next) {
   int count = clusters < n ? clusters : (int)n;
   if (count < 1 || count > 256 || iterations < 1) return 1;
   int64_t ids[256];
   vco_linspace_ids(n, count, ids);
-  int64_t tiles = (n + 127) / 128;
   float* centers = (float*)malloc(sizeof(float) * count * D);
   double* tile_sum = (double*)malloc(sizeof(double) * count * D);
   double* total = (double*)malloc(sizeof(double) * count * D);
@@ -228,7 +289,8 @@ VCO_EXPORT int vco_group_values(const uint16_t* v, int dtype, int64_t BH, int64_
     const uint16_t* vh = v + h * n * D;
     int32_t* lab = labels + h * n;
     for (int c = 0; c < count; ++c)
-      for (int d = 0; d < D; ++d) centers[c * D + d] = load_in(vh + ids[c] * D + d, dtype);
+      for (int d = 0; d < D; ++d)
+        centers[c * D + d] = centers_in ? centers_in[(h * count + c) * D + d] : load_in(vh + ids[c] * D + d, dtype);
     for (int it = 0; it < iterations; ++it) {
       for (int64_t t = 0; t < n; ++t) {
         double best = INFINITY;
@@ -243,25 +305,13 @@ VCO_EXPORT int vco_group_values(const uint16_t* v, int dtype, int64_t BH, int64_
         }
         lab[t] = bestc;
       }
-      if (it + 1 < iterations) {
-        for (int i = 0; i < count * D; ++i) total[i] = 0.0;
-        for (int c = 0; c < count; ++c) cnt[c] = 0;
-        for (int64_t tile = 0; tile < tiles; ++tile) {
-          for (int i = 0; i < count * D; ++i) tile_sum[i] = 0.0;
-          int64_t end = (tile + 1) * 128 < n ? (tile + 1) * 128 : n;
-          for (int64_t t = tile * 128; t < end; ++t) {
-            int c = lab[t];
-            cnt[c] += 1;
-            for (int d = 0; d < D; ++d) tile_sum[c * D + d] += (double)load_in(vh + t * D + d, dtype);
-          }
-          for (int i = 0; i < count * D; ++i) total[i] += tile_sum[i];
-        }
-        for (int c = 0; c < count; ++c)
-          if (cnt[c] > 0)
-            for (int d = 0; d < D; ++d) centers[c * D + d] = (float)(total[c * D + d] / (double)cnt[c]);
-      }
+      if (it + 1 < iterations) update_centers(vh, dtype, n, D, count, lab, centers, tile_sum, total, cnt);
     }
     if (centers_out) memcpy(centers_out + h * count * D, centers, sizeof(float) * count * D);
+    if (centers_next) {
+      update_centers(vh, dtype, n, D, count, lab, centers, tile_sum, total, cnt);
+      memcpy(centers_next + h * count * D, centers, sizeof(float) * count * D);
+    }
     /* stable counting sort by label */
     int64_t pos = 0;
     for (int c = 0; c < count; ++c)
@@ -270,6 +320,12 @@ VCO_EXPORT int vco_group_values(const uint16_t* v, int dtype, int64_t BH, int64_
   }
   free(centers); free(tile_sum); free(total); free(cnt);
   return 0;
+}
+
+VCO_EXPORT int vco_group_values(const uint16_t* v, int dtype, int64_t BH, int64_t n, int D,
+                                int clusters, int iterations, int64_t* perm, int32_t* labels,
+                                float* centers_out) {
+  return vco_group_values_ex(v, dtype, BH, n, D, clusters, iterations, NULL, perm, labels, centers_out, NULL);
 }
 
 /* ------------------------------------------------------------------ */
@@ -800,10 +856,9 @@ static uint8_t* affine_safe_flags(const qk_view* v, int64_t BH, float sm, const 
  *   (tiles before the last: base = float(acc), factor = RN(s2 * dq); last tile:
  *   base = RN(float(acc) * dq), factor = s2);
  *   m' = max(m, max_k fmaf(base, factor, -8.807f)); alpha = exp2(m - m')
- *   p = exp2(fmaf(base, factor, -m')) (binary32, unrounded); P byte = E4M3(p), RN-even
+ *   p = exp2(fmaf(base, factor, -m')) (binary32, correctly rounded: vco_exp2_rn);
+ *   P byte = E4M3(p), RN-even;
  *   mass = sum p (unrounded, also in the mean restore); PV uses the decoded P byte.
- * exp2 is libm's exp2f here; the kernel's hardware exp2 may differ from it by an ulp,
- * which moves a P byte only when p sits next to an E4M3 rounding midpoint.
  * q8 [BH][nq][D]; k8 [BH][nk][D]; v8 LOGICAL [BH][D][tiles*128];
  * qs [BH][ceil(nq/64)*32]; ks [BH][tiles*4];
  * vs: NULL (no scale), [BH][D] (channel) or [BH][tiles][D] (block_scale=1);
@@ -876,7 +931,7 @@ static void attention_rows(const int8_t* q8, const int8_t* k8, const uint8_t* v8
             p = (double)vdec[code[i]];
             mass += p;
           } else {
-            float e = exp2f(fmaf(logit[i], factor[i], -mnew));
+            float e = vco_exp2_rn(fmaf(logit[i], factor[i], -mnew));
             code[i] = vco_e4m3_encode(e);
             p = (double)vdec[code[i]];
             mass += (double)e;

@@ -43,7 +43,7 @@ def build(force: bool = True) -> Path:
     _LIB_PATH.parent.mkdir(parents=True, exist_ok=True)
     tmp = _LIB_PATH.with_suffix(".so.tmp%d" % os.getpid())
     cmd = ["gcc", "-O2", "-fPIC", "-shared", "-ffp-contract=off", "-fno-fast-math",
-           "-fopenmp", "-Wall", "-o", str(tmp), str(_HERE / "vc_oracle.c"), "-lm"]
+           "-fopenmp", "-Wall", "-o", str(tmp), str(_HERE / "vc_oracle.c"), "-lquadmath", "-lm"]
     subprocess.run(cmd, check=True)
     os.replace(tmp, _LIB_PATH)
     return _LIB_PATH
@@ -64,8 +64,12 @@ def _declare(L):
     i64, i32, f32 = ctypes.c_int64, ctypes.c_int, ctypes.c_float
     L.vco_expcast_code.restype = ctypes.c_uint8
     L.vco_expcast_code.argtypes = [f32]
+    L.vco_exp2_rn.restype = f32
+    L.vco_exp2_rn.argtypes = [f32]
+    L.vco_fp8_exp2_sweep.argtypes = [ctypes.c_uint32, i64, P]
+    L.vco_fp8_exp2_sweep.restype = None
     for name in ("vco_expcast_codes", "vco_e4m3_encode_array", "vco_e4m3_decode_array",
-                 "vco_cvt_u8_array"):
+                 "vco_cvt_u8_array", "vco_fp8_exp2_codes"):
         getattr(L, name).argtypes = [P, P, i64]
         getattr(L, name).restype = None
     L.vco_tile_tree_sum.restype = ctypes.c_double
@@ -73,6 +77,8 @@ def _declare(L):
     L.vco_linspace_ids.argtypes = [i64, i32, P]
     L.vco_group_values.restype = i32
     L.vco_group_values.argtypes = [P, i32, i64, i64, i32, i32, i32, P, P, P]
+    L.vco_group_values_ex.restype = i32
+    L.vco_group_values_ex.argtypes = [P, i32, i64, i64, i32, i32, i32, P, P, P, P, P]
     L.vco_k_mean.argtypes = [P, i32, i64, i64, i32, P, P]
     L.vco_quant_q.argtypes = [P, i32, i64, i64, i32, P, P]
     L.vco_quant_k.argtypes = [P, i32, i64, i64, i32, P, P, P, P]
@@ -121,6 +127,26 @@ def e4m3_decode(b) -> np.ndarray:
     return y
 
 
+def exp2_rn(x: float) -> float:
+    """Correctly rounded binary32 exp2 of a binary32 value."""
+    return float(lib().vco_exp2_rn(float(np.float32(x))))
+
+
+def fp8_exp2_codes(x) -> np.ndarray:
+    """E4M3 bytes of the control path's probabilities exp2(x) (correctly rounded binary32)."""
+    x = _c(x, np.float32)
+    y = np.empty(x.shape, np.uint8)
+    lib().vco_fp8_exp2_codes(_ptr(x), _ptr(y), x.size)
+    return y
+
+
+def fp8_exp2_sweep(first_bits: int, n: int) -> np.ndarray:
+    """fp8_exp2_codes of the binary32 values whose bits are first_bits .. first_bits + n - 1."""
+    y = np.empty(n, np.uint8)
+    lib().vco_fp8_exp2_sweep(first_bits, n, _ptr(y))
+    return y
+
+
 def cvt_u8(x) -> np.ndarray:
     x = _c(x, np.float32)
     y = np.empty(x.shape, np.uint8)
@@ -156,18 +182,24 @@ def _shape4(x):
     return x.shape
 
 
-def group_values(v, clusters: int, iterations: int, dtype: str = "bfloat16"):
+def group_values(v, clusters: int, iterations: int, dtype: str = "bfloat16", centers_in=None,
+                 return_next: bool = False):
+    """(perm, labels, centers of the final assignment[, centers_next]); centers_in warm-starts."""
     B, H, N, D = _shape4(v)
     v = _c(v, np.uint16)
     count = min(clusters, N)
     perm = np.empty((B, H, N), np.int64)
     labels = np.empty((B, H, N), np.int32)
     centers = np.empty((B, H, count, D), np.float32)
-    rc = lib().vco_group_values(_ptr(v), DTYPES[dtype], B * H, N, D, clusters, iterations,
-                                _ptr(perm), _ptr(labels), _ptr(centers))
+    nxt = np.empty((B, H, count, D), np.float32) if return_next else None
+    cin = None if centers_in is None else _c(centers_in, np.float32)
+    if cin is not None and cin.shape != (B, H, count, D):
+        raise ValueError("centers_in must be [B,H,count,D]")
+    rc = lib().vco_group_values_ex(_ptr(v), DTYPES[dtype], B * H, N, D, clusters, iterations, _ptr(cin),
+                                   _ptr(perm), _ptr(labels), _ptr(centers), _ptr(nxt))
     if rc:
         raise ValueError("invalid clustering parameters")
-    return perm, labels, centers
+    return (perm, labels, centers, nxt) if return_next else (perm, labels, centers)
 
 
 def k_mean(k, perm=None, dtype: str = "bfloat16") -> np.ndarray:
@@ -298,14 +330,18 @@ def prepare_values(v, perm=None, channel_scale: bool = True, dtype: str = "bfloa
 
 
 def prepare(q, k, v, *, expcast=True, v_smooth=True, clusters=8, iterations=2, sm_scale=None,
-            v_scale_mode="channel", dtype="bfloat16", qk_hadamard=False):
+            v_scale_mode="channel", dtype="bfloat16", qk_hadamard=False, permutation=None):
     """State dict of the sageattn_vc contract (reference vc.py:141-170); v is LOGICAL.
 
     expcast only selects the probability path of ``reference``; the payloads are the same.
-    qk_hadamard rotates Q and the centred K before the INT8 quantizer.
+    qk_hadamard rotates Q and the centred K before the INT8 quantizer. permutation (int64
+    [B,H,N]) replaces the grouping: K and V are gathered by it whether or not smoothing is
+    on, as vc_attention does with a cached layout (src/vc_attention/core.py:305-310).
     """
     perm = None
-    if v_smooth:
+    if permutation is not None:
+        perm = np.ascontiguousarray(permutation, dtype=np.int64)
+    elif v_smooth:
         perm, _, _ = group_values(v, clusters, iterations, dtype)
     km = k_mean(k, perm, dtype)
     q8, qs = quant_q(q, dtype, rotate=qk_hadamard)

@@ -27,7 +27,7 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_abi_version_and_value_order():
-    assert vcx.abi_version() == vcx.ABI_VERSION == 1
+    assert vcx.abi_version() == vcx.ABI_VERSION == 2
     tok = vcx.value_token()
     assert sorted(tok) == list(range(128))
     # closed form: position p = 32G + b holds token 16(b/4) + 8((b/2)%2) + 2G + b%2
@@ -43,6 +43,11 @@ def test_abi_version_and_value_order():
 def test_workspace_sizes():
     for op in (vcx.WS_PREPARE_QK, vcx.WS_PREPARE_V, vcx.WS_GROUP):
         assert vcx.workspace_bytes(op, 1, 28, 37741, 128, True) > 0
+    # grouping workspace grows with the cluster count and covers both schedules
+    g = [vcx.workspace_bytes(vcx.WS_GROUP, 1, 28, 37741, 128, clusters=c) for c in (1, 8, 9, 64, 256)]
+    assert g[2] < g[3] < g[4] and g[0] <= g[1]
+    with pytest.raises(vcx.VcxError, match="clusters"):
+        vcx.workspace_bytes(vcx.WS_GROUP, 1, 1, 100, 128, clusters=300)
     with pytest.raises(vcx.VcxError, match="unknown workspace op"):
         vcx.workspace_bytes(9, 1, 1, 1, 128)
     with pytest.raises(vcx.VcxError, match="invalid shape"):
@@ -94,8 +99,15 @@ def test_invalid_calls_rejected_before_launch():
     assert L.vcx_prepare_qk_fp8(None, None, 1, 1, 1, 64, 128, 128, 0, 0, 128, 0, 0, 128,
                                 None, None, None, None, None, None, 0, None) == 1
     assert L.vcx_expcast_codes(None, None, -1, None) == 1
-    assert L.vcx_group_values(None, 1, 1, 1, 10, 128, 0, 0, 128, 9, 2, None, None, None, None, 0, None) == 2
-    assert "8 effective clusters" in L.vcx_last_error().decode()
+    # grouping: 1..256 clusters in either mode; anything else is rejected before a launch
+    grp = lambda clusters, mode: L.vcx_group_values(None, 1, 1, 1, 10, 128, 0, 0, 128, clusters, 2, mode, None,
+                                                    None, None, None, None, None, 0, None)
+    assert grp(257, 0) == 1 and "[1, 256]" in L.vcx_last_error().decode()
+    assert grp(16, 2) == 1 and "mode" in L.vcx_last_error().decode()
+    assert grp(16, 1) == 1 and "v must be non-null" in L.vcx_last_error().decode()
+    assert L.vcx_fp8_exp2_codes(None, None, 4, 0, None) == 1
+    assert L.vcx_fp8_exp2_codes(ctypes.c_void_p(4096), ctypes.c_void_p(4096), 4, 2, None) == 1
+    assert "form" in L.vcx_last_error().decode()
     khz = ctypes.c_int(0)
     assert L.vcx_clock_probe(1000, None, ctypes.byref(khz), None) == 1
     assert "null" in L.vcx_last_error().decode()

@@ -168,6 +168,68 @@ def test_grouping_bit_exact(dim, dtype, n, clusters, iterations):
     np.testing.assert_array_equal(perm.cpu().numpy(), eperm)
 
 
+@pytest.mark.parametrize("dim", [64, 128])
+@pytest.mark.parametrize("n,clusters,iterations", [(2049, 16, 2), (1000, 64, 3), (600, 256, 2), (100, 256, 2),
+                                                   (129, 9, 2), (37741, 32, 2)])
+def test_grouping_many_clusters_bit_exact(dim, n, clusters, iterations):
+    # 9..256 effective clusters take the general schedule (the reference's legacy range,
+    # pybind.cpp:6-44); labels, perm, both center sets bit-exact against the oracle.
+    _print_case("grouping many", dim, n, clusters, iterations)
+    torch.manual_seed(401 + n + clusters)
+    heads = 1 if n > 10000 else 2
+    v = torch.randn(1, heads, n, dim).to(torch.bfloat16)
+    perm, labels, centers, nxt = vcx.group_values(v.to(DEV), clusters, iterations, debug=True, return_centers=True)
+    eperm, elabels, ecenters, enext = o.group_values(bits(v), clusters, iterations, return_next=True)
+    np.testing.assert_array_equal(labels.cpu().numpy(), elabels)
+    np.testing.assert_array_equal(centers.cpu().numpy().view(np.uint32), ecenters.view(np.uint32))
+    np.testing.assert_array_equal(nxt.cpu().numpy().view(np.uint32), enext.view(np.uint32))
+    np.testing.assert_array_equal(perm.cpu().numpy(), eperm)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("n,clusters,iterations", [(1, 8, 2), (127, 3, 3), (2049, 8, 2), (5000, 8, 3)])
+def test_grouping_general_schedule_equals_fused(dtype, n, clusters, iterations):
+    # grouping_mode="legacy" runs the general schedule for every count; at <= 8 clusters it
+    # must give the fused schedule's bits exactly (and the oracle's).
+    _print_case("grouping legacy == fused", dtype, n, clusters, iterations)
+    torch.manual_seed(5 + n)
+    v = torch.randn(2, 2, n, 128).to(dtype).to(DEV)
+    fused = vcx.group_values(v, clusters, iterations, debug=True, return_centers=True)
+    general = vcx.group_values(v, clusters, iterations, debug=True, return_centers=True, legacy=True)
+    for a, b in zip(fused, general):
+        assert torch.equal(a, b)
+    eperm, elabels, ecenters, enext = o.group_values(bits(v.cpu()), clusters, iterations, dtype_name(dtype),
+                                                     return_next=True)
+    np.testing.assert_array_equal(general[0].cpu().numpy(), eperm)
+    np.testing.assert_array_equal(general[3].cpu().numpy().view(np.uint32), enext.view(np.uint32))
+
+
+@pytest.mark.parametrize("legacy", [False, True])
+@pytest.mark.parametrize("clusters", [8, 16])
+def test_grouping_warm_start_bit_exact(legacy, clusters):
+    # a cached layout's refresh starts from the previous call's next centers
+    # (src/vc_attention/core.py:216-221); strided NHD input on a side stream.
+    _print_case("grouping warm start", legacy, clusters)
+    torch.manual_seed(9)
+    v0 = torch.randn(1, 3, 700, 128).to(torch.bfloat16)
+    v1 = (v0.float() + 0.3 * torch.randn(1, 3, 700, 128)).to(torch.bfloat16)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        d1 = v1.transpose(1, 2).contiguous().to(DEV).transpose(1, 2)  # NHD storage, HND view
+        _, cached = vcx.group_values(v0.to(DEV), clusters, 2, legacy=legacy, return_centers=True)
+        perm, labels, centers, nxt = vcx.group_values(d1, clusters, 2, debug=True, legacy=legacy, centers=cached,
+                                                      return_centers=True)
+    side.synchronize()
+    _, _, _, ecached = o.group_values(bits(v0), clusters, 2, return_next=True)
+    np.testing.assert_array_equal(cached.cpu().numpy().view(np.uint32), ecached.view(np.uint32))
+    eperm, elabels, ecenters, enext = o.group_values(bits(v1), clusters, 2, centers_in=ecached, return_next=True)
+    np.testing.assert_array_equal(labels.cpu().numpy(), elabels)
+    np.testing.assert_array_equal(centers.cpu().numpy().view(np.uint32), ecenters.view(np.uint32))
+    np.testing.assert_array_equal(nxt.cpu().numpy().view(np.uint32), enext.view(np.uint32))
+    np.testing.assert_array_equal(perm.cpu().numpy(), eperm)
+
+
 def test_grouping_known_answers():
     x = torch.tensor([2, 0, 1, 2, 1, 0], dtype=torch.float32)
     v = x.view(1, 1, 6, 1).expand(2, 2, 6, 64).contiguous().to(torch.bfloat16).to(DEV)
@@ -478,8 +540,8 @@ CONTROL = [  # B, H, Nq, Nk, D, dtype, V mode
 @pytest.mark.parametrize("case", CONTROL, ids=lambda c: _ids(c[:6]) + "_" + c[6])
 def test_control_path_p_bytes_and_output(case):
     # expcast=False, the Sage FP8 control path (vc_reference.py:58-66, attn_utils.cuh:355-455):
-    # P = E4M3(exp2(fmaf(base, factor, -m'))) with the hardware exp2, so a byte may move by
-    # one code where p sits next to an E4M3 rounding midpoint (expected a few per 10^6).
+    # P = E4M3(exp2(fmaf(base, factor, -m'))) with the correctly rounded binary32 exp2:
+    # every P byte equals the oracle's.
     B, H, Nq, Nk, D, dt, vmode = case
     _print_case("control path", case)
     smooth = vmode != "none"
@@ -494,8 +556,7 @@ def test_control_path_p_bytes_and_output(case):
                           False, smooth, st["output_type"], st["scale"], channel_scale=vmode != "block",
                           p_rows=(0, Nq))
     eout, ecodes = o.reference(st, return_codes=True)
-    diff = np.abs(pd.cpu().numpy().astype(np.int32) - ecodes.astype(np.int32))
-    assert diff.max() <= 1 and np.count_nonzero(diff) <= max(4, diff.size // 100000), np.count_nonzero(diff)
+    np.testing.assert_array_equal(pd.cpu().numpy(), ecodes)
     got = out.float().cpu().numpy()
     assert np.isfinite(got).all()
     err, bound = output_bound(got, eout)
@@ -529,6 +590,43 @@ def test_control_path_uniform_attention_known_answer_and_end_to_end():
     err, bound = output_bound(got, eout)
     assert np.all(err <= bound)
     assert cosine(got, eout) >= 0.9999
+
+
+def _f32_bits(lo, hi):
+    """Bits of every binary32 value in [lo, hi] (same sign), ascending in magnitude."""
+    a, b = (int(np.float32(v).view(np.uint32)) for v in (lo, hi))
+    return min(a, b), max(a, b)
+
+
+@pytest.mark.parametrize("last_tile", [False, True])
+def test_control_probability_bytes_exhaustive(last_tile):
+    # Every binary32 input of the control path's P byte (x <= 8.8125 = the offset maximum 8.807
+    # plus its rounding): E4M3(RN_f32(exp2(x))) from the fused kernel's device function vs the
+    # oracle (binary64 exp2 rechecked in binary128), all 4.7e8 inputs with 2^-24 <= |x| <= 11 /
+    # 8.8125. Outside that range the byte is fixed: 1.0 (0x38) for |x| < 2^-24, 0 for x < -11.
+    chunk = 1 << 25
+    mism = 0
+    for lo, hi in ((2.0 ** -24, 8.8125), (-(2.0 ** -24), -11.0)):
+        a, b = _f32_bits(lo, hi)
+        for first in range(a, b + 1, chunk):
+            n = min(chunk, b + 1 - first)
+            _print_case("control probability sweep", last_tile, hex(first), n)
+            x = torch.arange(first, first + n, dtype=torch.int64, device=DEV).to(torch.int32).view(torch.float32)
+            got = vcx.fp8_exp2_codes(x, last_tile).cpu().numpy()
+            exp = o.fp8_exp2_sweep(first, n)
+            bad = np.flatnonzero(got != exp)
+            assert bad.size == 0, (hex(first + int(bad[0])), int(got[bad[0]]), int(exp[bad[0]]), bad.size)
+            mism += bad.size
+    # the two fixed ranges, checked on the device (2.8e9 inputs)
+    for (lo, hi), want in ((_f32_bits(0.0, 2.0 ** -24 * 0.99999994), 0x38), (_f32_bits(-0.0, -(2.0 ** -24) * 0.99999994), 0x38),
+                           (_f32_bits(-11.000001, -3.4028235e38), 0)):
+        for first in range(lo, hi + 1, 1 << 28):
+            n = min(1 << 28, hi + 1 - first)
+            x = torch.arange(first, first + n, dtype=torch.int64, device=DEV).to(torch.int32).view(torch.float32)
+            y = vcx.fp8_exp2_codes(x, last_tile)
+            assert bool((y == want).all()), (hex(first), want)
+    assert vcx.fp8_exp2_codes(torch.tensor([-np.inf], device=DEV), last_tile).item() == 0
+    assert mism == 0
 
 
 FOLDED = [  # B, H, Nq, Nk, D, dtype, q/k magnitude (large values push |m'| past 128: group fallback)

@@ -287,6 +287,65 @@ def fp64_lloyd(v, clusters, iterations):
     return labels, centers
 
 
+def fp64_lloyd_from(v, centers, iterations):
+    """The same FP64 Lloyd from given initial centers, one cluster at a time (bounded memory);
+    also returns the update of the final labels (the warm start core.py:153-171 caches)."""
+    x = v.double()
+    centers = centers.double()
+    count = centers.shape[2]
+
+    def update(labels, centers):
+        out = []
+        for c in range(count):
+            m = (labels == c)
+            n_c = m.sum(-1, keepdim=True)
+            out.append(torch.where(n_c > 0, (x * m.unsqueeze(-1)).sum(2) / n_c.clamp_min(1), centers[:, :, c]))
+        return torch.stack(out, 2)
+
+    for step in range(iterations):
+        dist = torch.stack([(x - centers[:, :, c:c + 1]).square().sum(-1) for c in range(count)], -1)
+        labels = dist.argmin(-1)
+        if step + 1 < iterations:
+            centers = update(labels, centers)
+    return labels, centers, update(labels, centers)
+
+
+@pytest.mark.parametrize("n,clusters,iterations", [(2049, 16, 2), (1000, 64, 3), (600, 256, 2), (100, 256, 2)])
+def test_grouping_many_clusters_matches_independent_fp64_lloyd(n, clusters, iterations):
+    # the reference's public grouping serves up to 256 clusters (pybind.cpp:6-44, legacy path)
+    torch.manual_seed(17 + n)
+    v = torch.randn(2, 2, n, 64).to(torch.bfloat16)
+    perm, labels, centers, nxt = o.group_values(bits(v), clusters, iterations, return_next=True)
+    count = min(clusters, n)
+    ids = torch.linspace(0, n - 1, count).long()
+    elabels, ecenters, enext = fp64_lloyd_from(v, v.float().index_select(2, ids), iterations)
+    np.testing.assert_array_equal(labels, elabels.numpy())
+    np.testing.assert_allclose(centers, ecenters.numpy(), rtol=2e-5, atol=2e-6)
+    np.testing.assert_allclose(nxt, enext.numpy(), rtol=2e-5, atol=2e-6)
+    np.testing.assert_array_equal(perm, elabels.argsort(dim=-1, stable=True).numpy())
+
+
+@pytest.mark.parametrize("clusters", [8, 16])
+def test_grouping_warm_start_matches_independent_fp64_lloyd(clusters):
+    # a LayoutCache refresh reruns grouping from the cached centers (src/vc_attention/core.py:216-221)
+    torch.manual_seed(3)
+    v0 = torch.randn(1, 3, 700, 128).to(torch.bfloat16)
+    v1 = (v0.float() + 0.3 * torch.randn(1, 3, 700, 128)).to(torch.bfloat16)
+    _, _, _, cached = o.group_values(bits(v0), clusters, 2, return_next=True)
+    perm, labels, centers, nxt = o.group_values(bits(v1), clusters, 2, centers_in=cached, return_next=True)
+    elabels, ecenters, enext = fp64_lloyd_from(v1, torch.from_numpy(cached), 2)
+    np.testing.assert_array_equal(labels, elabels.numpy())
+    np.testing.assert_allclose(centers, ecenters.numpy(), rtol=2e-5, atol=2e-6)
+    np.testing.assert_allclose(nxt, enext.numpy(), rtol=2e-5, atol=2e-6)
+    np.testing.assert_array_equal(perm, elabels.argsort(dim=-1, stable=True).numpy())
+    # one iteration from the cached centers is a single assignment to exactly those centers
+    _, l1, c1 = o.group_values(bits(v1), clusters, 1, centers_in=cached)
+    np.testing.assert_array_equal(c1.view(np.uint32), cached.view(np.uint32))
+    # the warm start changes the result relative to the linspace start (it is really used)
+    _, lcold, _ = o.group_values(bits(v1), clusters, 2)
+    assert not np.array_equal(lcold, labels)
+
+
 @pytest.mark.parametrize("n,clusters,iterations", [(1, 8, 2), (7, 8, 1), (127, 3, 3), (128, 1, 2), (129, 8, 2), (2049, 8, 2)])
 def test_grouping_matches_independent_fp64_lloyd(n, clusters, iterations):
     torch.manual_seed(211 + n)
@@ -822,3 +881,64 @@ def test_rotated_int8_quantizers(D):
     assert np.abs(approx - exact).max() <= 0.05 * np.abs(exact).max()
     # rotation changes the bytes (it is not silently skipped)
     assert not np.array_equal(q8, o.quant_q(qb)[0])
+
+
+# ---- the control path's probability: correctly rounded binary32 exp2, then E4M3
+
+def _round_f32(v):
+    """Round a positive Fraction to the nearest binary32 (ties to even, subnormals included)."""
+    from fractions import Fraction
+    e = v.numerator.bit_length() - v.denominator.bit_length()
+    while Fraction(2) ** e > v:
+        e -= 1
+    while Fraction(2) ** (e + 1) <= v:
+        e += 1
+    q = max(e - 23, -149)
+    scaled = v / Fraction(2) ** q
+    n = scaled.numerator // scaled.denominator
+    r = scaled - n
+    if r > Fraction(1, 2) or (r == Fraction(1, 2) and n % 2 == 1):
+        n += 1
+    return np.float32(float(Fraction(n) * Fraction(2) ** q))
+
+
+def _exp2_decimal(x):
+    """binary32 exp2(x) from a 60-digit decimal evaluation, rounded once."""
+    from decimal import Decimal, localcontext
+    from fractions import Fraction
+    with localcontext() as ctx:
+        ctx.prec = 60
+        d = (Decimal(float(x)) * Decimal(2).ln()).exp()
+    return _round_f32(Fraction(d))
+
+
+def test_exp2_rn_is_correctly_rounded():
+    # integers give exact powers of two (subnormal results included)
+    for k in range(-149, 128):
+        assert o.exp2_rn(k) == 2.0 ** k, k
+    assert o.exp2_rn(-150) == 0.0  # 2^-150 is the tie between 0 and 2^-149: even is 0
+    assert np.isinf(o.exp2_rn(128.0)) and o.exp2_rn(-np.inf) == 0.0
+    rng = np.random.default_rng(5)
+    xs = list(rng.uniform(-12, 9, 1500).astype(np.float32)) + list(rng.uniform(-1e-3, 1e-3, 200).astype(np.float32))
+    # inputs whose exp2 lies next to an E4M3 rounding midpoint (where the control path's byte
+    # depends on the binary32 rounding): x0 = RN(log2 M) and its neighbours
+    codes = [c for c in range(1, 126)]
+    vals = [float(o.e4m3_decode(np.array([c], np.uint8))[0]) for c in codes + [126]]
+    for lo, hi in zip(vals[:-1], vals[1:]):
+        x0 = np.float32(np.log2((lo + hi) / 2))
+        xs += list((np.array([x0]).view(np.int32) + np.arange(-12, 13)).astype(np.int32).view(np.float32))
+    for x in xs:
+        assert o.exp2_rn(x) == _exp2_decimal(x), float(x)
+
+
+def test_fp8_exp2_codes_known_answers():
+    # p = exp2(x): 2^0 = 1 -> 0x38; 2^-1 -> 0x30; the offset maximum 2^8.807 ~ 447.9 -> 448 (0x7E);
+    # 2^-10 is the tie between 0 and the smallest subnormal 2^-9 (even: 0); just above it: 2^-9
+    x = np.array([0.0, -1.0, 8.807, -10.0, np.nextafter(np.float32(-10.0), np.float32(0)), -np.inf, -20.0],
+                 np.float32)
+    np.testing.assert_array_equal(o.fp8_exp2_codes(x), [0x38, 0x30, 0x7E, 0, 1, 0, 0])
+    # the sweep form equals the array form
+    first = int(np.float32(-3.0).view(np.uint32))
+    xs = (np.uint32(first) + np.arange(4096, dtype=np.uint32)).view(np.float32)
+    np.testing.assert_array_equal(o.fp8_exp2_sweep(first, 4096), o.fp8_exp2_codes(xs))
+    np.testing.assert_array_equal(o.fp8_exp2_codes(xs), o.e4m3_encode([o.exp2_rn(v) for v in xs]))

@@ -20,18 +20,18 @@ def test_arms_match_the_reference_table():
 def test_metrics_known_values():
     ref = torch.tensor([3.0, 4.0, 0.0, 0.0])
     got = torch.tensor([3.0, 4.0, 1.0, -1.0])
-    m = replay.metrics(got, ref)
+    m = replay.error_metrics(got, ref)
     assert m["rmse"] == pytest.approx(math.sqrt(2 / 4))
     assert m["relative_rmse"] == pytest.approx(math.sqrt((2 / 4) / (25 / 4)))
     assert m["max_abs"] == 1.0
     assert m["cosine"] == pytest.approx(25 / (5 * math.sqrt(27)))
     with pytest.raises(ValueError, match="Nonfinite"):
-        replay.metrics(torch.tensor([float("nan")]), torch.tensor([1.0]))
+        replay.error_metrics(torch.tensor([float("nan")]), torch.tensor([1.0]))
 
 
 def test_synthetic_inputs_are_deterministic_and_clustered():
-    a = replay.synthetic(256, 2, 64, 7, True)
-    b = replay.synthetic(256, 2, 64, 7, True)
+    a = replay.synthetic_inputs(256, 2, 64, 7, True)
+    b = replay.synthetic_inputs(256, 2, 64, 7, True)
     for x, y in zip(a, b):
         assert x.shape == (1, 2, 256, 64) and torch.equal(x, y)
     v = a[2][0, 0]
@@ -39,7 +39,7 @@ def test_synthetic_inputs_are_deterministic_and_clustered():
     d = torch.cdist(v, v)
     near = (d < 2.0).float().sum(-1)
     assert near.min() >= 2 and len(torch.unique((d < 2.0).float(), dim=0)) <= 8
-    g = replay.synthetic(256, 2, 64, 7, False)
+    g = replay.synthetic_inputs(256, 2, 64, 7, False)
     assert torch.equal(g[0], a[0]) and torch.equal(g[1], a[1]) and not torch.equal(g[2], a[2])
 
 
@@ -88,11 +88,46 @@ def test_exact_attention_matches_a_float64_softmax():
     torch.testing.assert_close(got, want, rtol=1e-5, atol=1e-5)
 
 
+def test_synthetic_draw_order_is_q_k_v_then_centroids_then_assignment():
+    # the reference's generator order (replay.py:41-48), restated with an explicit gather
+    gen = torch.Generator().manual_seed(11)
+    q, k, v = (torch.randn(1, 3, 40, 64, generator=gen) for _ in range(3))
+    cent = torch.randn(1, 3, 8, 64, generator=gen) * 8
+    ids = torch.randint(0, 8, (1, 3, 40, 1), generator=gen)
+    want = torch.gather(cent, 2, ids.expand(1, 3, 40, 64)) + 0.1 * v
+    got = replay.synthetic_inputs(40, 3, 64, 11, True)
+    assert torch.equal(got[0], q) and torch.equal(got[1], k) and torch.equal(got[2], want)
+
+
 def test_argument_rules(tmp_path):
     with pytest.raises(SystemExit):
-        replay.parse_args(["--tokens", "0"])
+        replay.parse_args(["synthetic", "--tokens", "0"])
     with pytest.raises(SystemExit):
-        replay.parse_args(["--q-limit", "-1"])
-    args = replay.parse_args(["--q-start", "64", "--output", str(tmp_path / "r.json")])
-    with pytest.raises(ValueError, match="q-start"):
+        replay.parse_args(["synthetic", "--queries", "0:-1"])
+    with pytest.raises(SystemExit):
+        replay.parse_args(["synthetic", "--queries", "12"])
+    with pytest.raises(SystemExit):
+        replay.parse_args([])
+    a = replay.parse_args(["capture", "x.pt", "--layout", "NHD", "--queries", "128:0"])
+    assert a.source == "capture" and a.file == "x.pt" and a.queries == (128, 0)
+    args = replay.parse_args(["synthetic", "--queries", "64:128", "--output", str(tmp_path / "r.json")])
+    with pytest.raises(ValueError, match="128-row block"):
         replay.run(args)
+
+
+def test_select_queries_keeps_every_key_row_range():
+    q = torch.zeros(1, 1, 600, 64)
+    sel, rng = replay.select_queries(q, 128, 256)
+    assert sel.shape[-2] == 256 and rng == [128, 384]
+    sel, rng = replay.select_queries(q, 512, 0)
+    assert sel.shape[-2] == 88 and rng == [512, 600]
+    with pytest.raises(ValueError):
+        replay.select_queries(q, 640, 0)
+
+
+def test_time_arms_rotates_the_order_on_the_cpu():
+    seen = []
+    calls = {n: (lambda n=n: seen.append(n) or torch.zeros(1)) for n in "abcd"}
+    times, results = replay.time_arms(calls, torch.device("cpu"), warmup=1, repeats=3)
+    assert seen[:4] == list("abcd") and seen[4:8] == list("abcd") and seen[8:12] == list("bcda")
+    assert seen[12:] == list("cdab") and all(len(t) == 3 for t in times.values()) and set(results) == set("abcd")

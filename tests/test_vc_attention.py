@@ -52,7 +52,7 @@ def test_config_fields_and_defaults_match_reference():
     (dict(HIP, qk_format="fp8_block"), "qk_format='int8'"),
     (dict(HIP, q_block=128), "q_block=64"),
     (dict(HIP, mean_dtype="float32"), "mean_dtype='float16'"),
-    (dict(HIP, clusters=9), "at most 8 clusters"),
+    (dict(HIP, clusters=257), "at most 256 clusters"),
 ])
 def test_config_rejections(kwargs, match):
     with pytest.raises(ValueError, match=match):
@@ -64,14 +64,15 @@ def test_config_accepts_reference_and_hip_configurations():
     Config(backend="cuda_fp8", cuda_schedule="fused", q_block=64, kv_block=128, k_quant_block=256)
     Config(backend="npu_fp8", k_quant_block=256, kv_block=128)
     Config(**HIP, v_smooth=True, clusters=8, iterations=2)
+    Config(**HIP, v_smooth=True, clusters=256, iterations=3)
     Config(**dict(HIP, expcast=False))  # the Sage FP8 control arm (reference replay.py:17)
     Config(**dict(HIP, qk_hadamard=True))  # Q/K rotation inside the INT8 quantizers
 
 
 def _counting_grouping(calls):
-    def grouping(v):
-        calls.append(tuple(v.shape))
-        return torch.argsort(v[..., 0], dim=-1, stable=True)
+    def grouping(v, centers):
+        calls.append((tuple(v.shape), centers))
+        return torch.argsort(v[..., 0], dim=-1, stable=True), ("centers", len(calls))
     return grouping
 
 
@@ -97,6 +98,22 @@ def test_cache_reuses_only_layout_and_resets_requests_and_shapes():
     _, _, refreshed = cache.layout(v[:, :, :-1], step=1, total_steps=20, request_id="b", layer_id=0, grouping=g)
     assert refreshed
     assert len(calls) == 4
+
+
+def test_cache_refresh_warm_starts_from_the_previous_centers():
+    # src/vc_attention/core.py:216-221: a refresh passes the cached centers to the grouping;
+    # the first grouping of a layer (and any after a reset) starts cold.
+    _, _, v = tensors()
+    cache = LayoutCache(Config(**HIP, v_smooth=True, active_fraction=1.0, refresh_interval=2))
+    calls = []
+    g = _counting_grouping(calls)
+    for step in range(6):
+        cache.layout(v, step=step, total_steps=6, request_id="r", layer_id=7, grouping=g)
+    assert [c for _, c in calls] == [None, ("centers", 1), ("centers", 2)]
+    cache.layout(v, step=0, total_steps=6, request_id="next", layer_id=7, grouping=g)
+    assert calls[-1][1] is None
+    cache.layout(v[:, :1], step=2, total_steps=6, request_id="next", layer_id=7, grouping=g)
+    assert calls[-1][1] is None and len(calls) == 5  # a new V shape is a new layout
 
 
 def test_cache_layers_are_independent_and_step_regression_resets():

@@ -666,9 +666,10 @@ __global__ __launch_bounds__(kThreadsPerBlock, (kBlocksPerCU<D, VM>)) void attn_
     for (int cb = 0; cb < W::CB; ++cb) w.O[qg][cb] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
   }
 
-  // The opaque copy keeps the compiler from rebuilding the constant operand every tile.
+  // Without block values the opaque copy keeps the compiler from rebuilding the constant
+  // operand every tile; the smoothing variants have no registers to spare for it.
   w.ones = v8i{0x38383838, 0x38383838, 0x38383838, 0x38383838, 0x38383838, 0x38383838, 0x38383838, 0x38383838};
-  asm volatile("" : "+v"(w.ones));
+  if constexpr (VM == 0 && (D == 128 || PM == 2)) asm volatile("" : "+v"(w.ones));
 
   LD ld;
   ld.init(a, bh);

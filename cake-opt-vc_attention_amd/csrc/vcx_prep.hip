@@ -9,6 +9,8 @@
 // tree: sequential over i, then lanes xor 16, xor 32, then (w0+w1)+(w2+w3).
 #include "vcx_common.hpp"
 
+#include <mutex>
+
 namespace vcx {
 namespace {
 
@@ -750,6 +752,57 @@ extern "C" int vcx_prepare_qk_int8_rotated(const void* q, const void* k, int dty
                                            void* stream) {
   return prepare_qk_int8(q, k, dtype, B, H, Nq, Nk, D, q_sb, q_sh, q_sn, k_sb, k_sh, k_sn, perm, q8, qs, k8, ks,
                          km_out, workspace, workspace_bytes, stream, true);
+}
+
+// ---------------------------------------------------------------- allocation-free variant
+
+namespace {
+// Scratch of vcx_prepare_qk_int8_noalloc: the fp64 K tile sums and the binary32 K mean
+// (ws_prepare_qk bytes) of shapes up to this size. Each GPU the library runs on holds one
+// copy until the process ends; every call on that GPU shares it, so calls that overlap on
+// one GPU race. Every byte a call reads it first writes, so nothing needs clearing.
+constexpr size_t kNoAllocScratchBytes = VCX_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+constexpr int kScratchDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_address[kScratchDevices];  // device address of `scratch`, per device ordinal
+
+// The current device's address of `scratch`, resolved once per device (with that device
+// current) by hipGetSymbolAddress; the host-side name is not a device address.
+int scratch_address(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(VCX_EHIP, "hipGetDevice: %s", hipGetErrorString(e));
+  VCX_REQUIRE(dev >= 0 && dev < kScratchDevices, "device ordinal %d is beyond the scratch table", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_address[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr)
+      return fail(VCX_EHIP, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+    g_scratch_address[dev] = p;
+  }
+  *out = g_scratch_address[dev];
+  return VCX_OK;
+}
+}  // namespace
+
+extern "C" int vcx_prepare_qk_int8_noalloc(const void* q, const void* k, int dtype, int64_t B, int64_t H,
+                                           int64_t Nq, int64_t Nk, int64_t D, int64_t q_sb, int64_t q_sh,
+                                           int64_t q_sn, int64_t k_sb, int64_t k_sh, int64_t k_sn,
+                                           const int64_t* perm, int8_t* q8, float* qs, int8_t* k8, float* ks,
+                                           void* km_out, void* stream) {
+  if (int rc = check_shape(B, H, Nk, D)) return rc;
+  const size_t need = ws_prepare_qk(B * H, Nk, D);
+  VCX_REQUIRE(need <= kNoAllocScratchBytes,
+              "vcx_prepare_qk_int8_noalloc: B*H=%lld, Nk=%lld, D=%lld needs %zu scratch bytes, above its %zu; "
+              "call vcx_prepare_qk_int8 with a workspace", static_cast<long long>(B * H),
+              static_cast<long long>(Nk), static_cast<long long>(D), need, kNoAllocScratchBytes);
+  void* ws = nullptr;
+  if (int rc = scratch_address(&ws)) return rc;
+  return prepare_qk_int8(q, k, dtype, B, H, Nq, Nk, D, q_sb, q_sh, q_sn, k_sb, k_sh, k_sn, perm, q8, qs, k8, ks,
+                         km_out, ws, kNoAllocScratchBytes, stream, false);
 }
 
 extern "C" int vcx_prepare_qk_fp8(const void* q, const void* k, int dtype, int64_t B, int64_t H,

@@ -19,6 +19,7 @@ ABI_VERSION = 2
 LIB_PATH = Path(__file__).resolve().parents[1] / "lib" / "libvcx.so"
 
 _OK, _EINVAL, _EUNSUPPORTED, _EHIP = 0, 1, 2, 3
+NOALLOC_SCRATCH_BYTES = 32 << 20  # VCX_NOALLOC_SCRATCH_BYTES
 WS_PREPARE_QK, WS_PREPARE_V, WS_GROUP, WS_PREPROCESS_QK = 1, 2, 3, 4
 _DTYPE = {torch.float16: 0, torch.bfloat16: 1}
 _PRE_DTYPE = {torch.float16: 0, torch.bfloat16: 1, torch.float32: 2}
@@ -47,6 +48,9 @@ def _declare(L):
     L.vcx_prepare_qk_int8.restype = i32
     L.vcx_prepare_qk_int8.argtypes = [P, P, i32, i64, i64, i64, i64, i64, i64, i64, i64, i64, i64, i64,
                                       P, P, P, P, P, P, P, ctypes.c_size_t, P]
+    L.vcx_prepare_qk_int8_noalloc.restype = i32
+    L.vcx_prepare_qk_int8_noalloc.argtypes = [P, P, i32, i64, i64, i64, i64, i64, i64, i64, i64, i64, i64, i64,
+                                              P, P, P, P, P, P, P]
     L.vcx_prepare_qk_int8_rotated.restype = i32
     L.vcx_prepare_qk_int8_rotated.argtypes = L.vcx_prepare_qk_int8.argtypes
     L.vcx_preprocess_qk.restype = i32
@@ -77,7 +81,8 @@ def _declare(L):
 
 
 EXPORTED = ("vcx_abi_version", "vcx_last_error", "vcx_value_token", "vcx_workspace_bytes",
-            "vcx_group_values", "vcx_prepare_qk_int8", "vcx_prepare_qk_int8_rotated", "vcx_preprocess_qk",
+            "vcx_group_values", "vcx_prepare_qk_int8", "vcx_prepare_qk_int8_noalloc", "vcx_prepare_qk_int8_rotated",
+            "vcx_preprocess_qk",
             "vcx_prepare_qk_fp8", "vcx_prepare_v_fp8", "vcx_attention_fwd", "vcx_attention_fwd_fp8",
             "vcx_expcast_codes", "vcx_fp8_exp2_codes", "vcx_convert_probe", "vcx_kernel_resources", "vcx_kernel_resources_fp8",
             "vcx_clock_probe")

@@ -39,6 +39,7 @@ extern "C" {
 
 #define VCX_ABI_VERSION 2
 #define VCX_CLOCK_PROBE_BLOCKS 8
+#define VCX_NOALLOC_SCRATCH_BYTES (32u << 20) /* scratch of vcx_prepare_qk_int8_noalloc, per GPU */
 
 enum vcx_status {
   VCX_OK = 0,
@@ -110,6 +111,20 @@ int vcx_prepare_qk_int8(const void* q, const void* k, int dtype, int64_t B, int6
                         int64_t q_sn, int64_t k_sb, int64_t k_sh, int64_t k_sn,
                         const int64_t* perm, int8_t* q8, float* qs, int8_t* k8, float* ks,
                         void* km_out, void* workspace, size_t workspace_bytes, void* stream);
+
+/* vcx_prepare_qk_int8 without a workspace argument and without any allocation: the K tile
+ * sums and mean live in a file-scope device array of VCX_NOALLOC_SCRATCH_BYTES (32 MiB) per
+ * GPU, held until the process ends. Same arguments (minus the workspace),
+ * outputs and results as vcx_prepare_qk_int8; shapes whose ws_prepare_qk workspace
+ * (8*B*H*ceil(Nk/128)*D + 4*B*H*D bytes, 256-byte aligned slices) exceeds the scratch are
+ * rejected with VCX_EINVAL. All calls on one GPU share the scratch: calls that overlap on one
+ * GPU (concurrent streams or threads) race. No counterpart in the reference; for callers that
+ * cannot allocate (code under HIP graph capture, allocation-free serving loops). */
+int vcx_prepare_qk_int8_noalloc(const void* q, const void* k, int dtype, int64_t B, int64_t H,
+                                int64_t Nq, int64_t Nk, int64_t D, int64_t q_sb, int64_t q_sh,
+                                int64_t q_sn, int64_t k_sb, int64_t k_sh, int64_t k_sn,
+                                const int64_t* perm, int8_t* q8, float* qs, int8_t* k8, float* ks,
+                                void* km_out, void* stream);
 
 /* vcx_prepare_qk_int8 with Q and the centred K rotated by the normalized Sylvester-
  * Hadamard transform before the INT8 quantizer: q' = H(q), k' = H(RN_in(k - km)), in

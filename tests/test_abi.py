@@ -108,6 +108,10 @@ def test_invalid_calls_rejected_before_launch():
     assert L.vcx_fp8_exp2_codes(None, None, 4, 0, None) == 1
     assert L.vcx_fp8_exp2_codes(ctypes.c_void_p(4096), ctypes.c_void_p(4096), 4, 2, None) == 1
     assert "form" in L.vcx_last_error().decode()
+    # the allocation-free Q/K entry point refuses shapes beyond its 32 MiB scratch before any GPU call
+    assert L.vcx_prepare_qk_int8_noalloc(None, None, 1, 1, 64, 128, 100000, 128, 0, 0, 128, 0, 0, 128, None,
+                                         None, None, None, None, None, None) == 1
+    assert "scratch" in L.vcx_last_error().decode()
     khz = ctypes.c_int(0)
     assert L.vcx_clock_probe(1000, None, ctypes.byref(khz), None) == 1
     assert "null" in L.vcx_last_error().decode()

@@ -36,7 +36,7 @@ PEAK_HBM_GBS = 8000.0   # MI355X HBM3E, GB/s (published)
 # commands are in profiles/attn_kernel_main_hbm_bytes.txt (FP8 QK variant:
 # profiles/attn_kernel_fp8_main_hbm_bytes.txt). Counters cannot be read from inside this
 # process, so the figure is keyed by QK format and configuration and null where unmeasured.
-MEASURED_TRAFFIC_BYTES = {("int8", "main"): 3.128e9, ("fp8", "main"): 3.133e9}
+MEASURED_TRAFFIC_BYTES = {("int8", "main"): 3.088e9, ("fp8", "main"): 3.133e9}
 
 CONFIGS = {
     # name: (B, H, N, D, kind, v_smooth, description)

@@ -281,11 +281,13 @@ VCO_EXPORT int vco_group_values_ex(const uint16_t* v, int dtype, int64_t BH, int
   if (count < 1 || count > 256 || iterations < 1) return 1;
   int64_t ids[256];
   vco_linspace_ids(n, count, ids);
-  float* centers = (float*)malloc(sizeof(float) * count * D);
-  double* tile_sum = (double*)malloc(sizeof(double) * count * D);
-  double* total = (double*)malloc(sizeof(double) * count * D);
-  int64_t* cnt = (int64_t*)malloc(sizeof(int64_t) * count);
+  /* heads are independent: one head per OpenMP iteration, buffers per thread */
+#pragma omp parallel for schedule(dynamic)
   for (int64_t h = 0; h < BH; ++h) {
+    float* centers = (float*)malloc(sizeof(float) * count * D);
+    double* tile_sum = (double*)malloc(sizeof(double) * count * D);
+    double* total = (double*)malloc(sizeof(double) * count * D);
+    int64_t* cnt = (int64_t*)malloc(sizeof(int64_t) * count);
     const uint16_t* vh = v + h * n * D;
     int32_t* lab = labels + h * n;
     for (int c = 0; c < count; ++c)
@@ -317,8 +319,8 @@ VCO_EXPORT int vco_group_values_ex(const uint16_t* v, int dtype, int64_t BH, int
     for (int c = 0; c < count; ++c)
       for (int64_t t = 0; t < n; ++t)
         if (lab[t] == c) perm[h * n + pos++] = t;
+    free(centers); free(tile_sum); free(total); free(cnt);
   }
-  free(centers); free(tile_sum); free(total); free(cnt);
   return 0;
 }
 

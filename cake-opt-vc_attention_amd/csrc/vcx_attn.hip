@@ -249,11 +249,13 @@ __device__ inline float acc_value(const v4i& acc, int r) { return __int_as_float
 template <int D, int VM, bool DUMP, int PM, int QF = 0>
 struct Wave {
   static constexpr bool EC = PM != 0;  // ExpCast bytes (1 unfused, 2 folded) or the control path (0)
-  // Biased INT8 accumulators (float(acc) = one v_sub_f32): the folded path, and the unfused
+  // Biased INT8 accumulators (float(acc) = one v_sub_f32): the folded path, the unfused
   // path at D128 with channel-scale smoothing (same-box: smoothing 11.13 -> 11.06 ms, long
-  // 43.24 -> 43.00 ms). D64 (168 VGPRs at three waves per SIMD) and per-block V scales keep
-  // v_cvt_f32_i32: the bias register costs them spills.
-  static constexpr bool IB = QF == 0 && (PM == 2 || (PM == 1 && D == 128 && VM == 1));
+  // 43.24 -> 43.00 ms) and the control path at D128 (but its per-block-scale diagnostic
+  // variant). D64 (168 VGPRs at three waves per SIMD) and the unfused path with per-block V
+  // scales keep v_cvt_f32_i32: the bias register costs them spills.
+  static constexpr bool IB = QF == 0 && (PM == 2 || (PM == 1 && D == 128 && VM == 1) ||
+                                         (PM == 0 && D == 128 && !(VM == 2 && DUMP)));
   static constexpr int DS = D / 64;  // 64-deep QK steps
   static constexpr int CB = D / 16;  // 16-channel output blocks
   static constexpr bool SMOOTH = VM >= 1, BSCALE = VM == 2;
@@ -445,36 +447,105 @@ struct Wave {
         // running maximum with the upstream 8.807 offset, P = E4M3(exp2(.)) and an
         // unrounded mass.
         float bs[8][4];
-        float tmax = -INFINITY;
+        float tmax;
         const float dq = qsv[qg] * ksv;
         const float f = LAST ? a.sm : a.sm * dq;
+        if constexpr (!LAST) {
+          // f > 0, so fmaf(b, f, -offset) is monotone in b: the maximum is taken on the
+          // scores (on the integers for INT8 accumulators), then shifted once
+          if constexpr (QF == 0) {
+            int im = S[qg][0][0];
 #pragma unroll
-        for (int j = 0; j < 8; ++j)
+            for (int j = 0; j < 8; ++j)
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            float b = static_cast<float>(S[qg][j][r]);
-            if constexpr (LAST) {
+              for (int r = 0; r < 4; ++r) {
+                im = im > S[qg][j][r] ? im : S[qg][j][r];
+                bs[j][r] = acc_float(S[qg][j][r]);
+              }
+            tmax = __builtin_fmaf(acc_float(im), f, -kFp8Offset);
+          } else {
+            float bm = -INFINITY;
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+#pragma unroll
+              for (int r = 0; r < 4; ++r) {
+                bs[j][r] = S[qg][j][r];
+                bm = vmax(bm, bs[j][r]);
+              }
+            tmax = __builtin_fmaf(bm, f, -kFp8Offset);
+          }
+          // f = +inf (an extreme sm_scale) with a zero maximum gives NaN where the maximum of
+          // the shifted terms (each -inf or NaN) is -inf
+          if (tmax != tmax) tmax = -INFINITY;
+        } else {
+          tmax = -INFINITY;
+#pragma unroll
+          for (int j = 0; j < 8; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              float b;
+              if constexpr (QF == 1) b = S[qg][j][r];
+              else b = acc_float(S[qg][j][r]);
               const int64_t key = t * kTile + 16 * j + 8 * (r >> 1) + 2 * G + (r & 1);
               b = key < a.Nk ? b * dq : -INFINITY;
+              bs[j][r] = b;
+              tmax = fmaxf(tmax, __builtin_fmaf(b, f, -kFp8Offset));
             }
-            bs[j][r] = b;
-            tmax = fmaxf(tmax, __builtin_fmaf(b, f, -kFp8Offset));
-          }
+        }
         const float mn = running_max(m[qg], tmax);
         mold[qg] = m[qg];
         m[qg] = mn;
-        float ls = 0.0f;
+        // Bytes of the +-2 ulp neighbours of every probability; an E4M3 midpoint within two
+        // ulps (the neighbours disagree, a few lanes per million) takes the binary64 recheck.
+        // At D128 the recheck is one branch per tile (a lane that missed redoes its tile from
+        // the scores, which stay live), so the loop stays one block that the MFMAs
+        // interleave with; D64's three waves per SIMD have no registers for that and branch
+        // per four probabilities.
+        float ls = -0.0f;  // -0 + p = p: the first addition folds away
+        if constexpr (D == 128) {
+          uint32_t miss = 0;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          float xs[4], pr[4];
+          for (int j = 0; j < 8; ++j) {
+            float pr[4];
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            xs[r] = __builtin_fmaf(bs[j][r], f, -mn);
-            pr[r] = __builtin_amdgcn_exp2f(xs[r]);
+            for (int r = 0; r < 4; ++r) pr[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(bs[j][r], f, -mn));
+            uint32_t lo, hi;
+            fp8_exp2_bounds<LAST, true>(pr, lo, hi);
+            P[qg][j] = static_cast<int>(lo);
+            miss |= lo ^ hi;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) ls += pr[r];
           }
-          P[qg][j] = static_cast<int>(fp8_exp2_word<LAST>(xs, pr));
+          if (__builtin_expect(miss != 0, 0)) {
+            ls = -0.0f;
 #pragma unroll
-          for (int r = 0; r < 4; ++r) ls += pr[r];
+            for (int j = 0; j < 8; ++j) {
+              float xs[4], pr[4];
+#pragma unroll
+              for (int r = 0; r < 4; ++r) {
+                float b = bs[j][r];
+                asm volatile("" : "+v"(b));  // recomputed here, not kept live from the loop above
+                xs[r] = __builtin_fmaf(b, f, -mn);
+                pr[r] = __builtin_amdgcn_exp2f(xs[r]);
+              }
+              P[qg][j] = static_cast<int>(fp8_exp2_word<LAST>(xs, pr));
+#pragma unroll
+              for (int r = 0; r < 4; ++r) ls += pr[r];
+            }
+          }
+        } else {
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            float xs[4], pr[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              xs[r] = __builtin_fmaf(bs[j][r], f, -mn);
+              pr[r] = __builtin_amdgcn_exp2f(xs[r]);
+            }
+            P[qg][j] = static_cast<int>(fp8_exp2_word<LAST>(xs, pr));
+#pragma unroll
+            for (int r = 0; r < 4; ++r) ls += pr[r];
+          }
         }
         tmass[qg] = row_sum(ls);
       }

@@ -111,11 +111,13 @@ __device__ inline uint32_t e4m3_sat(float x) {
 // SAT = true forms the lower neighbours with a saturating subtraction instead, for tiles
 // with masked keys (p = exp2(-inf) = 0). Reference: the probability byte of
 // sal/sageattention_local/vc_reference.py:68-75 and sal/csrc/qattn/attn_utils.cuh:355-455.
-// Binary64 exp2 rounded once to binary32: one out-of-line copy for the rare recheck.
+// fp8_exp2_bounds gives the bytes of both neighbour sets (lo, hi); fp8_exp2_word resolves a
+// disagreement. Binary64 exp2 rounded once to binary32: one out-of-line copy for the rare
+// recheck.
 __device__ __noinline__ inline float exp2_via_f64(float x) { return static_cast<float>(exp2(static_cast<double>(x))); }
 
-template <bool SAT = false>
-__device__ inline uint32_t fp8_exp2_word(const float (&x)[4], float (&p)[4]) {
+template <bool SAT = false, bool REUSE = false>
+__device__ inline void fp8_exp2_bounds(const float (&p)[4], uint32_t& lo, uint32_t& hi) {
   constexpr uint64_t kTwoUlps = 0x0000000200000002ull;
   float dn[4], up[4];
 #pragma unroll
@@ -134,10 +136,21 @@ __device__ inline uint32_t fp8_exp2_word(const float (&x)[4], float (&p)[4]) {
       dn[2 * h + 1] = __uint_as_float(static_cast<uint32_t>(d >> 32));
     }
   }
-  uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(dn[0], dn[1], 0, false));
+  // REUSE: the first conversion of each word writes its low half over an input that dies
+  // there (the high half is written next) instead of a zeroed register; one move less per
+  // word, at the price of a longer-lived input where registers are short
+  lo = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(dn[0], dn[1], REUSE ? __float_as_int(dn[0]) : 0, false));
   lo = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(dn[2], dn[3], static_cast<int>(lo), true));
-  uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(up[0], up[1], 0, false));
+  hi = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(up[0], up[1], REUSE ? __float_as_int(up[0]) : 0, false));
   hi = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(up[2], up[3], static_cast<int>(hi), true));
+}
+
+// The four bytes themselves: the lower neighbours' bytes when both neighbours agree, else the
+// binary64 recheck.
+template <bool SAT = false>
+__device__ inline uint32_t fp8_exp2_word(const float (&x)[4], float (&p)[4]) {
+  uint32_t lo, hi;
+  fp8_exp2_bounds<SAT>(p, lo, hi);
   if (__builtin_expect(lo != hi, 0)) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) p[r] = exp2_via_f64(x[r]);

@@ -178,10 +178,8 @@ __global__ __launch_bounds__(kThreads) void tile_stats_kernel(
 // RAW (FP8 block path, vc27): km = RN_f32(sum / n), written to km_f32 and, as binary32,
 // to the caller's km_out.
 template <int DT, bool RAW = false>
-__global__ void k_mean_kernel(const double* sums, int64_t tiles, int64_t n, int D, float* km_f32,
-                              void* km_out) {
-  const int64_t bh = blockIdx.x;
-  const int ch = threadIdx.x;
+__device__ inline void k_mean_body(const double* sums, int64_t tiles, int64_t n, int D, float* km_f32,
+                                   void* km_out, int64_t bh, int ch) {
   const double* col = sums + bh * tiles * D + ch;
   // Sequential fp64 sum over tiles (the contract's order); the loads of a batch
   // of tiles are issued together so that their latencies overlap.
@@ -205,6 +203,12 @@ __global__ void k_mean_kernel(const double* sums, int64_t tiles, int64_t n, int 
     km_f32[bh * D + ch] = in_to_f32<DT>(bits);
     if (km_out) static_cast<uint16_t*>(km_out)[bh * D + ch] = static_cast<uint16_t>(bits);
   }
+}
+
+template <int DT, bool RAW = false>
+__global__ void k_mean_kernel(const double* sums, int64_t tiles, int64_t n, int D, float* km_f32,
+                              void* km_out) {
+  k_mean_body<DT, RAW>(sums, tiles, n, D, km_f32, km_out, blockIdx.x, threadIdx.x);
 }
 
 // grid (B*H), D threads. Smoothing off: vs = RN(amax/448), recip = RN(448/amax)
@@ -261,12 +265,29 @@ __global__ void v_scale_kernel(const float* a0, const float* a1, int64_t tiles, 
 // group is 32 lanes (16 per row) of one wave; 4 passes of 8 groups.
 // ROT: the rows are rotated by the normalized Hadamard transform (hadamard_row, norm =
 // RN_f32(1/sqrt(D))) in binary32 before the group maximum and the codes.
-template <int DT, int D, bool ROT = false>
+// KM (the INT8 Q/K path): blocks (0, bh) instead compute head bh's K mean (k_mean_body, from
+// the K tile sums of the statistics launch before), so that this latency-bound walk runs
+// beside the streaming Q blocks instead of in a launch of its own; the Q blocks are
+// (1 + blk, bh). The K quantization launch that follows reads the mean.
+struct KMeanArgs {
+  const double* sums;
+  int64_t tiles, n;
+  float* km;
+  void* km_out;
+};
+
+template <int DT, int D, bool ROT = false, bool KM = false>
 __global__ __launch_bounds__(kThreads) void quant_q_kernel(const void* q, int64_t H, int64_t n,
                                                            int64_t sb, int64_t sh, int64_t sn,
-                                                           int8_t* q8, float* qs, float norm) {
+                                                           int8_t* q8, float* qs, float norm, KMeanArgs kma) {
   constexpr int CPT = D / 16;
-  const int64_t blk = blockIdx.x, bh = blockIdx.y;
+  if constexpr (KM) {
+    if (blockIdx.x == 0) {
+      if (threadIdx.x < D) k_mean_body<DT>(kma.sums, kma.tiles, kma.n, D, kma.km, kma.km_out, blockIdx.y, threadIdx.x);
+      return;
+    }
+  }
+  const int64_t blk = KM ? blockIdx.x - 1 : blockIdx.x, bh = blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, c = lane & 15, sel = (lane >> 4) & 1;
   const uint16_t* base = head_base(q, bh, H, sb, sh);
   const int64_t qs_len = (n + 63) / 64 * 32;
@@ -709,19 +730,20 @@ int prepare_qk_int8(const void* q, const void* k, int dtype, int64_t B, int64_t 
   float* km = reinterpret_cast<float*>(ws + align_up(sizeof(double) * BH * tiles * D));
   hipStream_t st = static_cast<hipStream_t>(stream);
   const float norm = static_cast<float>(1.0 / std::sqrt(static_cast<double>(D)));
+  // K statistics, then the Q quantization with the K mean in its first blocks, then the K
+  // quantization.
+  const KMeanArgs kma{ksum, tiles, Nk, km, km_out};
   return dispatch(dtype, D, [&](auto dt, auto dd) -> int {
     constexpr int DT = decltype(dt)::value, DD = decltype(dd)::value;
-    if (rotate)
-      quant_q_kernel<DT, DD, true><<<dim3(cdiv(Nq, 64), BH), kThreads, 0, st>>>(q, H, Nq, q_sb, q_sh, q_sn, q8, qs,
-                                                                              norm);
-    else
-      quant_q_kernel<DT, DD><<<dim3(cdiv(Nq, 64), BH), kThreads, 0, st>>>(q, H, Nq, q_sb, q_sh, q_sn, q8, qs, norm);
-    VCX_LAUNCHED("quant_q_kernel");
     tile_stats_kernel<DT, DD, kKSum><<<dim3(tiles, BH), kThreads, 0, st>>>(k, H, Nk, k_sb, k_sh, k_sn, perm,
                                                                           ksum, nullptr, nullptr);
     VCX_LAUNCHED("tile_stats_kernel<K>");
-    k_mean_kernel<DT><<<dim3(BH), DD, 0, st>>>(ksum, tiles, Nk, DD, km, km_out);
-    VCX_LAUNCHED("k_mean_kernel");
+    const dim3 qgrid(cdiv(Nq, 64) + 1, BH);
+    if (rotate)
+      quant_q_kernel<DT, DD, true, true><<<qgrid, kThreads, 0, st>>>(q, H, Nq, q_sb, q_sh, q_sn, q8, qs, norm, kma);
+    else
+      quant_q_kernel<DT, DD, false, true><<<qgrid, kThreads, 0, st>>>(q, H, Nq, q_sb, q_sh, q_sn, q8, qs, norm, kma);
+    VCX_LAUNCHED("quant_q_kernel");
     if (rotate)
       quant_k_kernel<DT, DD, true><<<dim3(tiles, BH), kThreads, 0, st>>>(k, H, Nk, k_sb, k_sh, k_sn, perm, km, k8,
                                                                         ks, norm);

@@ -37,6 +37,14 @@ PEAK_HBM_GBS = 8000.0   # MI355X HBM3E, GB/s (published)
 # profiles/attn_kernel_fp8_main_hbm_bytes.txt). Counters cannot be read from inside this
 # process, so the figure is keyed by QK format and configuration and null where unmeasured.
 MEASURED_TRAFFIC_BYTES = {("int8", "main"): 3.088e9, ("fp8", "main"): 3.133e9}
+# VALU instructions per wave and 128-key tile of the fused kernel ((SQ_INSTS_VALU -
+# SQ_INSTS_MFMA) / (waves x tiles), rocprofv3 --pmc; profiles/attn_kernel_main_counters.txt,
+# profiles/attn_kernel_d64_counters.txt), and the best issue rate measured for the kernel's
+# per-score VALU chain with two waves per SIMD (3.0 cycles per instruction per SIMD,
+# register-only microbenchmark). Together they give the VALU issue bound of a launch.
+MEASURED_VALU_PER_WAVE_TILE = {("int8", "main"): 281.2, ("int8", "d64"): 397.5}
+VALU_CYCLES_PER_INSTR = 3.0
+SIMDS = 1024            # 256 CUs x 4 SIMDs
 
 CONFIGS = {
     # name: (B, H, N, D, kind, v_smooth, description)
@@ -310,6 +318,18 @@ def main():
                            "method": "s_memtime / s_memrealtime ticks of 8 one-wave probe blocks (one per XCD) on a "
                                      "second stream over the first 60 % of fused launches 2-5 of an untimed burst "
                                      "that follows the timed steps (vcx_clock_probe)"}
+    valu = MEASURED_VALU_PER_WAVE_TILE.get((args.qk, args.config))
+    if valu is not None:
+        # one wave per 32 query rows, every wave walks every key tile
+        instr = valu * (B * H * tiles * 4) * tiles
+        ghz = result["clock"]["engine_ghz_under_load"] if "clock" in result else PEAK_CLOCK_GHZ
+        bound_ms = instr * VALU_CYCLES_PER_INSTR / SIMDS / (ghz * 1e9) * 1e3
+        result["roofline_valu"] = {"bound": "valu", "instructions_per_launch": instr,
+                                   "cycles_per_instruction": VALU_CYCLES_PER_INSTR, "clock_ghz": ghz,
+                                   "bound_ms": round(bound_ms, 4), "frac": round(bound_ms / mean_kernel_ms, 4),
+                                   "note": "VALU issue bound of the fused kernel: measured VALU instructions "
+                                           "per wave-tile x waves x tiles at the best measured two-wave issue "
+                                           "rate; frac = bound / mean kernel time"}
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(qc, kc, vc_, smooth, args.cpu_rows, 30.0, args.qk,
                                               args.qk_hadamard)

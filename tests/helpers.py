@@ -67,15 +67,21 @@ def cosine(a, b):
 def output_bound(actual, expected):
     """Elementwise tolerance of the bf16/fp16 output vs the fp32-simulated oracle.
 
-    |actual - expected| <= 2^-7 * |expected| + 2e-3 * max|expected| + 1e-6:
-    one output ulp (bf16 ulp <= 2^-7 relative) plus the FP8 MFMA accumulation
-    error (chunks truncated ~2^-13 below their largest product) relative to the
-    row scale.
+    |actual - expected| <= 2^-8 * |expected| + 1e-3 * max|expected| + 1e-6:
+    half an output ulp (bf16: <= 2^-8 relative; fp16 outputs are held to the same
+    term) plus the accumulation error relative to the row scale. Two sources: the
+    FP8 MFMA truncates its partial sums (~2^-13 below the largest product), so the
+    fp32 accumulators and the row mass are not exact sums; and with block values the
+    deferred mean restore multiplies by weights rounded to fp16 (2^-11 relative on the
+    mean term). Measured beyond the half ulp, as a fraction of the row's largest
+    output: at most 6.4e-5 without block values ([1,2,4096..37741,64/128], N(0,1) and
+    Student-t, both probability paths, bf16 and fp16) and 5.2e-4 with them
+    ([1,2,32760,64] and [1,2,75482,128] at full length); the bound allows 1e-3.
     """
     e = np.asarray(expected, np.float64)
     a = np.asarray(actual, np.float64)
     scale = np.abs(e).max(axis=-1, keepdims=True)
-    bound = 2.0 ** -7 * np.abs(e) + 2e-3 * scale + 1e-6
+    bound = 2.0 ** -8 * np.abs(e) + 1e-3 * scale + 1e-6
     return np.abs(a - e), bound
 
 

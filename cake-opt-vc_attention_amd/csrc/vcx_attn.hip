@@ -632,7 +632,8 @@ struct Wave {
       // G = c / 4 keeps the row's mass in slot c % 4 (the MFMA's k = c). At the chunk's
       // end (or the last tile) O^T[ch][row] += sum_k mean_k[ch] * w_k[row] over the
       // chunk, as v_mfma_f32_16x16x16f16 (A: means from the ring, exact in fp16, or with
-      // per-block scales RN_f16(vs_k[ch] * mean_k[ch]); B: the weights rounded to fp16).
+      // per-block scales RN_f16(vs_k[ch] * mean_k[ch]); B: the weights as fp16 hi and lo
+      // parts).
       // Slots of tiles past the last hold w = 0.
       const int c = static_cast<int>(t & (kChunk - 1));
 #pragma unroll
@@ -643,15 +644,18 @@ struct Wave {
     }
   }
 
-  // O += means (x) weights over the chunk that starts at tile `base` (VM 1, 2).
+  // O += means (x) weights over the chunk that starts at tile `base` (VM 1, 2). Each weight
+  // goes in as two fp16 parts, hi = RN_f16(w) and lo = RN_f16(w - hi) (w - hi is exact in
+  // binary32), so the mean term carries about 22 bits of the weight instead of 11.
   __device__ inline void flush_means(const uint8_t* ring, int64_t base) {
     typedef _Float16 v4h __attribute__((ext_vector_type(4)));
-    v4h b[2];
+    v4h b[2], bl[2];
 #pragma unroll
     for (int qg = 0; qg < 2; ++qg) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         b[qg][j] = static_cast<_Float16>(wts[qg][j]);
+        bl[qg][j] = static_cast<_Float16>(wts[qg][j] - static_cast<float>(b[qg][j]));
         wts[qg][j] = 0.0f;
       }
     }
@@ -671,7 +675,10 @@ struct Wave {
         }
       }
 #pragma unroll
-      for (int qg = 0; qg < 2; ++qg) O[qg][cb] = __builtin_amdgcn_mfma_f32_16x16x16f16(av, b[qg], O[qg][cb], 0, 0, 0);
+      for (int qg = 0; qg < 2; ++qg) {
+        O[qg][cb] = __builtin_amdgcn_mfma_f32_16x16x16f16(av, bl[qg], O[qg][cb], 0, 0, 0);
+        O[qg][cb] = __builtin_amdgcn_mfma_f32_16x16x16f16(av, b[qg], O[qg][cb], 0, 0, 0);
+      }
     }
   }
   const uint8_t* ring = nullptr;

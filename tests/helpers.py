@@ -67,21 +67,21 @@ def cosine(a, b):
 def output_bound(actual, expected):
     """Elementwise tolerance of the bf16/fp16 output vs the fp32-simulated oracle.
 
-    |actual - expected| <= 2^-8 * |expected| + 1e-3 * max|expected| + 1e-6:
+    |actual - expected| <= 2^-8 * |expected| + 2.5e-4 * max|expected| + 1e-6:
     half an output ulp (bf16: <= 2^-8 relative; fp16 outputs are held to the same
-    term) plus the accumulation error relative to the row scale. Two sources: the
-    FP8 MFMA truncates its partial sums (~2^-13 below the largest product), so the
-    fp32 accumulators and the row mass are not exact sums; and with block values the
-    deferred mean restore multiplies by weights rounded to fp16 (2^-11 relative on the
-    mean term). Measured beyond the half ulp, as a fraction of the row's largest
-    output: at most 6.4e-5 without block values ([1,2,4096..37741,64/128], N(0,1) and
-    Student-t, both probability paths, bf16 and fp16) and 5.2e-4 with them
-    ([1,2,32760,64] and [1,2,75482,128] at full length); the bound allows 1e-3.
+    term) plus the accumulation error relative to the row scale: the FP8 MFMA
+    truncates its partial sums (~2^-13 below the largest product), so the fp32
+    accumulators and the row mass are not exact sums (the deferred mean restore's
+    weights enter as fp16 hi + lo parts, about 22 bits). Measured beyond the half ulp,
+    as a fraction of the row's largest output: at most 6.4e-5 on [1,2,4096..37741,
+    64/128] inputs (N(0,1), outlier K / clustered V with smoothing, Student-t, both
+    probability paths, bf16 and fp16) and 1.0e-4 on [1,2,75482,128] with smoothing;
+    the bound allows 2.5e-4.
     """
     e = np.asarray(expected, np.float64)
     a = np.asarray(actual, np.float64)
     scale = np.abs(e).max(axis=-1, keepdims=True)
-    bound = 2.0 ** -8 * np.abs(e) + 1e-3 * scale + 1e-6
+    bound = 2.0 ** -8 * np.abs(e) + 2.5e-4 * scale + 1e-6
     return np.abs(a - e), bound
 
 

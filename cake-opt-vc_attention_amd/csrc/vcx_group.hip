@@ -66,12 +66,13 @@ __global__ void grp_init_kernel(const void* v, int64_t H, int64_t sb, int64_t sh
 // an LDS histogram.
 // The tile is staged through LDS with coalesced loads; each thread then reads its token's
 // row 16 bytes at a time and runs the distance chains of 8 clusters side by side (d
-// outermost), chunk after chunk of 8 centers; the fp64 centers are wave-uniform and come
-// through scalar loads.
+// outermost), chunk after chunk of 8 centers, in binary32 and, where that does not settle
+// the argmin, in fp64; the centers are wave-uniform and come through scalar loads.
 template <int DT, int D, bool STATS, bool WIDE, bool GENERAL>
 __global__ __launch_bounds__(kGroupThreads) void grp_assign_kernel(
     const void* v, int64_t H, int64_t n, int64_t sb, int64_t sh, int64_t sn, int count, int CS,
-    const double* __restrict__ centers64, int32_t* labels, double* psum, int32_t* pcnt) {
+    const float* __restrict__ centers32, const double* __restrict__ centers64, int32_t* labels, double* psum,
+    int32_t* pcnt) {
   constexpr int kStride = D + 8;  // 16-bit elements per staged row (16-byte aligned rows)
   __shared__ __attribute__((aligned(16))) uint16_t xs[kTile * kStride];
   const int64_t tile = blockIdx.x, bh = blockIdx.y, tiles = gridDim.x;
@@ -116,7 +117,55 @@ __global__ __launch_bounds__(kGroupThreads) void grp_assign_kernel(
   __syncthreads();
   const int64_t tok = tile * kTile + tid;
   int best = 0;
+  // The label is the argmin of the fp64 distances. The same distances are first formed in
+  // binary32 (x - c rounded, then a fused multiply-add chain): every term is non-negative,
+  // so each binary32 distance lies within (D + 2) * 2^-24 relative (plus a subnormal-sized
+  // absolute term) of the exact one. When the second smallest exceeds the smallest by more
+  // than twice that bound, the exact and the fp64 distances order the same way and the
+  // binary32 argmin is the label; otherwise (ties, near ties, overflow) the lane takes the
+  // fp64 chains below.
+  bool sure = false;
   if (tok < n) {
+    float b32 = INFINITY, s32 = INFINITY;
+    for (int c0 = 0; c0 < count; c0 += 8) {
+      const float* cen = centers32 + (bh * CS + c0) * D;  // wave-uniform: scalar loads
+      float acc[8];
+#pragma unroll
+      for (int c = 0; c < 8; ++c) acc[c] = 0.0f;
+#pragma unroll 2
+      for (int i = 0; i < D / 8; ++i) {
+        const uint4 q = *reinterpret_cast<const uint4*>(&xs[tid * kStride + 8 * i]);
+        const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const int d = 8 * i + 2 * k;
+          const float x0 = in_to_f32<DT>(w[k] & 0xffffu), x1 = in_to_f32<DT>(w[k] >> 16);
+#pragma unroll
+          for (int c = 0; c < 8; ++c) {
+            const float d0 = __fsub_rn(x0, cen[c * D + d]);
+            acc[c] = __fmaf_rn(d0, d0, acc[c]);
+            const float d1 = __fsub_rn(x1, cen[c * D + d + 1]);
+            acc[c] = __fmaf_rn(d1, d1, acc[c]);
+          }
+        }
+      }
+#pragma unroll
+      for (int c = 0; c < 8; ++c)
+        if (c0 + c < count) {
+          if (acc[c] < b32) {  // ties keep the lowest id (and make the order unsure)
+            s32 = b32;
+            b32 = acc[c];
+            best = c0 + c;
+          } else if (acc[c] < s32) {
+            s32 = acc[c];
+          }
+        }
+    }
+    constexpr float kOrder = 1.0f + 4.0e-5f;  // > (1 + e) / (1 - e), e = 130 * 2^-24
+    sure = s32 > b32 * kOrder + 1.0e-37f;       // false for NaN or an infinite b32
+  }
+  if (tok < n && !sure) {
+    best = 0;
     double best_d = 0.0;
     for (int c0 = 0; c0 < count; c0 += 8) {
       const double* cen = centers64 + (bh * CS + c0) * D;  // wave-uniform: scalar loads
@@ -149,8 +198,8 @@ __global__ __launch_bounds__(kGroupThreads) void grp_assign_kernel(
           best = c0 + c;
         }
     }
-    labels[bh * n + tok] = best;
   }
+  if (tok < n) labels[bh * n + tok] = best;
   const int64_t meta = (bh * tiles + tile) * CS;
   if constexpr (GENERAL) {
     if (tok < n) atomicAdd(&hist[best], 1);
@@ -447,10 +496,10 @@ extern "C" int vcx_group_values(const void* v, int dtype, int64_t B, int64_t H, 
       constexpr bool ST = decltype(stats)::value, GE = decltype(gen)::value;
       if (wide)
         grp_assign_kernel<DT, DD, ST, true, GE><<<dim3(tiles, BH), kGroupThreads, 0, st>>>(
-            v, H, N, v_sb, v_sh, v_sn, count, CS, ws.centers64, lab, psum, ws.pcnt);
+            v, H, N, v_sb, v_sh, v_sn, count, CS, ws.centers, ws.centers64, lab, psum, ws.pcnt);
       else
         grp_assign_kernel<DT, DD, ST, false, GE><<<dim3(tiles, BH), kGroupThreads, 0, st>>>(
-            v, H, N, v_sb, v_sh, v_sn, count, CS, ws.centers64, lab, psum, ws.pcnt);
+            v, H, N, v_sb, v_sh, v_sn, count, CS, ws.centers, ws.centers64, lab, psum, ws.pcnt);
     };
     auto sort = [&]() -> int {
       grp_offsets_kernel<<<dim3(BH), offset_threads, 0, st>>>(ws.pcnt, tiles, count, CS, ws.offsets);

@@ -168,6 +168,51 @@ def test_grouping_bit_exact(dim, dtype, n, clusters, iterations):
     np.testing.assert_array_equal(perm.cpu().numpy(), eperm)
 
 
+def _near_tie_values(dim, dtype, n=1024, seed=0):
+    """[1,2,n,dim] V whose tokens sit at or near the bisector of the two initial centers
+    (V[0] = -e_0 + w, V[n-1] = +e_0 + w, with the same random tail w in the other channels):
+    token t has channel 0 = s_t * 2^-k (k = 9..24, s_t in {-1, 0, +1}) and the tail w plus
+    small noise on a few tokens. Its two distances differ by 4 * channel 0, i.e. down to a
+    relative 2^-24 / (1 + |w|^2), far inside the binary32 error of the distance sums, so
+    the kernel's binary32 pass must leave these tokens to the fp64 chains; s_t = 0 gives exact
+    ties (lowest id)."""
+    g = torch.Generator().manual_seed(seed)
+    w = torch.randn(2, dim, generator=g).to(dtype).float()
+    w[:, 0] = 0
+    v = w[:, None, :].repeat(1, n, 1)
+    t = torch.arange(n)
+    k = 9 + t % 16
+    sgn = (t % 3 - 1).float()
+    v[:, :, 0] = sgn[None, :] * torch.pow(2.0, -k.float())[None, :]
+    noisy = t % 7 == 0
+    v[:, noisy, 1:] += 0.5 * torch.randn(2, int(noisy.sum()), dim - 1, generator=g)
+    v[:, 0, :] = w
+    v[:, 0, 0] = -1.0
+    v[:, n - 1, :] = w
+    v[:, n - 1, 0] = 1.0
+    return v[None].to(dtype)
+
+
+@pytest.mark.parametrize("dim", [64, 128])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("legacy", [False, True])
+def test_grouping_near_ties_take_the_fp64_chains(dim, dtype, legacy):
+    # Labels are the fp64 argmin (ties to the lowest id); a binary32 pass decides only when
+    # its order is certain. Tokens on and next to the bisector of the two centers must get
+    # the oracle's labels exactly, through both schedules.
+    _print_case("grouping near ties", dim, dtype, legacy)
+    v = _near_tie_values(dim, dtype)
+    perm, labels, centers = vcx.group_values(v.to(DEV), 2, 1, debug=True, legacy=legacy)
+    eperm, elabels, ecenters = o.group_values(bits(v), 2, 1, dtype_name(dtype))
+    np.testing.assert_array_equal(labels.cpu().numpy(), elabels)
+    np.testing.assert_array_equal(perm.cpu().numpy(), eperm)
+    # both labels occur, and exact ties went to cluster 0
+    assert 0 < elabels.mean() < 1
+    n = v.shape[2]
+    tie = (np.arange(n) % 3 == 1) & (np.arange(n) % 7 != 0) & (np.arange(n) > 0) & (np.arange(n) < n - 1)
+    assert np.all(elabels[..., tie] == 0)
+
+
 @pytest.mark.parametrize("dim", [64, 128])
 @pytest.mark.parametrize("n,clusters,iterations", [(2049, 16, 2), (1000, 64, 3), (600, 256, 2), (100, 256, 2),
                                                    (129, 9, 2), (37741, 32, 2)])

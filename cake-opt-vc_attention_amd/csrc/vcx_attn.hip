@@ -215,12 +215,19 @@ __device__ inline float vmax3(float a, float b, float c) {
 // Row reductions over the four lane groups that hold one query row: gfx950
 // permlane swaps give each lane the values of lanes l^16 and l^32 without an LDS
 // round trip. Every lane of the row ends with the same value (the adds commute).
-// running_max returns max(m, row maximum of x).
-__device__ inline float running_max(float m, float x) {
-  const auto x16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  x = vmax(__uint_as_float(x16[0]), __uint_as_float(x16[1]));
-  const auto x32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return vmax3(m, __uint_as_float(x32[0]), __uint_as_float(x32[1]));
+// running_max2 gives mn[g] = max(m[g], row maximum of x[g]) for both row groups of a wave
+// in one reduction. With the wave's 16-lane rows R0..R3 (lane group G = row RG): the 16-lane
+// swap of x[0] against x[1] and a maximum leave (x0 of R0|R1, x1 of R0|R1, x0 of R2|R3,
+// x1 of R2|R3) in R0..R3; the 32-lane swap and a maximum complete each group's maximum
+// (R0, R2: group 0; R1, R3: group 1); a last 16-lane swap hands every lane both.
+__device__ inline void running_max2(const float (&m)[2], const float (&x)[2], float (&mn)[2]) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x[0]), __float_as_uint(x[1]), false, false);
+  const float c = vmax(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(c), __float_as_uint(c), false, false);
+  const float d = vmax(__uint_as_float(b[0]), __uint_as_float(b[1]));
+  const auto e = __builtin_amdgcn_permlane16_swap(__float_as_uint(d), __float_as_uint(d), false, false);
+  mn[0] = vmax(m[0], __uint_as_float(e[0]));
+  mn[1] = vmax(m[1], __uint_as_float(e[1]));
 }
 
 // Whether `pred` holds on some active lane (a scalar test of the lane mask).
@@ -240,6 +247,14 @@ constexpr float kFp8Offset = 8.807f;
 // they read as the float 12582912 + acc, so float(acc) is one exact subtraction.
 constexpr int kBias = 0x4B400000;
 constexpr float kBiasF = 12582912.0f;
+
+// Mask of the active lanes whose x is a positive normal number: one v_cmp_class_f32 into an
+// SGPR pair (the ballot of __builtin_amdgcn_classf adds a select and a compare).
+__device__ inline uint64_t pos_normal_lanes(float x) {
+  uint64_t r;
+  asm("v_cmp_class_f32_e64 %0, %1, %2" : "=s"(r) : "v"(x), "s"(1 << 8));
+  return r;
+}
 
 // Score of accumulator element r: FP8 scores are floats already; the folded path's
 // INT8 accumulators carry the kBias offset.
@@ -276,8 +291,61 @@ struct Wave {
   float wts[2][4];  // VM 1, 2: pending mean weights of chunk tiles 4G..4G+3 (row li)
   int koff[DS], voff[2];
   v8i ones;  // all-ones E4M3 A operand of the row-mass MFMA, kept in registers
+  v4i bacc;  // kBias in every element: the initial QK accumulator of the biased paths
+  // Folded encode (INT8 QK): the per-tile fold conditions are known to hold on every tile
+  // but the last (set once per wave by fold_precheck; wave-uniform)
+  int fold_ok;
   int G, li;
   int64_t bh_;
+
+  // The folded encode's conditions on a tile before the last (scale = RN(sm * RN(qs * ks))
+  // and gain = RN(scale * A) positive normal, |m'| <= 128) hold on every such tile when
+  //  - RN(sm * RN(qs * ks)) is a positive normal at the head's smallest and largest K scale
+  //    and RN(scale * A) is one at the largest (RN and multiplication by positive factors
+  //    are monotone, so every tile's scale and gain lie between these; the K scales are
+  //    compared as bit patterns, which orders positive floats and sends zero, negative,
+  //    NaN and infinite scales to an end that fails), and
+  //  - |logit| <= RN(128 * sum|q8| * scale_hi) <= 128 for the lane's row: every score's
+  //    |acc| <= 128 * sum|q8|, so every logit, each tile's maximum and from the first tile on
+  //    the running maximum stay within it.
+  // fold_ok is the AND over the wave; when it fails the tiles test the conditions.
+  __device__ inline void fold_precheck(const AttnArgs& a, int lane) {
+    const uint32_t* kb = reinterpret_cast<const uint32_t*>(a.ks) + bh_ * a.tiles * 4;
+    uint32_t kmin = 0xffffffffu, kmax = 0u;
+    for (int64_t i = lane; i < a.tiles * 4; i += 64) {
+      const uint32_t u = kb[i];
+      kmin = u < kmin ? u : kmin;
+      kmax = u > kmax ? u : kmax;
+    }
+#pragma unroll
+    for (int sh = 32; sh >= 1; sh >>= 1) {
+      const uint32_t lo = __shfl_xor(kmin, sh), hi = __shfl_xor(kmax, sh);
+      kmin = lo < kmin ? lo : kmin;
+      kmax = hi > kmax ? hi : kmax;
+    }
+    uint64_t ok = __builtin_amdgcn_read_exec();
+#pragma unroll
+    for (int qg = 0; qg < 2; ++qg) {
+      int asum = 0;
+#pragma unroll
+      for (int ds = 0; ds < DS; ++ds)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+#pragma unroll
+          for (int by = 0; by < 4; ++by) {
+            const int x = static_cast<int8_t>((static_cast<uint32_t>(qf[qg][ds][e]) >> (8 * by)) & 0xffu);
+            asum += x < 0 ? -x : x;
+          }
+      asum += __shfl_xor(asum, 16);
+      asum += __shfl_xor(asum, 32);
+      const float s_lo = a.sm * (qsv[qg] * __uint_as_float(kmin));
+      const float s_hi = a.sm * (qsv[qg] * __uint_as_float(kmax));
+      const float bound = static_cast<float>(128 * asum) * s_hi;
+      ok &= pos_normal_lanes(s_lo) & pos_normal_lanes(s_hi) & pos_normal_lanes(s_hi * kExpA) &
+            __builtin_amdgcn_ballot_w64(bound <= 128.0f);
+    }
+    fold_ok = __builtin_amdgcn_readfirstlane(ok == __builtin_amdgcn_read_exec() ? 1 : 0);
+  }
 
   __device__ inline v8i load_v(const uint8_t* lv, int cb) const {
     const v4i lo = *reinterpret_cast<const v4i*>(lv + cb * 16 * kTile + voff[0]);
@@ -315,7 +383,7 @@ struct Wave {
                                  : v8i{qf[qg][0][0], qf[qg][0][1], qf[qg][0][2], qf[qg][0][3], 0, 0, 0, 0};
           S[qg][j] = mfma_fp8(ka, qb, v4f{0.0f, 0.0f, 0.0f, 0.0f});
         } else {
-          v4i acc = IB ? v4i{kBias, kBias, kBias, kBias} : v4i{0, 0, 0, 0};
+          v4i acc = IB ? bacc : v4i{0, 0, 0, 0};
 #pragma unroll
           for (int ds = 0; ds < DS; ++ds) acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(kf[j][ds], qf[qg][ds], acc, 0, 0, 0);
           S[qg][j] = acc;
@@ -325,20 +393,21 @@ struct Wave {
     }
 
     // ---- logits, online max, P bytes (ExpCast codes, or E4M3 probabilities on the control path)
+    // Phase 1, per row group: the values the encode reads and the tile's row maximum in this
+    // lane's keys. Phase 2: both row groups' running maxima in one cross-lane reduction.
+    // Phase 3, per row group: the bytes.
     v8i P[2];
     float mold[2], tmass[2];
+    // PM 2 and 0: float(acc) (last tile: float(acc) * dq, or -inf past Nk); PM 1: the logits
+    float bs[2][8][4];
+    // tmax: this lane's maximum; scl: PM 2 the logit scale, PM 0 the log2-domain factor
+    float tmax[2], scl[2];
 #pragma unroll
     for (int qg = 0; qg < 2; ++qg) {
+      const float dq = qsv[qg] * ksv;
       if constexpr (PM == 2) {
-        // Folded ExpCast encode (the reference's default kernel modes without block
-        // values, sal/csrc/vc/vc_math.cuh:16-111): code = RNE(fmaf(base, gain, bias)) with
-        // gain = RN(scale * A) and bias = fmaf(-m', A, B), unless some row of this 16-row
-        // group has |m'| > 128 or a lane's scale underflows or its gain overflows; then the
-        // whole group takes the unfused code RNE(fmaf(RN(RN(base * scale) - m'), A, B)).
-        float bs[8][4];
-        const float dq = qsv[qg] * ksv;
         const float scale = LAST ? a.sm : a.sm * dq;
-        float tmax;
+        scl[qg] = scale;
         if constexpr (!LAST && QF == 1) {
           // scale > 0, so RN(max(base) * scale) is the maximum of the rounded logits
           float bm = -INFINITY;
@@ -346,10 +415,10 @@ struct Wave {
           for (int j = 0; j < 8; ++j)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-              bs[j][r] = S[qg][j][r];
-              bm = fmaxf(bm, bs[j][r]);
+              bs[qg][j][r] = S[qg][j][r];
+              bm = fmaxf(bm, bs[qg][j][r]);
             }
-          tmax = bm * scale;
+          tmax[qg] = bm * scale;
         } else if constexpr (!LAST) {
           // float(acc) is exact and monotone: the row maximum is taken on the integers
           int im = S[qg][0][0];
@@ -358,10 +427,10 @@ struct Wave {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
               im = im > S[qg][j][r] ? im : S[qg][j][r];
-              bs[j][r] = __int_as_float(S[qg][j][r]) - kBiasF;
+              bs[qg][j][r] = __int_as_float(S[qg][j][r]) - kBiasF;
             }
           // the biased bits read as 12582912 + max: one exact subtraction gives float(max)
-          tmax = (__int_as_float(im) - kBiasF) * scale;
+          tmax[qg] = (__int_as_float(im) - kBiasF) * scale;
         } else {
           float bm = -INFINITY;
 #pragma unroll
@@ -370,53 +439,21 @@ struct Wave {
             for (int r = 0; r < 4; ++r) {
               const int64_t key = t * kTile + 16 * j + 8 * (r >> 1) + 2 * G + (r & 1);
               const float f = acc_value(S[qg][j], r);
-              bs[j][r] = key < a.Nk ? f * dq : -INFINITY;
-              bm = fmaxf(bm, bs[j][r]);
+              bs[qg][j][r] = key < a.Nk ? f * dq : -INFINITY;
+              bm = fmaxf(bm, bs[qg][j][r]);
             }
-          tmax = bm * scale;
-        }
-        const float mn = running_max(m[qg], tmax);
-        mold[qg] = m[qg];
-        m[qg] = mn;
-        const float gain = scale * kExpA;
-        // every lane admits the fold: scale normal, gain finite, |m'| <= 128 (lane masks
-        // combined on the scalar unit)
-        const uint64_t safe = __builtin_amdgcn_ballot_w64(scale >= 1.1754943508222875e-38f) &
-                              __builtin_amdgcn_ballot_w64(__builtin_isfinite(gain)) &
-                              __builtin_amdgcn_ballot_w64(fabsf(mn) <= 128.0f);
-        if (safe == __builtin_amdgcn_read_exec()) {
-          const float bias = __builtin_fmaf(-mn, kExpA, kExpB);
-#pragma unroll
-          for (int j = 0; j < 8; ++j) {
-            uint32_t w = 0;
-#pragma unroll
-            for (int r = 0; r < 4; ++r) w = __builtin_amdgcn_cvt_pk_u8_f32(__builtin_fmaf(bs[j][r], gain, bias), r, w);
-            P[qg][j] = static_cast<int>(w);
-          }
-        } else {
-#pragma unroll
-          for (int j = 0; j < 8; ++j) {
-            uint32_t w = 0;
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              const float lgt = bs[j][r] * scale;
-              w = __builtin_amdgcn_cvt_pk_u8_f32(__builtin_fmaf(lgt - mn, kExpA, kExpB), r, w);
-            }
-            P[qg][j] = static_cast<int>(w);
-          }
+          tmax[qg] = bm * scale;
         }
       } else if constexpr (PM == 1) {
-        float lg[8][4];
-        float tmax = -INFINITY;
-        const float dq = qsv[qg] * ksv;
+        float tm = -INFINITY;
         if constexpr (!LAST) {
           const float c = a.sm * dq;
 #pragma unroll
           for (int j = 0; j < 8; ++j)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-              lg[j][r] = acc_float(S[qg][j][r]) * c;
-              tmax = fmaxf(tmax, lg[j][r]);
+              bs[qg][j][r] = acc_float(S[qg][j][r]) * c;
+              tm = fmaxf(tm, bs[qg][j][r]);
             }
         } else {
 #pragma unroll
@@ -425,31 +462,18 @@ struct Wave {
             for (int r = 0; r < 4; ++r) {
               const int64_t key = t * kTile + 16 * j + 8 * (r >> 1) + 2 * G + (r & 1);
               float x = (acc_float(S[qg][j][r]) * dq) * a.sm;
-              lg[j][r] = key < a.Nk ? x : -INFINITY;
-              tmax = fmaxf(tmax, lg[j][r]);
+              bs[qg][j][r] = key < a.Nk ? x : -INFINITY;
+              tm = fmaxf(tm, bs[qg][j][r]);
             }
         }
-        const float mn = running_max(m[qg], tmax);
-        mold[qg] = m[qg];
-        m[qg] = mn;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          uint32_t w = 0;
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const float u = __builtin_fmaf(lg[j][r] - mn, kExpA, kExpB);
-            w = __builtin_amdgcn_cvt_pk_u8_f32(u, r, w);
-          }
-          P[qg][j] = static_cast<int>(w);
-        }
+        tmax[qg] = tm;
       } else {
         // Sage FP8 control path: log2-domain logits (a.sm carries RN(sm * RN(log2 e))),
         // running maximum with the upstream 8.807 offset, P = E4M3(exp2(.)) and an
         // unrounded mass.
-        float bs[8][4];
-        float tmax;
-        const float dq = qsv[qg] * ksv;
         const float f = LAST ? a.sm : a.sm * dq;
+        scl[qg] = f;
+        float tm;
         if constexpr (!LAST) {
           // f > 0, so fmaf(b, f, -offset) is monotone in b: the maximum is taken on the
           // scores (on the integers for INT8 accumulators), then shifted once
@@ -460,25 +484,25 @@ struct Wave {
 #pragma unroll
               for (int r = 0; r < 4; ++r) {
                 im = im > S[qg][j][r] ? im : S[qg][j][r];
-                bs[j][r] = acc_float(S[qg][j][r]);
+                bs[qg][j][r] = acc_float(S[qg][j][r]);
               }
-            tmax = __builtin_fmaf(acc_float(im), f, -kFp8Offset);
+            tm = __builtin_fmaf(acc_float(im), f, -kFp8Offset);
           } else {
             float bm = -INFINITY;
 #pragma unroll
             for (int j = 0; j < 8; ++j)
 #pragma unroll
               for (int r = 0; r < 4; ++r) {
-                bs[j][r] = S[qg][j][r];
-                bm = vmax(bm, bs[j][r]);
+                bs[qg][j][r] = S[qg][j][r];
+                bm = vmax(bm, bs[qg][j][r]);
               }
-            tmax = __builtin_fmaf(bm, f, -kFp8Offset);
+            tm = __builtin_fmaf(bm, f, -kFp8Offset);
           }
           // f = +inf (an extreme sm_scale) with a zero maximum gives NaN where the maximum of
           // the shifted terms (each -inf or NaN) is -inf
-          if (tmax != tmax) tmax = -INFINITY;
+          if (tm != tm) tm = -INFINITY;
         } else {
-          tmax = -INFINITY;
+          tm = -INFINITY;
 #pragma unroll
           for (int j = 0; j < 8; ++j)
 #pragma unroll
@@ -488,13 +512,76 @@ struct Wave {
               else b = acc_float(S[qg][j][r]);
               const int64_t key = t * kTile + 16 * j + 8 * (r >> 1) + 2 * G + (r & 1);
               b = key < a.Nk ? b * dq : -INFINITY;
-              bs[j][r] = b;
-              tmax = fmaxf(tmax, __builtin_fmaf(b, f, -kFp8Offset));
+              bs[qg][j][r] = b;
+              tm = fmaxf(tm, __builtin_fmaf(b, f, -kFp8Offset));
             }
         }
-        const float mn = running_max(m[qg], tmax);
+        tmax[qg] = tm;
+      }
+    }
+    {
+      float mn[2];
+      running_max2(m, tmax, mn);
+#pragma unroll
+      for (int qg = 0; qg < 2; ++qg) {
         mold[qg] = m[qg];
-        m[qg] = mn;
+        m[qg] = mn[qg];
+      }
+    }
+#pragma unroll
+    for (int qg = 0; qg < 2; ++qg) {
+      const float mn = m[qg];
+      if constexpr (PM == 2) {
+        // Folded ExpCast encode (the reference's default kernel modes without block
+        // values, sal/csrc/vc/vc_math.cuh:16-111): code = RNE(fmaf(base, gain, bias)) with
+        // gain = RN(scale * A) and bias = fmaf(-m', A, B), unless some row of this 16-row
+        // group has |m'| > 128 or a lane's scale underflows or its gain overflows; then the
+        // whole group takes the unfused code RNE(fmaf(RN(RN(base * scale) - m'), A, B)).
+        const float scale = scl[qg];
+        const float gain = scale * kExpA;
+        // every lane admits the fold: scale a positive normal (so gain is a positive normal
+        // or +inf) and gain a positive normal (finite), |m'| <= 128; lane masks combined on
+        // the scalar unit
+        bool fold = true;
+        if (LAST || QF == 1 || !fold_ok) {
+          const uint64_t safe = pos_normal_lanes(scale) & pos_normal_lanes(gain) &
+                                __builtin_amdgcn_ballot_w64(fabsf(mn) <= 128.0f);
+          fold = safe == __builtin_amdgcn_read_exec();
+        }
+        if (fold) {
+          const float bias = __builtin_fmaf(-mn, kExpA, kExpB);
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            uint32_t w = 0;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) w = __builtin_amdgcn_cvt_pk_u8_f32(__builtin_fmaf(bs[qg][j][r], gain, bias), r, w);
+            P[qg][j] = static_cast<int>(w);
+          }
+        } else {
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            uint32_t w = 0;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const float lgt = bs[qg][j][r] * scale;
+              w = __builtin_amdgcn_cvt_pk_u8_f32(__builtin_fmaf(lgt - mn, kExpA, kExpB), r, w);
+            }
+            P[qg][j] = static_cast<int>(w);
+          }
+        }
+      } else if constexpr (PM == 1) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          uint32_t w = 0;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const float u = __builtin_fmaf(bs[qg][j][r] - mn, kExpA, kExpB);
+            w = __builtin_amdgcn_cvt_pk_u8_f32(u, r, w);
+          }
+          P[qg][j] = static_cast<int>(w);
+        }
+      } else {
+        const float f = scl[qg];
         // Bytes of the +-2 ulp neighbours of every probability; an E4M3 midpoint within two
         // ulps (the neighbours disagree, a few lanes per million) takes the binary64 recheck.
         // At D128 the recheck is one branch per tile (a lane that missed redoes its tile from
@@ -508,7 +595,7 @@ struct Wave {
           for (int j = 0; j < 8; ++j) {
             float pr[4];
 #pragma unroll
-            for (int r = 0; r < 4; ++r) pr[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(bs[j][r], f, -mn));
+            for (int r = 0; r < 4; ++r) pr[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(bs[qg][j][r], f, -mn));
             uint32_t lo, hi;
             fp8_exp2_bounds<LAST, true>(pr, lo, hi);
             P[qg][j] = static_cast<int>(lo);
@@ -523,7 +610,7 @@ struct Wave {
               float xs[4], pr[4];
 #pragma unroll
               for (int r = 0; r < 4; ++r) {
-                float b = bs[j][r];
+                float b = bs[qg][j][r];
                 asm volatile("" : "+v"(b));  // recomputed here, not kept live from the loop above
                 xs[r] = __builtin_fmaf(b, f, -mn);
                 pr[r] = __builtin_amdgcn_exp2f(xs[r]);
@@ -539,7 +626,7 @@ struct Wave {
             float xs[4], pr[4];
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-              xs[r] = __builtin_fmaf(bs[j][r], f, -mn);
+              xs[r] = __builtin_fmaf(bs[qg][j][r], f, -mn);
               pr[r] = __builtin_amdgcn_exp2f(xs[r]);
             }
             P[qg][j] = static_cast<int>(fp8_exp2_word<LAST>(xs, pr));
@@ -748,6 +835,10 @@ __global__ __launch_bounds__(kThreadsPerBlock, (kBlocksPerCU<D, VM>)) void attn_
   // operand every tile; the smoothing variants have no registers to spare for it.
   w.ones = v8i{0x38383838, 0x38383838, 0x38383838, 0x38383838, 0x38383838, 0x38383838, 0x38383838, 0x38383838};
   if constexpr (VM == 0 && (D == 128 || PM == 2)) asm volatile("" : "+v"(w.ones));
+  w.bacc = v4i{kBias, kBias, kBias, kBias};
+  if constexpr (W::IB && VM == 0 && D == 128) asm volatile("" : "+v"(w.bacc));
+  w.fold_ok = 0;
+  if constexpr (PM == 2 && QF == 0) w.fold_precheck(a, lane);
 
   LD ld;
   ld.init(a, bh);

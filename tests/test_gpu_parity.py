@@ -745,6 +745,50 @@ def test_folded_encode_known_answer_and_group_fallback_on_gpu(extreme, code):
     np.testing.assert_array_equal(got, ecodes)
 
 
+@pytest.mark.parametrize("factor", [1e4, 1e-36], ids=["large", "tiny"])
+def test_folded_encode_known_answer_when_the_head_precheck_fails(factor):
+    # The kernel first tests the fold conditions for a whole head at once (the extreme K
+    # scales, a |logit| bound per row). Scaling the last tile's K scales by 1e4 (the bound
+    # passes 128) or 1e-36 (the smallest scale is subnormal) fails that test, so tile 0
+    # tests the conditions itself: they hold there, and key 96 keeps its folded byte.
+    s = folded_encode_payload()
+    s["ks"] = s["ks"].copy()
+    s["ks"][:, :, 4:8] *= np.float32(factor)
+    _print_case("folded encode KA, head precheck fails", factor)
+    to = _to_dev
+    v8 = to(logical_to_storage(s["v"], vcx.value_token())).view(torch.float8_e4m3fn)
+    _, pd = vcx.forward(to(s["q"]), to(s["k"]), v8, to(s["qs"]), to(s["ks"]), to(s["vs"]), None,
+                        True, False, 1, s["scale"], affine=True, p_rows=(0, 32))
+    got = pd.cpu().numpy()
+    assert got[0, 0, 0, 96] == FOLD_CODE_FOLDED and got[0, 0, 0, 45] == 120
+    _, ecodes = o.reference(s, return_codes=True, affine=True)
+    np.testing.assert_array_equal(got, ecodes)
+
+
+@pytest.mark.parametrize("dim", [64, 128])
+@pytest.mark.parametrize("factor", [10.0, 300.0, 1e-36], ids=["moderate", "large", "tiny"])
+def test_folded_encode_per_tile_conditions_with_k_scale_outliers(dim, factor):
+    # The K scales of tile 2 (of 8) multiplied by `factor`: the head-wide test of the fold
+    # conditions fails, and every tile tests them itself. moderate: every |m'| stays <= 128
+    # (all tiles fold); large: tile 2's logits pass 128, so from tile 2 on every row group
+    # takes the unfused bytes; tiny: tile 2's scale is subnormal (tile 2 unfused only).
+    # P bytes exact against the oracle, output within the bound.
+    q, k, v = make_qkv(1, 2, 160, 900, dim, torch.bfloat16, seed=23)
+    st = _oracle_state(q, k, v, False, torch.bfloat16)
+    st["ks"] = st["ks"].copy()
+    st["ks"][:, :, 8:12] *= np.float32(factor)
+    _print_case("fold conditions per tile", dim, factor)
+    to = _to_dev
+    v8 = to(logical_to_storage(st["v"], vcx.value_token())).view(torch.float8_e4m3fn)
+    out, pd = vcx.forward(to(st["q"]), to(st["k"]), v8, to(st["qs"]), to(st["ks"]), to(st["vs"]), None,
+                          True, False, st["output_type"], st["scale"], affine=True, p_rows=(0, 160))
+    eout, ecodes = o.reference(st, return_codes=True, affine=True)
+    np.testing.assert_array_equal(pd.cpu().numpy(), ecodes)
+    got = out.float().cpu().numpy()
+    err, bound = output_bound(got, eout)
+    assert np.all(err <= bound), float((err - bound).max())
+
+
 def test_deferred_mean_restore_rising_maximum_across_chunks():
     # Smoothing path: the block-mean restore is applied every 16 tiles from the rows' tile
     # masses, rescaled whenever the running maximum moves. Scores that grow with the key

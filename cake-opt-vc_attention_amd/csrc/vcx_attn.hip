@@ -215,6 +215,14 @@ __device__ inline float vmax3(float a, float b, float c) {
 // Row reductions over the four lane groups that hold one query row: gfx950
 // permlane swaps give each lane the values of lanes l^16 and l^32 without an LDS
 // round trip. Every lane of the row ends with the same value (the adds commute).
+// running_max returns max(m, row maximum of x).
+__device__ inline float running_max(float m, float x) {
+  const auto x16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = vmax(__uint_as_float(x16[0]), __uint_as_float(x16[1]));
+  const auto x32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return vmax3(m, __uint_as_float(x32[0]), __uint_as_float(x32[1]));
+}
+
 // running_max2 gives mn[g] = max(m[g], row maximum of x[g]) for both row groups of a wave
 // in one reduction. With the wave's 16-lane rows R0..R3 (lane group G = row RG): the 16-lane
 // swap of x[0] against x[1] and a maximum leave (x0 of R0|R1, x1 of R0|R1, x0 of R2|R3,
@@ -271,6 +279,7 @@ struct Wave {
   // scales keep v_cvt_f32_i32: the bias register costs them spills.
   static constexpr bool IB = QF == 0 && (PM == 2 || (PM == 1 && D == 128 && VM == 1) ||
                                          (PM == 0 && D == 128 && !(VM == 2 && DUMP)));
+  static constexpr int kD = D;
   static constexpr int DS = D / 64;  // 64-deep QK steps
   static constexpr int CB = D / 16;  // 16-channel output blocks
   static constexpr bool SMOOTH = VM >= 1, BSCALE = VM == 2;
@@ -353,7 +362,259 @@ struct Wave {
     return v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
   }
 
+  // Phase 1 of a tile for row group qg: the values the encode reads (PM 2 and 0: float(acc),
+  // on the last tile float(acc) * dq or -inf past Nk; PM 1: the logits), the logit scale
+  // (PM 2) or log2-domain factor (PM 0), and the maximum over this lane's keys.
   template <bool LAST>
+  __device__ __forceinline__ float logits(const AttnArgs& a, int64_t t, int qg, const Acc (&Sq)[8], float ksv,
+                                          float (&bs)[8][4], float& scl) const {
+    float tmo;
+    const float dq = qsv[qg] * ksv;
+    if constexpr (PM == 2) {
+      const float scale = LAST ? a.sm : a.sm * dq;
+      scl = scale;
+      if constexpr (!LAST && QF == 1) {
+        // scale > 0, so RN(max(base) * scale) is the maximum of the rounded logits
+        float bm = -INFINITY;
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            bs[j][r] = Sq[j][r];
+            bm = fmaxf(bm, bs[j][r]);
+          }
+        tmo = bm * scale;
+      } else if constexpr (!LAST) {
+        // float(acc) is exact and monotone: the row maximum is taken on the integers
+        int im = Sq[0][0];
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            im = im > Sq[j][r] ? im : Sq[j][r];
+            bs[j][r] = __int_as_float(Sq[j][r]) - kBiasF;
+          }
+        // the biased bits read as 12582912 + max: one exact subtraction gives float(max)
+        tmo = (__int_as_float(im) - kBiasF) * scale;
+      } else {
+        float bm = -INFINITY;
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int64_t key = t * kTile + 16 * j + 8 * (r >> 1) + 2 * G + (r & 1);
+            const float f = acc_value(Sq[j], r);
+            bs[j][r] = key < a.Nk ? f * dq : -INFINITY;
+            bm = fmaxf(bm, bs[j][r]);
+          }
+        tmo = bm * scale;
+      }
+    } else if constexpr (PM == 1) {
+      float tm = -INFINITY;
+      if constexpr (!LAST) {
+        const float c = a.sm * dq;
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            bs[j][r] = acc_float(Sq[j][r]) * c;
+            tm = fmaxf(tm, bs[j][r]);
+          }
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int64_t key = t * kTile + 16 * j + 8 * (r >> 1) + 2 * G + (r & 1);
+            float x = (acc_float(Sq[j][r]) * dq) * a.sm;
+            bs[j][r] = key < a.Nk ? x : -INFINITY;
+            tm = fmaxf(tm, bs[j][r]);
+          }
+      }
+      tmo = tm;
+    } else {
+      // Sage FP8 control path: log2-domain logits (a.sm carries RN(sm * RN(log2 e))),
+      // running maximum with the upstream 8.807 offset, P = E4M3(exp2(.)) and an
+      // unrounded mass.
+      const float f = LAST ? a.sm : a.sm * dq;
+      scl = f;
+      float tm;
+      if constexpr (!LAST) {
+        // f > 0, so fmaf(b, f, -offset) is monotone in b: the maximum is taken on the
+        // scores (on the integers for INT8 accumulators), then shifted once
+        if constexpr (QF == 0) {
+          int im = Sq[0][0];
+#pragma unroll
+          for (int j = 0; j < 8; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              im = im > Sq[j][r] ? im : Sq[j][r];
+              bs[j][r] = acc_float(Sq[j][r]);
+            }
+          tm = __builtin_fmaf(acc_float(im), f, -kFp8Offset);
+        } else {
+          float bm = -INFINITY;
+#pragma unroll
+          for (int j = 0; j < 8; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              bs[j][r] = Sq[j][r];
+              bm = vmax(bm, bs[j][r]);
+            }
+          tm = __builtin_fmaf(bm, f, -kFp8Offset);
+        }
+        // f = +inf (an extreme sm_scale) with a zero maximum gives NaN where the maximum of
+        // the shifted terms (each -inf or NaN) is -inf
+        if (tm != tm) tm = -INFINITY;
+      } else {
+        tm = -INFINITY;
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            float b;
+            if constexpr (QF == 1) b = Sq[j][r];
+            else b = acc_float(Sq[j][r]);
+            const int64_t key = t * kTile + 16 * j + 8 * (r >> 1) + 2 * G + (r & 1);
+            b = key < a.Nk ? b * dq : -INFINITY;
+            bs[j][r] = b;
+            tm = fmaxf(tm, __builtin_fmaf(b, f, -kFp8Offset));
+          }
+      }
+      tmo = tm;
+    }
+    return tmo;
+  }
+
+  // Phase 3 of a tile for row group qg: the P bytes against the running maximum mx (and on
+  // the control path the row's unrounded mass tmq).
+  template <bool LAST, bool PRE>
+  __device__ __forceinline__ void bytes(const AttnArgs& a, const float (&bs)[8][4], float scl, float mx, v8i& Pq,
+                                        float& tmq) const {
+    if constexpr (PM == 2) {
+      // Folded ExpCast encode (the reference's default kernel modes without block
+      // values, sal/csrc/vc/vc_math.cuh:16-111): code = RNE(fmaf(base, gain, bias)) with
+      // gain = RN(scale * A) and bias = fmaf(-m', A, B), unless some row of this 16-row
+      // group has |m'| > 128 or a lane's scale underflows or its gain overflows; then the
+      // whole group takes the unfused code RNE(fmaf(RN(RN(base * scale) - m'), A, B)).
+      const float scale = scl;
+      const float gain = scale * kExpA;
+      // every lane admits the fold: scale a positive normal (so gain is a positive normal
+      // or +inf) and gain a positive normal (finite), |m'| <= 128; lane masks combined on
+      // the scalar unit
+      bool fold = true;
+      if constexpr (!PRE) {
+        const uint64_t safe = pos_normal_lanes(scale) & pos_normal_lanes(gain) &
+                              __builtin_amdgcn_ballot_w64(fabsf(mx) <= 128.0f);
+        fold = safe == __builtin_amdgcn_read_exec();
+      }
+      if (fold) {
+        const float bias = __builtin_fmaf(-mx, kExpA, kExpB);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          uint32_t w = 0;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) w = __builtin_amdgcn_cvt_pk_u8_f32(__builtin_fmaf(bs[j][r], gain, bias), r, w);
+          Pq[j] = static_cast<int>(w);
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          uint32_t w = 0;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const float lgt = bs[j][r] * scale;
+            w = __builtin_amdgcn_cvt_pk_u8_f32(__builtin_fmaf(lgt - mx, kExpA, kExpB), r, w);
+          }
+          Pq[j] = static_cast<int>(w);
+        }
+      }
+    } else if constexpr (PM == 1) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        uint32_t w = 0;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float u = __builtin_fmaf(bs[j][r] - mx, kExpA, kExpB);
+          w = __builtin_amdgcn_cvt_pk_u8_f32(u, r, w);
+        }
+        Pq[j] = static_cast<int>(w);
+      }
+    } else {
+      const float f = scl;
+      // Bytes of the +-2 ulp neighbours of every probability; an E4M3 midpoint within two
+      // ulps (the neighbours disagree, a few lanes per million) takes the binary64 recheck.
+      // At D128 the recheck is one branch per tile (a lane that missed redoes its tile from
+      // the scores, which stay live), so the loop stays one block that the MFMAs
+      // interleave with; D64's three waves per SIMD have no registers for that and branch
+      // per four probabilities.
+      float ls = -0.0f;  // -0 + p = p: the first addition folds away
+      if constexpr (D == 128) {
+        uint32_t miss = 0;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          float pr[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) pr[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(bs[j][r], f, -mx));
+          uint32_t lo, hi;
+          fp8_exp2_bounds<LAST, true>(pr, lo, hi);
+          Pq[j] = static_cast<int>(lo);
+          miss |= lo ^ hi;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) ls += pr[r];
+        }
+        if (__builtin_expect(miss != 0, 0)) {
+          ls = -0.0f;
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            float xs[4], pr[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              float b = bs[j][r];
+              asm volatile("" : "+v"(b));  // recomputed here, not kept live from the loop above
+              xs[r] = __builtin_fmaf(b, f, -mx);
+              pr[r] = __builtin_amdgcn_exp2f(xs[r]);
+            }
+            Pq[j] = static_cast<int>(fp8_exp2_word<LAST>(xs, pr));
+#pragma unroll
+            for (int r = 0; r < 4; ++r) ls += pr[r];
+          }
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          float xs[4], pr[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            xs[r] = __builtin_fmaf(bs[j][r], f, -mx);
+            pr[r] = __builtin_amdgcn_exp2f(xs[r]);
+          }
+          Pq[j] = static_cast<int>(fp8_exp2_word<LAST>(xs, pr));
+#pragma unroll
+          for (int r = 0; r < 4; ++r) ls += pr[r];
+        }
+      }
+      tmq = row_sum(ls);
+    }
+  }
+
+  // DUMP: the P bytes of rows prow0..prow1 to pdump in logical key order.
+  __device__ __forceinline__ void dump_p(const AttnArgs& a, int64_t t, int qg, const v8i& Pq) const {
+    if constexpr (DUMP) {
+      if (row[qg] >= a.prow0 && row[qg] < a.prow1 && row[qg] < a.Nq) {
+        const int64_t npad = a.tiles * kTile;
+        uint8_t* dst = a.pdump + (bh_ * (a.prow1 - a.prow0) + (row[qg] - a.prow0)) * npad + t * kTile;
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            dst[16 * j + 8 * (r >> 1) + 2 * G + (r & 1)] = static_cast<uint8_t>((static_cast<uint32_t>(Pq[j]) >> (8 * r)) & 0xffu);
+      }
+    }
+  }
+
+  // PRE: the fold conditions hold on this tile (fold_precheck), so it does not test them
+  template <bool LAST, bool PRE = false>
   __device__ inline void tile(const AttnArgs& a, int64_t t, const uint8_t* lk, const uint8_t* lv, const uint8_t* lm) {
     const float ksv = *reinterpret_cast<const float*>(lm + LD::KS_OFF + (QF == 1 ? 0 : 4 * G));
 
@@ -393,270 +654,53 @@ struct Wave {
     }
 
     // ---- logits, online max, P bytes (ExpCast codes, or E4M3 probabilities on the control path)
-    // Phase 1, per row group: the values the encode reads and the tile's row maximum in this
-    // lane's keys. Phase 2: both row groups' running maxima in one cross-lane reduction.
-    // Phase 3, per row group: the bytes.
     v8i P[2];
-    float mold[2], tmass[2];
-    // PM 2 and 0: float(acc) (last tile: float(acc) * dq, or -inf past Nk); PM 1: the logits
-    float bs[2][8][4];
-    // tmax: this lane's maximum; scl: PM 2 the logit scale, PM 0 the log2-domain factor
-    float tmax[2], scl[2];
-#pragma unroll
-    for (int qg = 0; qg < 2; ++qg) {
-      const float dq = qsv[qg] * ksv;
-      if constexpr (PM == 2) {
-        const float scale = LAST ? a.sm : a.sm * dq;
-        scl[qg] = scale;
-        if constexpr (!LAST && QF == 1) {
-          // scale > 0, so RN(max(base) * scale) is the maximum of the rounded logits
-          float bm = -INFINITY;
-#pragma unroll
-          for (int j = 0; j < 8; ++j)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              bs[qg][j][r] = S[qg][j][r];
-              bm = fmaxf(bm, bs[qg][j][r]);
-            }
-          tmax[qg] = bm * scale;
-        } else if constexpr (!LAST) {
-          // float(acc) is exact and monotone: the row maximum is taken on the integers
-          int im = S[qg][0][0];
-#pragma unroll
-          for (int j = 0; j < 8; ++j)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              im = im > S[qg][j][r] ? im : S[qg][j][r];
-              bs[qg][j][r] = __int_as_float(S[qg][j][r]) - kBiasF;
-            }
-          // the biased bits read as 12582912 + max: one exact subtraction gives float(max)
-          tmax[qg] = (__int_as_float(im) - kBiasF) * scale;
-        } else {
-          float bm = -INFINITY;
-#pragma unroll
-          for (int j = 0; j < 8; ++j)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              const int64_t key = t * kTile + 16 * j + 8 * (r >> 1) + 2 * G + (r & 1);
-              const float f = acc_value(S[qg][j], r);
-              bs[qg][j][r] = key < a.Nk ? f * dq : -INFINITY;
-              bm = fmaxf(bm, bs[qg][j][r]);
-            }
-          tmax[qg] = bm * scale;
-        }
-      } else if constexpr (PM == 1) {
-        float tm = -INFINITY;
-        if constexpr (!LAST) {
-          const float c = a.sm * dq;
-#pragma unroll
-          for (int j = 0; j < 8; ++j)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              bs[qg][j][r] = acc_float(S[qg][j][r]) * c;
-              tm = fmaxf(tm, bs[qg][j][r]);
-            }
-        } else {
-#pragma unroll
-          for (int j = 0; j < 8; ++j)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              const int64_t key = t * kTile + 16 * j + 8 * (r >> 1) + 2 * G + (r & 1);
-              float x = (acc_float(S[qg][j][r]) * dq) * a.sm;
-              bs[qg][j][r] = key < a.Nk ? x : -INFINITY;
-              tm = fmaxf(tm, bs[qg][j][r]);
-            }
-        }
-        tmax[qg] = tm;
-      } else {
-        // Sage FP8 control path: log2-domain logits (a.sm carries RN(sm * RN(log2 e))),
-        // running maximum with the upstream 8.807 offset, P = E4M3(exp2(.)) and an
-        // unrounded mass.
-        const float f = LAST ? a.sm : a.sm * dq;
-        scl[qg] = f;
-        float tm;
-        if constexpr (!LAST) {
-          // f > 0, so fmaf(b, f, -offset) is monotone in b: the maximum is taken on the
-          // scores (on the integers for INT8 accumulators), then shifted once
-          if constexpr (QF == 0) {
-            int im = S[qg][0][0];
-#pragma unroll
-            for (int j = 0; j < 8; ++j)
-#pragma unroll
-              for (int r = 0; r < 4; ++r) {
-                im = im > S[qg][j][r] ? im : S[qg][j][r];
-                bs[qg][j][r] = acc_float(S[qg][j][r]);
-              }
-            tm = __builtin_fmaf(acc_float(im), f, -kFp8Offset);
-          } else {
-            float bm = -INFINITY;
-#pragma unroll
-            for (int j = 0; j < 8; ++j)
-#pragma unroll
-              for (int r = 0; r < 4; ++r) {
-                bs[qg][j][r] = S[qg][j][r];
-                bm = vmax(bm, bs[qg][j][r]);
-              }
-            tm = __builtin_fmaf(bm, f, -kFp8Offset);
-          }
-          // f = +inf (an extreme sm_scale) with a zero maximum gives NaN where the maximum of
-          // the shifted terms (each -inf or NaN) is -inf
-          if (tm != tm) tm = -INFINITY;
-        } else {
-          tm = -INFINITY;
-#pragma unroll
-          for (int j = 0; j < 8; ++j)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              float b;
-              if constexpr (QF == 1) b = S[qg][j][r];
-              else b = acc_float(S[qg][j][r]);
-              const int64_t key = t * kTile + 16 * j + 8 * (r >> 1) + 2 * G + (r & 1);
-              b = key < a.Nk ? b * dq : -INFINITY;
-              bs[qg][j][r] = b;
-              tm = fmaxf(tm, __builtin_fmaf(b, f, -kFp8Offset));
-            }
-        }
-        tmax[qg] = tm;
-      }
-    }
-    {
-      float mn[2];
-      running_max2(m, tmax, mn);
+    float tmass[2], bs[2][8][4], tmax[2], scl[2];
+    // resc: some maximum of the row group moved; dm: m - m' on each lane
+    bool resc[2] = {false, false};
+    float dm[2];
+    if constexpr (PM == 0) {
+      // Control path, one row group at a time (D64's three waves per SIMD have no registers
+      // for both groups' probabilities at once).
 #pragma unroll
       for (int qg = 0; qg < 2; ++qg) {
-        mold[qg] = m[qg];
-        m[qg] = mn[qg];
+        tmax[qg] = logits<LAST>(a, t, qg, S[qg], ksv, bs[qg], scl[qg]);
+        const float mn = running_max(m[qg], tmax[qg]);
+        resc[qg] = wave_any(m[qg] != mn);
+        dm[qg] = m[qg] - mn;
+        m[qg] = mn;
+        bytes<LAST, PRE>(a, bs[qg], scl[qg], m[qg], P[qg], tmass[qg]);
+        if constexpr (DUMP) dump_p(a, t, qg, P[qg]);
       }
-    }
+    } else {
 #pragma unroll
-    for (int qg = 0; qg < 2; ++qg) {
-      const float mn = m[qg];
-      if constexpr (PM == 2) {
-        // Folded ExpCast encode (the reference's default kernel modes without block
-        // values, sal/csrc/vc/vc_math.cuh:16-111): code = RNE(fmaf(base, gain, bias)) with
-        // gain = RN(scale * A) and bias = fmaf(-m', A, B), unless some row of this 16-row
-        // group has |m'| > 128 or a lane's scale underflows or its gain overflows; then the
-        // whole group takes the unfused code RNE(fmaf(RN(RN(base * scale) - m'), A, B)).
-        const float scale = scl[qg];
-        const float gain = scale * kExpA;
-        // every lane admits the fold: scale a positive normal (so gain is a positive normal
-        // or +inf) and gain a positive normal (finite), |m'| <= 128; lane masks combined on
-        // the scalar unit
-        bool fold = true;
-        if (LAST || QF == 1 || !fold_ok) {
-          const uint64_t safe = pos_normal_lanes(scale) & pos_normal_lanes(gain) &
-                                __builtin_amdgcn_ballot_w64(fabsf(mn) <= 128.0f);
-          fold = safe == __builtin_amdgcn_read_exec();
+      for (int qg = 0; qg < 2; ++qg) tmax[qg] = logits<LAST>(a, t, qg, S[qg], ksv, bs[qg], scl[qg]);
+      // Both row groups' running maxima in one cross-lane reduction, skipped when no lane's
+      // maximum exceeds its row's running maximum (then no row maximum moves).
+      if ((__builtin_amdgcn_ballot_w64(tmax[0] > m[0]) | __builtin_amdgcn_ballot_w64(tmax[1] > m[1])) != 0) {
+        float mn[2];
+        running_max2(m, tmax, mn);
+#pragma unroll
+        for (int qg = 0; qg < 2; ++qg) {
+          resc[qg] = wave_any(m[qg] != mn[qg]);
+          dm[qg] = m[qg] - mn[qg];
+          m[qg] = mn[qg];
         }
-        if (fold) {
-          const float bias = __builtin_fmaf(-mn, kExpA, kExpB);
-#pragma unroll
-          for (int j = 0; j < 8; ++j) {
-            uint32_t w = 0;
-#pragma unroll
-            for (int r = 0; r < 4; ++r) w = __builtin_amdgcn_cvt_pk_u8_f32(__builtin_fmaf(bs[qg][j][r], gain, bias), r, w);
-            P[qg][j] = static_cast<int>(w);
-          }
-        } else {
-#pragma unroll
-          for (int j = 0; j < 8; ++j) {
-            uint32_t w = 0;
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              const float lgt = bs[qg][j][r] * scale;
-              w = __builtin_amdgcn_cvt_pk_u8_f32(__builtin_fmaf(lgt - mn, kExpA, kExpB), r, w);
-            }
-            P[qg][j] = static_cast<int>(w);
-          }
-        }
-      } else if constexpr (PM == 1) {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          uint32_t w = 0;
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const float u = __builtin_fmaf(bs[qg][j][r] - mn, kExpA, kExpB);
-            w = __builtin_amdgcn_cvt_pk_u8_f32(u, r, w);
-          }
-          P[qg][j] = static_cast<int>(w);
-        }
-      } else {
-        const float f = scl[qg];
-        // Bytes of the +-2 ulp neighbours of every probability; an E4M3 midpoint within two
-        // ulps (the neighbours disagree, a few lanes per million) takes the binary64 recheck.
-        // At D128 the recheck is one branch per tile (a lane that missed redoes its tile from
-        // the scores, which stay live), so the loop stays one block that the MFMAs
-        // interleave with; D64's three waves per SIMD have no registers for that and branch
-        // per four probabilities.
-        float ls = -0.0f;  // -0 + p = p: the first addition folds away
-        if constexpr (D == 128) {
-          uint32_t miss = 0;
-#pragma unroll
-          for (int j = 0; j < 8; ++j) {
-            float pr[4];
-#pragma unroll
-            for (int r = 0; r < 4; ++r) pr[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(bs[qg][j][r], f, -mn));
-            uint32_t lo, hi;
-            fp8_exp2_bounds<LAST, true>(pr, lo, hi);
-            P[qg][j] = static_cast<int>(lo);
-            miss |= lo ^ hi;
-#pragma unroll
-            for (int r = 0; r < 4; ++r) ls += pr[r];
-          }
-          if (__builtin_expect(miss != 0, 0)) {
-            ls = -0.0f;
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-              float xs[4], pr[4];
-#pragma unroll
-              for (int r = 0; r < 4; ++r) {
-                float b = bs[qg][j][r];
-                asm volatile("" : "+v"(b));  // recomputed here, not kept live from the loop above
-                xs[r] = __builtin_fmaf(b, f, -mn);
-                pr[r] = __builtin_amdgcn_exp2f(xs[r]);
-              }
-              P[qg][j] = static_cast<int>(fp8_exp2_word<LAST>(xs, pr));
-#pragma unroll
-              for (int r = 0; r < 4; ++r) ls += pr[r];
-            }
-          }
-        } else {
-#pragma unroll
-          for (int j = 0; j < 8; ++j) {
-            float xs[4], pr[4];
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              xs[r] = __builtin_fmaf(bs[qg][j][r], f, -mn);
-              pr[r] = __builtin_amdgcn_exp2f(xs[r]);
-            }
-            P[qg][j] = static_cast<int>(fp8_exp2_word<LAST>(xs, pr));
-#pragma unroll
-            for (int r = 0; r < 4; ++r) ls += pr[r];
-          }
-        }
-        tmass[qg] = row_sum(ls);
       }
-      if constexpr (DUMP) {
-        if (row[qg] >= a.prow0 && row[qg] < a.prow1 && row[qg] < a.Nq) {
-          const int64_t npad = a.tiles * kTile;
-          uint8_t* dst = a.pdump + (bh_ * (a.prow1 - a.prow0) + (row[qg] - a.prow0)) * npad + t * kTile;
 #pragma unroll
-          for (int j = 0; j < 8; ++j)
-#pragma unroll
-            for (int r = 0; r < 4; ++r)
-              dst[16 * j + 8 * (r >> 1) + 2 * G + (r & 1)] = static_cast<uint8_t>((static_cast<uint32_t>(P[qg][j]) >> (8 * r)) & 0xffu);
-        }
+      for (int qg = 0; qg < 2; ++qg) {
+        bytes<LAST, PRE>(a, bs[qg], scl[qg], m[qg], P[qg], tmass[qg]);
+        if constexpr (DUMP) dump_p(a, t, qg, P[qg]);
       }
     }
 
-    // ---- rescale the history only when some row maximum moved: alpha = exp(m - m')
+    // ---- rescale the history of a row group in which some maximum moved: alpha = exp(m - m')
     // (exp2 of the log2-domain difference on the control path) is exactly 1 on the other
     // lanes, and O, den (and the pending mean weights) are scaled before this tile adds in.
 #pragma unroll
     for (int qg = 0; qg < 2; ++qg) {
-      if (wave_any(mold[qg] != m[qg])) {
-        const float alpha = EC ? __builtin_amdgcn_exp2f((mold[qg] - m[qg]) * 1.44269504088896341f)
-                               : __builtin_amdgcn_exp2f(mold[qg] - m[qg]);
+      if (resc[qg]) {
+        const float alpha = EC ? __builtin_amdgcn_exp2f(dm[qg] * 1.44269504088896341f) : __builtin_amdgcn_exp2f(dm[qg]);
 #pragma unroll
         for (int cb = 0; cb < CB; ++cb) O[qg][cb] *= alpha;
         den[qg] *= alpha;
@@ -778,6 +822,33 @@ struct Wave {
 template <int D, int VM>
 constexpr int kBlocksPerCU = (D == 64 && VM < 2) ? 3 : 2;
 
+
+// Tiles 0 .. tiles-2, two per iteration so each buffer is a fixed LDS object; on return t is
+// the last tile, whose K/V the DMA has been issued for (buffer t & 1).
+template <bool PRE, class W, class LD>
+__device__ __forceinline__ void body_tiles(W& w, const LD& ld, const AttnArgs& a, int64_t& t, uint8_t* lds0,
+                                           uint8_t* lds1, uint8_t* meta0, uint8_t* meta1) {
+  constexpr int KB = kTile * W::kD;
+  const int64_t body = a.tiles - 1;
+  for (; t + 2 <= body; t += 2) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    ld.issue(t + 1, lds1, lds1 + KB, meta1);
+    w.template tile<false, PRE>(a, t, lds0, lds0 + KB, meta0);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    ld.issue(t + 2, lds0, lds0 + KB, meta0);
+    w.template tile<false, PRE>(a, t + 1, lds1, lds1 + KB, meta1);
+  }
+  if (t < body) {  // odd count of body tiles: one more from buffer 0, last tile lands in buffer 1
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    ld.issue(t + 1, lds1, lds1 + KB, meta1);
+    w.template tile<false, PRE>(a, t, lds0, lds0 + KB, meta0);
+    ++t;
+  }
+}
+
 template <int D, int VM, bool DUMP, int OUT, int PM, int QF = 0>
 __global__ __launch_bounds__(kThreadsPerBlock, (kBlocksPerCU<D, VM>)) void attn_kernel(AttnArgs a) {
   typedef TileLoader<D, VM, QF> LD;
@@ -858,25 +929,14 @@ __global__ __launch_bounds__(kThreadsPerBlock, (kBlocksPerCU<D, VM>)) void attn_
     w.vsring = vsring;
   }
   ld.issue(0, lds0, lds0 + KB, meta0);
-  // Tiles before the last, two per iteration so each buffer is a fixed LDS object.
-  const int64_t body = a.tiles - 1;
+  // Tiles before the last; a wave whose fold conditions were prechecked runs the copy of
+  // the loop without the tests.
   int64_t t = 0;
-  for (; t + 2 <= body; t += 2) {
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    ld.issue(t + 1, lds1, lds1 + KB, meta1);
-    w.template tile<false>(a, t, lds0, lds0 + KB, meta0);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    ld.issue(t + 2, lds0, lds0 + KB, meta0);
-    w.template tile<false>(a, t + 1, lds1, lds1 + KB, meta1);
-  }
-  if (t < body) {  // odd count of body tiles: one more from buffer 0, last tile lands in buffer 1
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    ld.issue(t + 1, lds1, lds1 + KB, meta1);
-    w.template tile<false>(a, t, lds0, lds0 + KB, meta0);
-    ++t;
+  if constexpr (PM == 2 && QF == 0) {
+    if (w.fold_ok) body_tiles<true>(w, ld, a, t, lds0, lds1, meta0, meta1);
+    else body_tiles<false>(w, ld, a, t, lds0, lds1, meta0, meta1);
+  } else {
+    body_tiles<false>(w, ld, a, t, lds0, lds1, meta0, meta1);
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();

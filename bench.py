@@ -169,6 +169,9 @@ def main():
                     help="full: the benchmark; kernel: prepare once, then only the fused kernel "
                          "(--steps launches, for profilers); copy: a plain 1 GiB device copy "
                          "(calibrates profiler byte counters)")
+    ap.add_argument("--ready-file", default=None,
+                    help="kernel mode: create this file when the launch loop starts (a power or clock "
+                         "sampler running beside the benchmark waits for it)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build runs the sageattn_vc path on ONE GPU; multi-GPU runs are not part of it "
@@ -226,6 +229,9 @@ def main():
 
     if args.mode == "kernel":
         p = prep()
+        torch.cuda.synchronize()
+        if args.ready_file:
+            Path(args.ready_file).write_text("launching\n")
         for _ in range(args.warmup + args.steps):
             fused(p)
         torch.cuda.synchronize()

@@ -48,7 +48,12 @@
 // to an E4M3 rounding midpoint); den and the mean restore use the unrounded sum of P.
 #include "vcx_common.hpp"
 
+#include <functional>
+#include <map>
+#include <mutex>
 #include <type_traits>
+#include <utility>
+#include <vector>
 
 namespace vcx {
 namespace {
@@ -74,6 +79,9 @@ struct AttnArgs {
   float sm;
   uint8_t* pdump;
   int64_t prow0, prow1;
+  // Block list: nfull 128-row blocks, dealt to the 8 XCDs as contiguous ranges; the last kconv
+  // blocks of every XCD's range run as two 64-row blocks each, after all its 128-row blocks.
+  int64_t nfull, kconv;
 };
 
 // LDS placement of the K and V^T tiles. Both operands are read as lane (G = l/16,
@@ -269,7 +277,9 @@ __device__ inline uint64_t pos_normal_lanes(float x) {
 __device__ inline float acc_value(const v4f& acc, int r) { return acc[r]; }
 __device__ inline float acc_value(const v4i& acc, int r) { return __int_as_float(acc[r]) - kBiasF; }
 
-template <int D, int VM, bool DUMP, int PM, int QF = 0>
+// NQG: 16-row groups per wave (2: a 128-row block of 4 waves; 1: a 64-row block, the
+// finer work pieces that end each XCD's list of blocks).
+template <int D, int VM, bool DUMP, int PM, int QF = 0, int NQG = 2>
 struct Wave {
   static constexpr bool EC = PM != 0;  // ExpCast bytes (1 unfused, 2 folded) or the control path (0)
   // Biased INT8 accumulators (float(acc) = one v_sub_f32): the folded path, the unfused
@@ -292,12 +302,12 @@ struct Wave {
     else return static_cast<float>(x);
   }
 
-  v4i qf[2][DS];
-  float qsv[2];
-  int64_t row[2];
-  float m[2], den[2];
-  v4f O[2][CB];
-  float wts[2][4];  // VM 1, 2: pending mean weights of chunk tiles 4G..4G+3 (row li)
+  v4i qf[NQG][DS];
+  float qsv[NQG];
+  int64_t row[NQG];
+  float m[NQG], den[NQG];
+  v4f O[NQG][CB];
+  float wts[NQG][4];  // VM 1, 2: pending mean weights of chunk tiles 4G..4G+3 (row li)
   int koff[DS], voff[2];
   v8i ones;  // all-ones E4M3 A operand of the row-mass MFMA, kept in registers
   v4i bacc;  // kBias in every element: the initial QK accumulator of the biased paths
@@ -334,7 +344,7 @@ struct Wave {
     }
     uint64_t ok = __builtin_amdgcn_read_exec();
 #pragma unroll
-    for (int qg = 0; qg < 2; ++qg) {
+    for (int qg = 0; qg < NQG; ++qg) {
       int asum = 0;
 #pragma unroll
       for (int ds = 0; ds < DS; ++ds)
@@ -619,7 +629,7 @@ struct Wave {
     const float ksv = *reinterpret_cast<const float*>(lm + LD::KS_OFF + (QF == 1 ? 0 : 4 * G));
 
     // ---- S^T = K Q^T
-    Acc S[2][8];
+    Acc S[NQG][8];
     v4i kf[8][DS];
 #pragma unroll
     for (int j = 0; j < 2; ++j)
@@ -632,7 +642,7 @@ struct Wave {
         for (int ds = 0; ds < DS; ++ds) kf[j + 2][ds] = *reinterpret_cast<const v4i*>(lk + (j + 2) * 16 * D + koff[ds]);
       }
 #pragma unroll
-      for (int qg = 0; qg < 2; ++qg) {
+      for (int qg = 0; qg < NQG; ++qg) {
         if constexpr (QF == 1) {
           // E4M3 x E4M3 over all D channels in one 128-deep step; lane group G holds the
           // channel sets {16G..16G+15} and {64+16G..64+16G+15} for both operands.
@@ -654,16 +664,18 @@ struct Wave {
     }
 
     // ---- logits, online max, P bytes (ExpCast codes, or E4M3 probabilities on the control path)
-    v8i P[2];
-    float tmass[2], bs[2][8][4], tmax[2], scl[2];
+    v8i P[NQG];
+    float tmass[NQG], bs[NQG][8][4], tmax[NQG], scl[NQG];
     // resc: some maximum of the row group moved; dm: m - m' on each lane
-    bool resc[2] = {false, false};
-    float dm[2];
+    bool resc[NQG];
+    float dm[NQG];
+#pragma unroll
+    for (int qg = 0; qg < NQG; ++qg) resc[qg] = false;
     if constexpr (PM == 0) {
       // Control path, one row group at a time (D64's three waves per SIMD have no registers
       // for both groups' probabilities at once).
 #pragma unroll
-      for (int qg = 0; qg < 2; ++qg) {
+      for (int qg = 0; qg < NQG; ++qg) {
         tmax[qg] = logits<LAST>(a, t, qg, S[qg], ksv, bs[qg], scl[qg]);
         const float mn = running_max(m[qg], tmax[qg]);
         resc[qg] = wave_any(m[qg] != mn);
@@ -674,21 +686,24 @@ struct Wave {
       }
     } else {
 #pragma unroll
-      for (int qg = 0; qg < 2; ++qg) tmax[qg] = logits<LAST>(a, t, qg, S[qg], ksv, bs[qg], scl[qg]);
+      for (int qg = 0; qg < NQG; ++qg) tmax[qg] = logits<LAST>(a, t, qg, S[qg], ksv, bs[qg], scl[qg]);
       // Both row groups' running maxima in one cross-lane reduction, skipped when no lane's
       // maximum exceeds its row's running maximum (then no row maximum moves).
-      if ((__builtin_amdgcn_ballot_w64(tmax[0] > m[0]) | __builtin_amdgcn_ballot_w64(tmax[1] > m[1])) != 0) {
-        float mn[2];
-        running_max2(m, tmax, mn);
+      uint64_t up = __builtin_amdgcn_ballot_w64(tmax[0] > m[0]);
+      if constexpr (NQG == 2) up |= __builtin_amdgcn_ballot_w64(tmax[1] > m[1]);
+      if (up != 0) {
+        float mn[NQG];
+        if constexpr (NQG == 2) running_max2(m, tmax, mn);
+        else mn[0] = running_max(m[0], tmax[0]);
 #pragma unroll
-        for (int qg = 0; qg < 2; ++qg) {
+        for (int qg = 0; qg < NQG; ++qg) {
           resc[qg] = wave_any(m[qg] != mn[qg]);
           dm[qg] = m[qg] - mn[qg];
           m[qg] = mn[qg];
         }
       }
 #pragma unroll
-      for (int qg = 0; qg < 2; ++qg) {
+      for (int qg = 0; qg < NQG; ++qg) {
         bytes<LAST, PRE>(a, bs[qg], scl[qg], m[qg], P[qg], tmass[qg]);
         if constexpr (DUMP) dump_p(a, t, qg, P[qg]);
       }
@@ -698,7 +713,7 @@ struct Wave {
     // (exp2 of the log2-domain difference on the control path) is exactly 1 on the other
     // lanes, and O, den (and the pending mean weights) are scaled before this tile adds in.
 #pragma unroll
-    for (int qg = 0; qg < 2; ++qg) {
+    for (int qg = 0; qg < NQG; ++qg) {
       if (resc[qg]) {
         const float alpha = EC ? __builtin_amdgcn_exp2f(dm[qg] * 1.44269504088896341f) : __builtin_amdgcn_exp2f(dm[qg]);
 #pragma unroll
@@ -713,13 +728,13 @@ struct Wave {
 
     // ---- O^T += V^T P^T, mass = 1^T P^T
     const v4f zero = {0.0f, 0.0f, 0.0f, 0.0f};
-    float mass[2];
+    float mass[NQG];
     if constexpr (BSCALE) {
       // Per-block V scales: O += vs_t * PV_t per channel, one FMA per element on the PV
       // temporary of each channel block; the mean term vs_t * mean_t * mass joins the
       // deferred restore below.
 #pragma unroll
-      for (int qg = 0; qg < 2; ++qg) {
+      for (int qg = 0; qg < NQG; ++qg) {
         if constexpr (EC) mass[qg] = mfma_fp8(ones, P[qg], zero)[0];
         else mass[qg] = tmass[qg];
         den[qg] += mass[qg];
@@ -732,7 +747,7 @@ struct Wave {
         const float4 vsb = *reinterpret_cast<const float4*>(vsl + 4 * (16 * cb + 4 * G));
         const float sc[4] = {vsb.x, vsb.y, vsb.z, vsb.w};
 #pragma unroll
-        for (int qg = 0; qg < 2; ++qg) {
+        for (int qg = 0; qg < NQG; ++qg) {
           const v4f pv = mfma_fp8(vc, P[qg], zero);
 #pragma unroll
           for (int r = 0; r < 4; ++r) O[qg][cb][r] = __builtin_fmaf(pv[r], sc[r], O[qg][cb][r]);
@@ -748,11 +763,11 @@ struct Wave {
       for (int cb = 0; cb < CB; ++cb) {
         if (cb + 2 < CB) vf[cb + 2] = load_v(lv, cb + 2);
 #pragma unroll
-        for (int qg = 0; qg < 2; ++qg) O[qg][cb] = mfma_fp8(vf[cb], P[qg], O[qg][cb]);
+        for (int qg = 0; qg < NQG; ++qg) O[qg][cb] = mfma_fp8(vf[cb], P[qg], O[qg][cb]);
         __builtin_amdgcn_sched_barrier(0);
       }
 #pragma unroll
-      for (int qg = 0; qg < 2; ++qg) {
+      for (int qg = 0; qg < NQG; ++qg) {
         if constexpr (EC) mass[qg] = mfma_fp8(ones, P[qg], zero)[0];
         else mass[qg] = tmass[qg];
         den[qg] += mass[qg];
@@ -768,7 +783,7 @@ struct Wave {
       // Slots of tiles past the last hold w = 0.
       const int c = static_cast<int>(t & (kChunk - 1));
 #pragma unroll
-      for (int qg = 0; qg < 2; ++qg)
+      for (int qg = 0; qg < NQG; ++qg)
 #pragma unroll
         for (int j = 0; j < 4; ++j) wts[qg][j] = (G == (c >> 2) && j == (c & 3)) ? mass[qg] : wts[qg][j];
       if (LAST || c == kChunk - 1) flush_means(ring, t - c);
@@ -780,9 +795,9 @@ struct Wave {
   // binary32), so the mean term carries about 22 bits of the weight instead of 11.
   __device__ inline void flush_means(const uint8_t* ring, int64_t base) {
     typedef _Float16 v4h __attribute__((ext_vector_type(4)));
-    v4h b[2], bl[2];
+    v4h b[NQG], bl[NQG];
 #pragma unroll
-    for (int qg = 0; qg < 2; ++qg) {
+    for (int qg = 0; qg < NQG; ++qg) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         b[qg][j] = static_cast<_Float16>(wts[qg][j]);
@@ -806,7 +821,7 @@ struct Wave {
         }
       }
 #pragma unroll
-      for (int qg = 0; qg < 2; ++qg) {
+      for (int qg = 0; qg < NQG; ++qg) {
         O[qg][cb] = __builtin_amdgcn_mfma_f32_16x16x16f16(av, bl[qg], O[qg][cb], 0, 0, 0);
         O[qg][cb] = __builtin_amdgcn_mfma_f32_16x16x16f16(av, b[qg], O[qg][cb], 0, 0, 0);
       }
@@ -849,27 +864,15 @@ __device__ __forceinline__ void body_tiles(W& w, const LD& ld, const AttnArgs& a
   }
 }
 
-template <int D, int VM, bool DUMP, int OUT, int PM, int QF = 0>
-__global__ __launch_bounds__(kThreadsPerBlock, (kBlocksPerCU<D, VM>)) void attn_kernel(AttnArgs a) {
+// One block's rows [row0, row0 + 64 * NQG) of head bh: 4 waves of 16 * NQG rows.
+template <int D, int VM, bool DUMP, int OUT, int PM, int QF, int NQG>
+__device__ __forceinline__ void attn_block(const AttnArgs& a, int64_t bh, int64_t row0, uint8_t* lds0, uint8_t* lds1,
+                                           uint8_t* meta0, uint8_t* meta1, uint8_t* ring, uint8_t* vsring) {
   typedef TileLoader<D, VM, QF> LD;
-  typedef Wave<D, VM, DUMP, PM, QF> W;
-  constexpr int KB = kTile * D, VB = D * kTile;
-  __shared__ __attribute__((aligned(16))) uint8_t lds0[KB + VB];
-  __shared__ __attribute__((aligned(16))) uint8_t lds1[KB + VB];
-  __shared__ __attribute__((aligned(16))) uint8_t meta0[LD::META_BYTES];
-  __shared__ __attribute__((aligned(16))) uint8_t meta1[LD::META_BYTES];
+  typedef Wave<D, VM, DUMP, PM, QF, NQG> W;
+  constexpr int KB = kTile * D;
   constexpr int RING_BYTES = LD::RING ? LD::NR * 2 * D : 16;
-  __shared__ __attribute__((aligned(16))) uint8_t ring[RING_BYTES];
   constexpr int VSRING_BYTES = LD::BSCALE ? LD::NR * 4 * D : 16;
-  __shared__ __attribute__((aligned(16))) uint8_t vsring[VSRING_BYTES];
-
-  // XCD-aware order: the hardware deals blocks round-robin over 8 XCDs; give
-  // each XCD a contiguous range of (head, query block) so its L2 serves one head.
-  const int64_t nb = gridDim.x, p = blockIdx.x;
-  const int64_t per = nb / 8, rem = nb % 8, xcd = p % 8, idx = p / 8;
-  const int64_t logical = (xcd < rem ? xcd * (per + 1) : rem * (per + 1) + (xcd - rem) * per) + idx;
-  const int64_t bh = logical / a.qblocks, qb = logical % a.qblocks;
-
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   W w;
   w.G = lane >> 4;
@@ -883,8 +886,8 @@ __global__ __launch_bounds__(kThreadsPerBlock, (kBlocksPerCU<D, VM>)) void attn_
 
   // Q fragments (B operand) and per-row scales.
 #pragma unroll
-  for (int qg = 0; qg < 2; ++qg) {
-    const int64_t r = qb * kRowsPerBlock + wave * 32 + qg * 16 + w.li;
+  for (int qg = 0; qg < NQG; ++qg) {
+    const int64_t r = row0 + wave * (16 * NQG) + qg * 16 + w.li;
     w.row[qg] = r;
     // Q scale: Sage per-thread INT8 index (row/16)*8 + row%8, or the FP8 row block row/64
     const int64_t si = QF == 1 ? r / 64 : (r / 16) * 8 + r % 8;
@@ -946,7 +949,7 @@ __global__ __launch_bounds__(kThreadsPerBlock, (kBlocksPerCU<D, VM>)) void attn_
   // ---- epilogue: normalise, per-channel V scale, store 4 channels per lane and block
   const int64_t b = bh / a.H, h = bh % a.H;
 #pragma unroll
-  for (int qg = 0; qg < 2; ++qg) {
+  for (int qg = 0; qg < NQG; ++qg) {
     if (w.row[qg] >= a.Nq) continue;
     const float inv = 1.0f / w.den[qg];
     uint16_t* out = static_cast<uint16_t*>(a.out) + b * a.osb + h * a.osh + w.row[qg] * a.osn;
@@ -969,6 +972,44 @@ __global__ __launch_bounds__(kThreadsPerBlock, (kBlocksPerCU<D, VM>)) void attn_
       *reinterpret_cast<uint2*>(out + ch) = packed;
     }
   }
+}
+
+template <int D, int VM, bool DUMP, int OUT, int PM, int QF = 0>
+__global__ __launch_bounds__(kThreadsPerBlock, (kBlocksPerCU<D, VM>)) void attn_kernel(AttnArgs a) {
+#if defined(__HIP_DEVICE_COMPILE__)  // device code; the host pass only emits the launch stub
+  typedef TileLoader<D, VM, QF> LD;
+  constexpr int KB = kTile * D, VB = D * kTile;
+  __shared__ __attribute__((aligned(16))) uint8_t lds0[KB + VB];
+  __shared__ __attribute__((aligned(16))) uint8_t lds1[KB + VB];
+  __shared__ __attribute__((aligned(16))) uint8_t meta0[LD::META_BYTES];
+  __shared__ __attribute__((aligned(16))) uint8_t meta1[LD::META_BYTES];
+  constexpr int RING_BYTES = LD::RING ? LD::NR * 2 * D : 16;
+  __shared__ __attribute__((aligned(16))) uint8_t ring[RING_BYTES];
+  constexpr int VSRING_BYTES = LD::BSCALE ? LD::NR * 4 * D : 16;
+  __shared__ __attribute__((aligned(16))) uint8_t vsring[VSRING_BYTES];
+
+  // XCD-aware order: the hardware deals blocks round-robin over 8 XCDs; give each XCD a
+  // contiguous range of (head, query block) so its L2 serves one head. The j-th block of XCD
+  // x is the j-th entry of its list: the range's first n_x - kconv 128-row blocks, then each
+  // of its last kconv blocks as two 64-row halves, so that the XCD's last round is made of
+  // half-length pieces (the grid has nfull + 8 * kconv blocks; kconv <= nfull / 8).
+  const int64_t p = blockIdx.x;
+  const int64_t per = a.nfull / 8, rem = a.nfull % 8, xcd = p % 8, j = p / 8;
+  const int64_t start = xcd < rem ? xcd * (per + 1) : rem * (per + 1) + (xcd - rem) * per;
+  const int64_t nfx = per + (xcd < rem ? 1 : 0) - a.kconv;
+  if (j < nfx) {
+    const int64_t logical = start + j;
+    const int64_t bh = logical / a.qblocks, qb = logical % a.qblocks;
+    attn_block<D, VM, DUMP, OUT, PM, QF, 2>(a, bh, qb * kRowsPerBlock, lds0, lds1, meta0, meta1, ring, vsring);
+  } else {
+    const int64_t hj = j - nfx, logical = start + nfx + hj / 2;
+    const int64_t bh = logical / a.qblocks, qb = logical % a.qblocks;
+    attn_block<D, VM, DUMP, OUT, PM, QF, 1>(a, bh, qb * kRowsPerBlock + (hj & 1) * (kRowsPerBlock / 2), lds0, lds1,
+                                           meta0, meta1, ring, vsring);
+  }
+#else
+  (void)a;
+#endif
 }
 
 // Explicit instantiation of every launch variant: hipcc's host pass otherwise
@@ -1055,29 +1096,77 @@ template __global__ void attn_kernel<128, 0, false, 1, 0, 1>(AttnArgs);
 template __global__ void attn_kernel<128, 0, true, 0, 0, 1>(AttnArgs);
 template __global__ void attn_kernel<128, 0, true, 1, 0, 1>(AttnArgs);
 
+// Makespan, in units of one 128-row block's time, of one XCD's block list on S slots served
+// in list order, each block to the slot that frees first: n - k full blocks, then 2k halves
+// of relative length h.
+double list_makespan(int64_t n, int64_t k, int S, double h) {
+  std::vector<double> slot(static_cast<size_t>(S), 0.0);
+  const int64_t nf = n - k, r = nf / S, f = nf % S;
+  for (int i = 0; i < S; ++i) slot[static_cast<size_t>(i)] = static_cast<double>(r + (i < f ? 1 : 0));
+  std::make_heap(slot.begin(), slot.end(), std::greater<double>());
+  for (int64_t i = 0; i < 2 * k; ++i) {
+    std::pop_heap(slot.begin(), slot.end(), std::greater<double>());
+    slot.back() += h;
+    std::push_heap(slot.begin(), slot.end(), std::greater<double>());
+  }
+  return *std::max_element(slot.begin(), slot.end());
+}
+
+// Relative length of a 64-row block: half the MFMA and encode work, the same K/V streaming.
+constexpr double kHalfBlockTime = 0.6;
+
+// How many of each XCD's last 128-row blocks run as two 64-row blocks: the k in [0, min(nfull/8,
+// 2 S)] with the smallest modelled makespan of the fullest XCD (the smallest such k), S = the
+// XCD's block slots (CUs / 8 x blocks per CU). Cached per (nfull, S).
+int64_t tail_split(int64_t nfull, int blocks_per_cu) {
+  static std::mutex mu;
+  static std::map<std::pair<int64_t, int>, int64_t> cache;
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      cus < 8)
+    return 0;
+  const int S = cus / 8 * blocks_per_cu;
+  std::lock_guard<std::mutex> lock(mu);
+  const auto key = std::make_pair(nfull, S);
+  const auto it = cache.find(key);
+  if (it != cache.end()) return it->second;
+  const int64_t per = nfull / 8, n = per + (nfull % 8 ? 1 : 0);
+  int64_t best = 0;
+  double best_t = list_makespan(n, 0, S, kHalfBlockTime);
+  for (int64_t k = 1; k <= std::min<int64_t>(per, 2 * S); ++k) {
+    const double t = list_makespan(n, k, S, kHalfBlockTime);
+    if (t < best_t - 1e-9) { best_t = t; best = k; }
+  }
+  cache.emplace(key, best);
+  return best;
+}
+
 template <int D, int VM, bool DUMP, int OUT, int PM, int QF>
-int launch(const AttnArgs& a, int64_t nblocks, hipStream_t st) {
-  attn_kernel<D, VM, DUMP, OUT, PM, QF><<<dim3(static_cast<unsigned>(nblocks)), kThreadsPerBlock, 0, st>>>(a);
+int launch(const AttnArgs& a, hipStream_t st) {
+  AttnArgs b = a;
+  b.kconv = tail_split(a.nfull, kBlocksPerCU<D, VM>);
+  const int64_t grid = b.nfull + 8 * b.kconv;
+  attn_kernel<D, VM, DUMP, OUT, PM, QF><<<dim3(static_cast<unsigned>(grid)), kThreadsPerBlock, 0, st>>>(b);
   return check_launch("attn_kernel");
 }
 
 template <int D, int VM, int PM, int QF>
-int launch_out(const AttnArgs& a, int64_t nblocks, bool dump, int out_dtype, hipStream_t st) {
+int launch_out(const AttnArgs& a, bool dump, int out_dtype, hipStream_t st) {
   if (dump) {
-    return out_dtype == VCX_BFLOAT16 ? launch<D, VM, true, VCX_BFLOAT16, PM, QF>(a, nblocks, st)
-                                     : launch<D, VM, true, VCX_FLOAT16, PM, QF>(a, nblocks, st);
+    return out_dtype == VCX_BFLOAT16 ? launch<D, VM, true, VCX_BFLOAT16, PM, QF>(a, st)
+                                     : launch<D, VM, true, VCX_FLOAT16, PM, QF>(a, st);
   }
-  return out_dtype == VCX_BFLOAT16 ? launch<D, VM, false, VCX_BFLOAT16, PM, QF>(a, nblocks, st)
-                                   : launch<D, VM, false, VCX_FLOAT16, PM, QF>(a, nblocks, st);
+  return out_dtype == VCX_BFLOAT16 ? launch<D, VM, false, VCX_BFLOAT16, PM, QF>(a, st)
+                                   : launch<D, VM, false, VCX_FLOAT16, PM, QF>(a, st);
 }
 
 template <int D, int VM, int QF = 0>
-int launch_mode(const AttnArgs& a, int64_t nblocks, bool dump, int out_dtype, int mode, hipStream_t st) {
+int launch_mode(const AttnArgs& a, bool dump, int out_dtype, int mode, hipStream_t st) {
   if constexpr (VM == 0) {
-    if (mode == 2) return launch_out<D, VM, 2, QF>(a, nblocks, dump, out_dtype, st);
+    if (mode == 2) return launch_out<D, VM, 2, QF>(a, dump, out_dtype, st);
   }
-  return mode == 1 ? launch_out<D, VM, 1, QF>(a, nblocks, dump, out_dtype, st)
-                   : launch_out<D, VM, 0, QF>(a, nblocks, dump, out_dtype, st);
+  return mode == 1 ? launch_out<D, VM, 1, QF>(a, dump, out_dtype, st)
+                   : launch_out<D, VM, 0, QF>(a, dump, out_dtype, st);
 }
 
 // Argument checks shared by the INT8 and FP8 block entry points.
@@ -1131,17 +1220,18 @@ extern "C" int vcx_attention_fwd(const int8_t* q8, const int8_t* k8, const uint8
   a.sm = expcast != 0 ? sm_scale : sm_scale * 1.4426950408889634f;
   a.pdump = p_dump; a.prow0 = p_row_begin; a.prow1 = p_row_end;
   const int64_t nblocks = B * H * a.qblocks;
-  VCX_REQUIRE(nblocks < (int64_t(1) << 31), "too many blocks");
+  VCX_REQUIRE(nblocks < (int64_t(1) << 30), "too many blocks");
+  a.nfull = nblocks;
   hipStream_t st = static_cast<hipStream_t>(stream);
   const bool dump = p_dump != nullptr;
   if (D == 128) {
-    if (!block_values) return launch_mode<128, 0>(a, nblocks, dump, out_dtype, expcast, st);
-    return channel_scale ? launch_mode<128, 1>(a, nblocks, dump, out_dtype, expcast, st)
-                         : launch_mode<128, 2>(a, nblocks, dump, out_dtype, expcast, st);
+    if (!block_values) return launch_mode<128, 0>(a, dump, out_dtype, expcast, st);
+    return channel_scale ? launch_mode<128, 1>(a, dump, out_dtype, expcast, st)
+                         : launch_mode<128, 2>(a, dump, out_dtype, expcast, st);
   }
-  if (!block_values) return launch_mode<64, 0>(a, nblocks, dump, out_dtype, expcast, st);
-  return channel_scale ? launch_mode<64, 1>(a, nblocks, dump, out_dtype, expcast, st)
-                       : launch_mode<64, 2>(a, nblocks, dump, out_dtype, expcast, st);
+  if (!block_values) return launch_mode<64, 0>(a, dump, out_dtype, expcast, st);
+  return channel_scale ? launch_mode<64, 1>(a, dump, out_dtype, expcast, st)
+                       : launch_mode<64, 2>(a, dump, out_dtype, expcast, st);
 }
 
 extern "C" int vcx_attention_fwd_fp8(const uint8_t* q8, const uint8_t* k8, const uint8_t* v8, const float* qs,
@@ -1164,11 +1254,12 @@ extern "C" int vcx_attention_fwd_fp8(const uint8_t* q8, const uint8_t* k8, const
   a.sm = expcast != 0 ? sm_scale : sm_scale * 1.4426950408889634f;
   a.pdump = p_dump; a.prow0 = p_row_begin; a.prow1 = p_row_end;
   const int64_t nblocks = B * H * a.qblocks;
-  VCX_REQUIRE(nblocks < (int64_t(1) << 31), "too many blocks");
+  VCX_REQUIRE(nblocks < (int64_t(1) << 30), "too many blocks");
+  a.nfull = nblocks;
   hipStream_t st = static_cast<hipStream_t>(stream);
   const bool dump = p_dump != nullptr;
-  return D == 128 ? launch_mode<128, 0, 1>(a, nblocks, dump, out_dtype, expcast, st)
-                  : launch_mode<64, 0, 1>(a, nblocks, dump, out_dtype, expcast, st);
+  return D == 128 ? launch_mode<128, 0, 1>(a, dump, out_dtype, expcast, st)
+                  : launch_mode<64, 0, 1>(a, dump, out_dtype, expcast, st);
 }
 
 namespace vcx {

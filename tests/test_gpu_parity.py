@@ -433,6 +433,33 @@ def test_full_length_prep_exact_and_sampled_p_bytes():
     assert cosine(got, eout) >= 0.9999
 
 
+def test_block_list_writes_every_row_and_halves_match_the_oracle():
+    # [1,2,37741,128] makes 590 128-row blocks. Each XCD takes a contiguous range of them, and
+    # the last blocks of every range run as two 64-row blocks. On a 256-CU MI355X the chosen
+    # split makes rows 8192..9471 of both heads 64-row blocks (the end of the first and of the
+    # fifth XCD's range). Every output row must be written, and those rows must carry the
+    # oracle's P bytes (folded encode) and output.
+    B, H, N, D = 1, 2, 37741, 128
+    q, k, v = make_qkv(B, H, N, N, D, torch.bfloat16, seed=3)
+    _print_case("block list", N)
+    qd, kd, vd = (x.to(DEV) for x in (q, k, v))
+    q8, qs, k8, ks, _ = vcx.prepare_qk(qd, kd)
+    v8, vs, _ = vcx.prepare_v(vd)
+    out = torch.full((B, H, N, D), float("nan"), dtype=torch.bfloat16, device=DEV)
+    vcx.forward(q8, k8, v8, qs, ks, vs, None, True, False, 1, D ** -0.5, affine=True, out=out)
+    assert bool(torch.isfinite(out).all())
+    st = _oracle_state(q, k, v, False, torch.bfloat16)
+    r0, r1 = 8192, 9472
+    out2, pd = vcx.forward(q8, k8, v8, qs, ks, vs, None, True, False, 1, D ** -0.5, affine=True, p_rows=(r0, r1))
+    assert torch.equal(out2, out)
+    eout, ecodes = o.reference(st, query_indices=np.arange(r0, r1), return_codes=True, affine=True)
+    np.testing.assert_array_equal(pd.cpu().numpy(), ecodes)
+    got = out[:, :, r0:r1].float().cpu().numpy()
+    err, bound = output_bound(got, eout)
+    assert np.all(err <= bound)
+    assert cosine(got, eout) >= 0.9999
+
+
 @pytest.mark.parametrize("nk", [2, 129, 300])
 def test_last_tile_rounding_order_known_answer_on_gpu(nk):
     # The fused kernel's P bytes on the rounding-order payload: byte 96 when the pair of

@@ -331,10 +331,19 @@ struct Wave {
   __device__ inline void fold_precheck(const AttnArgs& a, int lane) {
     const uint32_t* kb = reinterpret_cast<const uint32_t*>(a.ks) + bh_ * a.tiles * 4;
     uint32_t kmin = 0xffffffffu, kmax = 0u;
-    for (int64_t i = lane; i < a.tiles * 4; i += 64) {
-      const uint32_t u = kb[i];
-      kmin = u < kmin ? u : kmin;
-      kmax = u > kmax ? u : kmax;
+    // 16 loads per lane in flight before any is used (one round trip per 1024 scales)
+    constexpr int kBatch = 16;
+    const int64_t n = a.tiles * 4;
+    for (int64_t i0 = lane; i0 < n; i0 += 64 * kBatch) {
+      uint32_t u[kBatch];
+#pragma unroll
+      for (int b = 0; b < kBatch; ++b) u[b] = i0 + 64 * b < n ? kb[i0 + 64 * b] : kb[i0];
+      __builtin_amdgcn_sched_barrier(0);  // all loads issued before the first use
+#pragma unroll
+      for (int b = 0; b < kBatch; ++b) {
+        kmin = u[b] < kmin ? u[b] : kmin;
+        kmax = u[b] > kmax ? u[b] : kmax;
+      }
     }
 #pragma unroll
     for (int sh = 32; sh >= 1; sh >>= 1) {

@@ -67,7 +67,10 @@ __global__ void grp_init_kernel(const void* v, int64_t H, int64_t sb, int64_t sh
 // The tile is staged through LDS with coalesced loads; each thread then reads its token's
 // row 16 bytes at a time and runs the distance chains of 8 clusters side by side (d
 // outermost), chunk after chunk of 8 centers, in binary32 and, where that does not settle
-// the argmin, in fp64; the centers are wave-uniform and come through scalar loads.
+// the argmin, in fp64. The fused schedule's binary32 centers sit in LDS channel-major and
+// come through broadcast reads (as scalar operands, 8 centers x 16 channels outgrew the
+// SGPRs and spilled into VGPR lanes); the general schedule and the fp64 chains read them
+// through scalar loads.
 template <int DT, int D, bool STATS, bool WIDE, bool GENERAL>
 __global__ __launch_bounds__(kGroupThreads) void grp_assign_kernel(
     const void* v, int64_t H, int64_t n, int64_t sb, int64_t sh, int64_t sn, int count, int CS,
@@ -114,6 +117,14 @@ __global__ __launch_bounds__(kGroupThreads) void grp_assign_kernel(
   if constexpr (GENERAL) {
     for (int c = tid; c < count; c += kGroupThreads) hist[c] = 0;
   }
+  // Fused schedule: the head's 8 binary32 centers, channel-major ([d][8]), so that one
+  // wave-uniform (broadcast) 16-byte LDS read gives four clusters' values of a channel.
+  constexpr bool LDSC = !GENERAL && D == 64;
+  __shared__ __attribute__((aligned(16))) float cl[LDSC ? kFusedClusters * D : 4];
+  if constexpr (LDSC) {
+    const float* src = centers32 + bh * kFusedClusters * D;
+    for (int e = tid; e < kFusedClusters * D; e += kGroupThreads) cl[(e % D) * kFusedClusters + e / D] = src[e];
+  }
   __syncthreads();
   const int64_t tok = tile * kTile + tid;
   int best = 0;
@@ -125,7 +136,47 @@ __global__ __launch_bounds__(kGroupThreads) void grp_assign_kernel(
   // binary32 argmin is the label; otherwise (ties, near ties, overflow) the lane takes the
   // fp64 chains below.
   bool sure = false;
-  if (tok < n) {
+  if (tok < n && LDSC) {
+    float b32 = INFINITY, s32 = INFINITY;
+    float acc[8];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) acc[c] = 0.0f;
+    const float4* cl4 = reinterpret_cast<const float4*>(cl);
+#pragma unroll 2
+    for (int i = 0; i < D / 8; ++i) {
+      const uint4 q = *reinterpret_cast<const uint4*>(&xs[tid * kStride + 8 * i]);
+      const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int d = 8 * i + 2 * k;
+        const float x0 = in_to_f32<DT>(w[k] & 0xffffu), x1 = in_to_f32<DT>(w[k] >> 16);
+        const float4 a0 = cl4[2 * d], a1 = cl4[2 * d + 1], b0 = cl4[2 * d + 2], b1 = cl4[2 * d + 3];
+        const float c0v[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+        const float c1v[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+          const float d0 = __fsub_rn(x0, c0v[c]);
+          acc[c] = __fmaf_rn(d0, d0, acc[c]);
+          const float d1 = __fsub_rn(x1, c1v[c]);
+          acc[c] = __fmaf_rn(d1, d1, acc[c]);
+        }
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < 8; ++c)
+      if (c < count) {
+        if (acc[c] < b32) {  // ties keep the lowest id (and make the order unsure)
+          s32 = b32;
+          b32 = acc[c];
+          best = c;
+        } else if (acc[c] < s32) {
+          s32 = acc[c];
+        }
+      }
+    constexpr float kOrder = 1.0f + 4.0e-5f;  // > (1 + e) / (1 - e), e = 130 * 2^-24
+    sure = s32 > b32 * kOrder + 1.0e-37f;       // false for NaN or an infinite b32
+  }
+  if (tok < n && !LDSC) {
     float b32 = INFINITY, s32 = INFINITY;
     for (int c0 = 0; c0 < count; c0 += 8) {
       const float* cen = centers32 + (bh * CS + c0) * D;  // wave-uniform: scalar loads
@@ -182,11 +233,30 @@ __global__ __launch_bounds__(kGroupThreads) void grp_assign_kernel(
           const int d = 8 * i + 2 * k;
           const double x0 = static_cast<double>(in_to_f32<DT>(w[k] & 0xffffu));
           const double x1 = static_cast<double>(in_to_f32<DT>(w[k] >> 16));
+          // fused schedule: the fp64 centers are the exact widenings of the LDS fp32 ones
+          double c0v[8], c1v[8];
+          if constexpr (LDSC) {
+            const float4* cl4 = reinterpret_cast<const float4*>(cl);
+            const float4 a0 = cl4[2 * d], a1 = cl4[2 * d + 1], b0 = cl4[2 * d + 2], b1 = cl4[2 * d + 3];
+            const float f0[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+            const float f1[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+#pragma unroll
+            for (int c = 0; c < 8; ++c) {
+              c0v[c] = static_cast<double>(f0[c]);
+              c1v[c] = static_cast<double>(f1[c]);
+            }
+          } else {
+#pragma unroll
+            for (int c = 0; c < 8; ++c) {
+              c0v[c] = cen[c * D + d];
+              c1v[c] = cen[c * D + d + 1];
+            }
+          }
 #pragma unroll
           for (int c = 0; c < 8; ++c) {
-            const double d0 = __dsub_rn(x0, cen[c * D + d]);
+            const double d0 = __dsub_rn(x0, c0v[c]);
             acc[c] = __fma_rn(d0, d0, acc[c]);
-            const double d1 = __dsub_rn(x1, cen[c * D + d + 1]);
+            const double d1 = __dsub_rn(x1, c1v[c]);
             acc[c] = __fma_rn(d1, d1, acc[c]);
           }
         }

@@ -211,51 +211,62 @@ __global__ void k_mean_kernel(const double* sums, int64_t tiles, int64_t n, int 
   k_mean_body<DT, RAW>(sums, tiles, n, D, km_f32, km_out, blockIdx.x, threadIdx.x);
 }
 
-// grid (B*H), D threads. Smoothing off: vs = RN(amax/448), recip = RN(448/amax)
-// (0 for a zero channel). Smoothing on (channel scale): vs = max(P>0 ? RN(P/448) : 1, RN(M/65504)).
-__global__ void v_scale_kernel(const float* a0, const float* a1, int64_t tiles, int D, int smooth,
-                               float* vs, float* recip) {
+// grid (B*H), D * S threads (S = 1024 / D slices of the tiles). Smoothing off: vs =
+// RN(amax/448), recip = RN(448/amax) (0 for a zero channel). Smoothing on (channel scale):
+// vs = max(P>0 ? RN(P/448) : 1, RN(M/65504)). Every quantity is a maximum, which no order
+// changes: each thread takes the maximum over its slice of tiles (loads batched), and slice 0
+// combines the slices from LDS.
+constexpr int kScaleThreads = 1024;
+template <bool SMOOTH>
+__global__ __launch_bounds__(kScaleThreads) void v_scale_kernel(const float* a0, const float* a1, int64_t tiles,
+                                                                int D, float* vs, float* recip) {
+  __shared__ float red[2][kScaleThreads];
   const int64_t bh = blockIdx.x;
-  const int ch = threadIdx.x;
+  const int ch = threadIdx.x % D, sl = threadIdx.x / D, S = blockDim.x / D;
   const float* c0 = a0 + bh * tiles * D + ch;
-  const float* c1 = smooth ? a1 + bh * tiles * D + ch : nullptr;
-  // Maxima are order-free; loads of a batch of tiles are issued together.
-  constexpr int kBatch = 16;
-  if (!smooth) {
-    float amax = 0.0f;
-    int64_t t = 0;
-    for (; t + kBatch <= tiles; t += kBatch) {
-      float v[kBatch];
+  const float* c1 = SMOOTH ? a1 + bh * tiles * D + ch : nullptr;
+  constexpr int kBatch = 8;
+  float m0 = 0.0f, m1 = 0.0f;  // smoothing off: amax; on: M (|mean|) and P (peak)
+  int64_t t = sl;
+  for (; t + (kBatch - 1) * S < tiles; t += kBatch * S) {
+    float v0[kBatch], v1[kBatch];
 #pragma unroll
-      for (int i = 0; i < kBatch; ++i) v[i] = c0[(t + i) * D];
-#pragma unroll
-      for (int i = 0; i < kBatch; ++i) amax = fmaxf(amax, v[i]);
+    for (int i = 0; i < kBatch; ++i) {
+      v0[i] = c0[(t + i * S) * D];
+      if constexpr (SMOOTH) v1[i] = c1[(t + i * S) * D];
     }
-    for (; t < tiles; ++t) amax = fmaxf(amax, c0[t * D]);
-    vs[bh * D + ch] = amax > 0.0f ? __fdiv_rn(amax, 448.0f) : 0.0f;
-    recip[bh * D + ch] = amax > 0.0f ? __fdiv_rn(448.0f, amax) : 0.0f;
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i) {
+      if constexpr (SMOOTH) {
+        m0 = fmaxf(m0, fabsf(v0[i]));
+        m1 = fmaxf(m1, v1[i]);
+      } else {
+        m0 = fmaxf(m0, v0[i]);
+      }
+    }
+  }
+  for (; t < tiles; t += S) {
+    if constexpr (SMOOTH) {
+      m0 = fmaxf(m0, fabsf(c0[t * D]));
+      m1 = fmaxf(m1, c1[t * D]);
+    } else {
+      m0 = fmaxf(m0, c0[t * D]);
+    }
+  }
+  red[0][threadIdx.x] = m0;
+  red[1][threadIdx.x] = m1;
+  __syncthreads();
+  if (sl != 0) return;
+  for (int k = 1; k < S; ++k) {
+    m0 = fmaxf(m0, red[0][k * D + ch]);
+    m1 = fmaxf(m1, red[1][k * D + ch]);
+  }
+  if constexpr (!SMOOTH) {
+    vs[bh * D + ch] = m0 > 0.0f ? __fdiv_rn(m0, 448.0f) : 0.0f;
+    recip[bh * D + ch] = m0 > 0.0f ? __fdiv_rn(448.0f, m0) : 0.0f;
   } else {
-    float P = 0.0f, M = 0.0f;
-    int64_t t = 0;
-    for (; t + kBatch <= tiles; t += kBatch) {
-      float v0[kBatch], v1[kBatch];
-#pragma unroll
-      for (int i = 0; i < kBatch; ++i) {
-        v0[i] = c0[(t + i) * D];
-        v1[i] = c1[(t + i) * D];
-      }
-#pragma unroll
-      for (int i = 0; i < kBatch; ++i) {
-        P = fmaxf(P, v1[i]);
-        M = fmaxf(M, fabsf(v0[i]));
-      }
-    }
-    for (; t < tiles; ++t) {
-      P = fmaxf(P, c1[t * D]);
-      M = fmaxf(M, fabsf(c0[t * D]));
-    }
-    float s = P > 0.0f ? __fdiv_rn(P, 448.0f) : 1.0f;
-    vs[bh * D + ch] = fmaxf(s, __fdiv_rn(M, 65504.0f));
+    const float sc = m1 > 0.0f ? __fdiv_rn(m1, 448.0f) : 1.0f;
+    vs[bh * D + ch] = fmaxf(sc, __fdiv_rn(m0, 65504.0f));
   }
 }
 
@@ -893,7 +904,7 @@ extern "C" int vcx_prepare_v_fp8(const void* v, int dtype, int64_t B, int64_t H,
     if (!smooth) {
       tile_stats_kernel<DT, DD, kVAmax><<<grid, kThreads, 0, st>>>(v, H, N, v_sb, v_sh, v_sn, perm, nullptr, a0, nullptr);
       VCX_LAUNCHED("tile_stats_kernel<Vamax>");
-      v_scale_kernel<<<dim3(BH), DD, 0, st>>>(a0, nullptr, tiles, DD, 0, vs, recip);
+      v_scale_kernel<false><<<dim3(BH), kScaleThreads / DD * DD, 0, st>>>(a0, nullptr, tiles, DD, vs, recip);
       VCX_LAUNCHED("v_scale_kernel");
       quant_v_kernel<DT, DD, 0, 1><<<grid, kThreads, 0, st>>>(v, H, N, v_sb, v_sh, v_sn, perm, recip, nullptr,
                                                               nullptr, v8, nullptr, nullptr);
@@ -903,7 +914,7 @@ extern "C" int vcx_prepare_v_fp8(const void* v, int dtype, int64_t B, int64_t H,
     tile_stats_kernel<DT, DD, kVSmooth><<<grid, kThreads, 0, st>>>(v, H, N, v_sb, v_sh, v_sn, perm, nullptr, a0, a1);
     VCX_LAUNCHED("tile_stats_kernel<Vsmooth>");
     if (channel_scale) {
-      v_scale_kernel<<<dim3(BH), DD, 0, st>>>(a0, a1, tiles, DD, 1, vs, nullptr);
+      v_scale_kernel<true><<<dim3(BH), kScaleThreads / DD * DD, 0, st>>>(a0, a1, tiles, DD, vs, nullptr);
       VCX_LAUNCHED("v_scale_kernel");
       quant_v_kernel<DT, DD, 1, 1><<<grid, kThreads, 0, st>>>(v, H, N, v_sb, v_sh, v_sn, perm, vs, a0, a1, v8,
                                                               nullptr, means);

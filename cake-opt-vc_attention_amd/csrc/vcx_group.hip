@@ -307,13 +307,23 @@ __global__ __launch_bounds__(kGroupThreads) void grp_assign_kernel(
     if constexpr (STATS) {
       __syncthreads();
       if (tid < D) {
-        // per-cluster sums over the tile's tokens in token order
+        // per-cluster sums over the tile's tokens in token order, 8 tokens a step: their
+        // indices (the same on every lane) and then their values are all loaded before the
+        // additions, which keep the list order
+        constexpr int kB = 8;
         for (int c = 0; c < count; ++c) {
           double acc = 0.0;
-          const int e = start[c + 1];
-          for (int k = start[c]; k < e; ++k) {
-            const int t = order[k];
-            acc = __dadd_rn(acc, static_cast<double>(in_to_f32<DT>(xs[t * kStride + tid])));
+          const int b = __builtin_amdgcn_readfirstlane(start[c]), e = __builtin_amdgcn_readfirstlane(start[c + 1]);
+          for (int k = b; k < e; k += kB) {
+            int ti[kB];
+            float xv[kB];
+#pragma unroll
+            for (int i = 0; i < kB; ++i) ti[i] = __builtin_amdgcn_readfirstlane(order[k + i < e ? k + i : e - 1]);
+#pragma unroll
+            for (int i = 0; i < kB; ++i) xv[i] = in_to_f32<DT>(xs[ti[i] * kStride + tid]);
+#pragma unroll
+            for (int i = 0; i < kB; ++i)
+              if (k + i < e) acc = __dadd_rn(acc, static_cast<double>(xv[i]));
           }
           psum[(meta + c) * D + tid] = acc;
         }

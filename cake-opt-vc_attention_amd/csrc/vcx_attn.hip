@@ -1146,6 +1146,7 @@ int64_t tail_split(int64_t nfull, int blocks_per_cu) {
     const double t = list_makespan(n, k, S, kHalfBlockTime);
     if (t < best_t - 1e-9) { best_t = t; best = k; }
   }
+  if (cache.size() >= 4096) cache.clear();  // a serving process sees a bounded set of shapes; stay small
   cache.emplace(key, best);
   return best;
 }

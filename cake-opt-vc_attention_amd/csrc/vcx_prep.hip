@@ -92,6 +92,16 @@ __device__ inline void tile_tree(double (&a)[D / 16], double* red, double* out_c
   if (tid < D) *out_ch = (red[tid] + red[D + tid]) + (red[2 * D + tid] + red[3 * D + tid]);
 }
 
+// One thread's INT8 (or FP8) payload piece (CPT bytes) as a non-temporal store: the payload goes to
+// HBM now instead of staying dirty in the memory-side cache, where the next streaming pass's
+// reads would pay for evicting it.
+template <int CPT>
+__device__ inline void store_payload_nt(void* dst, const uint32_t* packed) {
+  typedef uint32_t v2u __attribute__((ext_vector_type(2)));
+  if constexpr (CPT == 8) __builtin_nontemporal_store(v2u{packed[0], packed[1]}, reinterpret_cast<v2u*>(dst));
+  else __builtin_nontemporal_store(packed[0], reinterpret_cast<uint32_t*>(dst));
+}
+
 // ---------------------------------------------------------------- tile statistics
 
 enum StatsMode { kKSum = 0, kVAmax = 1, kVSmooth = 2 };
@@ -334,8 +344,7 @@ __global__ __launch_bounds__(kThreads) void quant_q_kernel(const void* q, int64_
         packed[j] = wv;
       }
       int8_t* dst = q8 + (bh * n + row) * D + c * CPT;
-      if constexpr (CPT == 8) *reinterpret_cast<uint2*>(dst) = make_uint2(packed[0], packed[1]);
-      else *reinterpret_cast<uint32_t*>(dst) = packed[0];
+      store_payload_nt<CPT>(dst, packed);
     }
     if ((lane & 31) == 0) qs[bh * qs_len + (blk * 4 + g) * 8 + t] = s;
   }
@@ -400,8 +409,7 @@ __global__ __launch_bounds__(kThreads) void quant_fp8_kernel(const void* x, int6
       packed[j] = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(y[2], y[3], wv, true));
     }
     uint8_t* dst = codes + (bh * n + row) * D + c * CPT;
-    if constexpr (CPT == 8) *reinterpret_cast<uint2*>(dst) = make_uint2(packed[0], packed[1]);
-    else *reinterpret_cast<uint32_t*>(dst) = packed[0];
+    store_payload_nt<CPT>(dst, packed);
   }
 }
 
@@ -531,8 +539,7 @@ __global__ __launch_bounds__(kThreads) void quant_k_kernel(const void* k, int64_
       packed[j] = wv;
     }
     int8_t* dst = k8 + (bh * n + key) * D + c * CPT;
-    if constexpr (CPT == 8) *reinterpret_cast<uint2*>(dst) = make_uint2(packed[0], packed[1]);
-    else *reinterpret_cast<uint32_t*>(dst) = packed[0];
+    store_payload_nt<CPT>(dst, packed);
   }
 }
 
@@ -638,7 +645,9 @@ __global__ __launch_bounds__(kThreads) void quant_v_kernel(
   for (int s = tid; s < D * 8; s += kThreads) {
     const int ch = s >> 3, part = s & 7;
     uint4 val = *reinterpret_cast<const uint4*>(&stage[ch * kTile + ((part ^ (ch / CPG)) * 16)]);
-    *reinterpret_cast<uint4*>(v8 + (bh * D + ch) * npad + tile * kTile + part * 16) = val;
+    typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+    __builtin_nontemporal_store(v4u{val.x, val.y, val.z, val.w},
+                                reinterpret_cast<v4u*>(v8 + (bh * D + ch) * npad + tile * kTile + part * 16));
   }
 }
 

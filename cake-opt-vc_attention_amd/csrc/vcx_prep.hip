@@ -22,15 +22,20 @@ struct Row {
   uint32_t w[CPT / 2];                // packed 16-bit inputs
 };
 
-// Load CPT 16-bit values of token `tok` (already permuted) for chunk c.
-template <int D>
+// Load CPT 16-bit values of token `tok` (already permuted) for chunk c. NT: a
+// non-temporal load, for a tensor read once (Q), so that it does not displace one that is
+// read again soon (K between its statistics and quantization passes) from the
+// memory-side cache.
+template <int D, bool NT = false>
 __device__ inline void load_row(const uint16_t* base, int64_t sn, int64_t tok, int c, Row<D>& r) {
   const uint16_t* p = base + tok * sn + c * Row<D>::CPT;
+  typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+  typedef uint32_t v2u __attribute__((ext_vector_type(2)));
   if constexpr (D == 128) {
-    uint4 v = *reinterpret_cast<const uint4*>(p);
+    const v4u v = NT ? __builtin_nontemporal_load(reinterpret_cast<const v4u*>(p)) : *reinterpret_cast<const v4u*>(p);
     r.w[0] = v.x; r.w[1] = v.y; r.w[2] = v.z; r.w[3] = v.w;
   } else {
-    uint2 v = *reinterpret_cast<const uint2*>(p);
+    const v2u v = NT ? __builtin_nontemporal_load(reinterpret_cast<const v2u*>(p)) : *reinterpret_cast<const v2u*>(p);
     r.w[0] = v.x; r.w[1] = v.y;
   }
 }
@@ -318,7 +323,7 @@ __global__ __launch_bounds__(kThreads) void quant_q_kernel(const void* q, int64_
   for (int pass = 0; pass < 4; ++pass) {
     const int grp = pass * 8 + w * 2 + (lane >> 5);
     const int64_t row = blk * 64 + 16 * (grp >> 3) + (grp & 7) + 8 * sel;
-    load_row<D>(base, sn, row < n ? row : 0, c, rows[pass]);
+    load_row<D, true>(base, sn, row < n ? row : 0, c, rows[pass]);
   }
 #pragma unroll
   for (int pass = 0; pass < 4; ++pass) {

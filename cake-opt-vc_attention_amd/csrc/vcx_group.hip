@@ -333,35 +333,37 @@ __global__ __launch_bounds__(kGroupThreads) void grp_assign_kernel(
 }
 
 // Fused schedule. grid (B*H, count), D threads: new center = RN_f32(sum / n) for a
-// non-empty cluster, the fp64 sum taken over tiles in order (loads batched).
-__global__ void grp_update_kernel(float* centers, double* centers64, const double* psum, const int32_t* pcnt,
-                                  int64_t tiles, int D) {
+// non-empty cluster, the fp64 sum taken over tiles in order. The launch is small (one
+// block per head and cluster), so its time is the chain of load round trips: each batch
+// puts 64 tiles' partials in flight before adding them in order (5 round trips for 295
+// tiles instead of 19 with batches of 16).
+__global__ __launch_bounds__(128) void grp_update_kernel(float* centers, double* centers64, const double* psum,
+                                                         const int32_t* pcnt, int64_t tiles, int D) {
   const int64_t bh = blockIdx.x;
   const int c = blockIdx.y, d = threadIdx.x;
-  constexpr int kBatch = 16;
-  double s = 0.0;
+  // Token count of the cluster: an integer sum (exact in any order), spread over the lanes
+  // and combined in LDS.
+  __shared__ int64_t cnt_sh[128];
+  int64_t part = 0;
+  for (int64_t t = d; t < tiles; t += D) part += pcnt[(bh * tiles + t) * kFusedClusters + c];
+  cnt_sh[d] = part;
+  __syncthreads();
   int64_t total = 0;
+  for (int i = 0; i < D; ++i) total += cnt_sh[i];
+  constexpr int kBatch = 64;
+  const double* col = psum + (bh * tiles * kFusedClusters + c) * D + d;
+  const int64_t stride = static_cast<int64_t>(kFusedClusters) * D;
+  double s = 0.0;
   int64_t t = 0;
   for (; t + kBatch <= tiles; t += kBatch) {
     double v[kBatch];
-    int cnt[kBatch];
 #pragma unroll
-    for (int i = 0; i < kBatch; ++i) {
-      const int64_t meta = (bh * tiles + t + i) * kFusedClusters + c;
-      v[i] = psum[meta * D + d];
-      cnt[i] = pcnt[meta];
-    }
+    for (int i = 0; i < kBatch; ++i) v[i] = col[(t + i) * stride];
+    __builtin_amdgcn_sched_barrier(0);  // every load of the batch issued before the first add
 #pragma unroll
-    for (int i = 0; i < kBatch; ++i) {
-      s = __dadd_rn(s, v[i]);
-      total += cnt[i];
-    }
+    for (int i = 0; i < kBatch; ++i) s = __dadd_rn(s, v[i]);
   }
-  for (; t < tiles; ++t) {
-    const int64_t meta = (bh * tiles + t) * kFusedClusters + c;
-    s = __dadd_rn(s, psum[meta * D + d]);
-    total += pcnt[meta];
-  }
+  for (; t < tiles; ++t) s = __dadd_rn(s, col[t * stride]);
   if (total > 0) {
     const float x = static_cast<float>(__ddiv_rn(s, static_cast<double>(total)));
     centers[(bh * kFusedClusters + c) * D + d] = x;

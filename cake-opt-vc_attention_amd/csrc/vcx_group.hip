@@ -416,63 +416,93 @@ __global__ void grp_update_sorted_kernel(const void* v, int64_t H, int64_t n, in
   }
 }
 
-// grid (B*H), max(64, count rounded up to 64) threads: start offset of each (tile, label)
-// in the sorted order (integer counts, so the batched loads do not change the result).
-__global__ void grp_offsets_kernel(const int32_t* pcnt, int64_t tiles, int count, int CS, int64_t* offsets) {
+// grid (B*H), 256 threads: start offset of each (tile, label) in the sorted order, labels
+// in order and tiles in order within a label. Integer counts, so the sums may be formed in
+// any order: 32 lanes per label each sum a contiguous segment of tiles (loads batched), a
+// shuffle scan over the 32 segments gives each segment's start inside its label, and the
+// labels' totals in LDS give each label's start. Labels are taken 8 at a time.
+constexpr int kOffsetThreads = 256;
+__global__ __launch_bounds__(kOffsetThreads) void grp_offsets_kernel(const int32_t* pcnt, int64_t tiles, int count,
+                                                                     int CS, int64_t* offsets) {
   __shared__ int64_t total[kMaxClusters];
   const int64_t bh = blockIdx.x;
-  const int c = threadIdx.x;
+  const int tid = threadIdx.x, r = tid & 31, sub = tid >> 5;
+  const int64_t per = (tiles + 31) / 32, t0 = r * per < tiles ? r * per : tiles;
+  const int64_t t1 = t0 + per < tiles ? t0 + per : tiles;
+  const int32_t* head = pcnt + bh * tiles * CS;
   constexpr int kBatch = 16;
-  const int32_t* col = pcnt + bh * tiles * CS + c;
-  if (c < count) {
+  auto seg_sum = [&](int c) {
     int64_t s = 0;
-    int64_t t = 0;
-    for (; t + kBatch <= tiles; t += kBatch) {
+    int64_t t = t0;
+    for (; t + kBatch <= t1; t += kBatch) {
       int v[kBatch];
 #pragma unroll
-      for (int i = 0; i < kBatch; ++i) v[i] = col[(t + i) * CS];
+      for (int i = 0; i < kBatch; ++i) v[i] = head[(t + i) * CS + c];
 #pragma unroll
       for (int i = 0; i < kBatch; ++i) s += v[i];
     }
-    for (; t < tiles; ++t) s += col[t * CS];
-    total[c] = s;
+    for (; t < t1; ++t) s += head[t * CS + c];
+    return s;
+  };
+  // exclusive start of this lane's segment inside its label (all 32 lanes take part)
+  auto seg_start = [&](int64_t s, int64_t& incl) {
+    incl = s;
+#pragma unroll
+    for (int o = 1; o < 32; o <<= 1) {
+      const int64_t y = __shfl_up(incl, o, 32);
+      if (r >= o) incl += y;
+    }
+    return incl - s;
+  };
+  for (int c0 = 0; c0 < count; c0 += 8) {
+    const int c = c0 + sub;
+    int64_t incl;
+    seg_start(c < count ? seg_sum(c) : 0, incl);
+    if (r == 31 && c < count) total[c] = incl;
   }
   __syncthreads();
-  if (c < count) {
-    int64_t off = 0;
-    for (int i = 0; i < c; ++i) off += total[i];
-    int64_t* out = offsets + bh * tiles * CS + c;
-    int64_t t = 0;
-    for (; t + kBatch <= tiles; t += kBatch) {
-      int v[kBatch];
-#pragma unroll
-      for (int i = 0; i < kBatch; ++i) v[i] = col[(t + i) * CS];
-#pragma unroll
-      for (int i = 0; i < kBatch; ++i) {
-        out[(t + i) * CS] = off;
-        off += v[i];
+  for (int c0 = 0; c0 < count; c0 += 8) {
+    const int c = c0 + sub;
+    int64_t incl;
+    int64_t off = seg_start(c < count ? seg_sum(c) : 0, incl);
+    if (c < count) {
+      for (int i = 0; i < c; ++i) off += total[i];
+      int64_t* out = offsets + bh * tiles * CS + c;
+      for (int64_t t = t0; t < t1; ++t) {
+        out[t * CS] = off;
+        off += head[t * CS + c];
       }
-    }
-    for (; t < tiles; ++t) {
-      out[t * CS] = off;
-      off += col[t * CS];
     }
   }
 }
 
-// grid (tiles, B*H), 128 threads: stable scatter of token indices.
+// grid (tiles, B*H), 128 threads (one per token): perm[offset(tile, L) + rank] = token, rank
+// = tokens of the tile before this one with the same label. Each wave finds its lanes with
+// the same label by ballots over the label's bits; the second wave adds the first wave's
+// count of that label (from LDS).
 __global__ __launch_bounds__(kGroupThreads) void grp_scatter_kernel(const int32_t* labels, int64_t n, int CS,
                                                                     const int64_t* offsets, int64_t* perm) {
-  __shared__ int lab[kTile];
+  __shared__ int first[kMaxClusters];
   const int64_t tile = blockIdx.x, bh = blockIdx.y, tiles = gridDim.x;
-  const int tid = threadIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int64_t tok = tile * kTile + tid;
   const int L = tok < n ? labels[bh * n + tok] : -1;
-  lab[tid] = L;
+  for (int i = tid; i < CS; i += kGroupThreads) first[i] = 0;
+  // labels are below 256; -1 (past n) differs from every label in bit 8
+  uint64_t same = ~0ull;
+#pragma unroll
+  for (int b = 0; b < 9; ++b) {
+    const bool bit = ((L >> b) & 1) != 0;
+    const uint64_t m = __builtin_amdgcn_ballot_w64(bit);
+    same &= bit ? m : ~m;
+  }
+  const int before = __builtin_popcountll(same & ((1ull << lane) - 1ull));
+  __syncthreads();
+  // the highest lane of each label group in wave 0 records the group's size
+  if (w == 0 && L >= 0 && (same >> lane) == 1ull) first[L] = before + 1;
   __syncthreads();
   if (tok >= n) return;
-  int rank = 0;
-  for (int t = 0; t < tid; ++t) rank += lab[t] == L;
+  const int rank = before + (w == 1 ? first[L] : 0);
   perm[bh * n + offsets[(bh * tiles + tile) * CS + L] + rank] = tok;
 }
 
@@ -565,7 +595,6 @@ extern "C" int vcx_group_values(const void* v, int dtype, int64_t B, int64_t H, 
   linspace_ids(N, count, ids);
   hipStream_t st = static_cast<hipStream_t>(stream);
   const bool wide = aligned(v, 16) && v_sb % 8 == 0 && v_sh % 8 == 0 && v_sn % 8 == 0;
-  const int offset_threads = std::max(64, (count + 63) / 64 * 64);
   auto copy_centers = [&](float* dst) -> int {
     hipError_t e = hipMemcpy2DAsync(dst, sizeof(float) * count * D, ws.centers, sizeof(float) * CS * D,
                                     sizeof(float) * count * D, BH, hipMemcpyDeviceToDevice, st);
@@ -584,7 +613,7 @@ extern "C" int vcx_group_values(const void* v, int dtype, int64_t B, int64_t H, 
             v, H, N, v_sb, v_sh, v_sn, count, CS, ws.centers, ws.centers64, lab, psum, ws.pcnt);
     };
     auto sort = [&]() -> int {
-      grp_offsets_kernel<<<dim3(BH), offset_threads, 0, st>>>(ws.pcnt, tiles, count, CS, ws.offsets);
+      grp_offsets_kernel<<<dim3(BH), kOffsetThreads, 0, st>>>(ws.pcnt, tiles, count, CS, ws.offsets);
       VCX_LAUNCHED("grp_offsets_kernel");
       grp_scatter_kernel<<<dim3(tiles, BH), kGroupThreads, 0, st>>>(lab, N, CS, ws.offsets, perm);
       VCX_LAUNCHED("grp_scatter_kernel");

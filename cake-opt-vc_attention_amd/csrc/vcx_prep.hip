@@ -362,21 +362,31 @@ __global__ __launch_bounds__(kThreads) void quant_q_kernel(const void* q, int64_
 // blk*ROWS + rr + 16*i. x' = CENTER ? RN(x - km) : x (binary32); s = max(RN(amax/448), 1e-12);
 // code = E4M3_satfinite(RN(x'/s)). Rows past n are not part of the block.
 // Reference: quantize_qk_fp8, sal/csrc/vc/qk_fp8.cu:38-74 (Q: 64 rows; K: 128 rows, centred).
-template <int DT, int D, int ROWS, bool CENTER>
+// KM (the Q pass): blocks (0, h) instead compute head h's K mean km = RN_f32(sum / n) from
+// the K statistics (the FP8 path's unrounded mean), so that walk runs beside the Q blocks.
+template <int DT, int D, int ROWS, bool CENTER, bool KM = false>
 __global__ __launch_bounds__(kThreads) void quant_fp8_kernel(const void* x, int64_t H, int64_t n,
                                                              int64_t sb, int64_t sh, int64_t sn,
-                                                             const float* km, uint8_t* codes, float* scales) {
+                                                             const float* km, uint8_t* codes, float* scales,
+                                                             KMeanArgs kma) {
+  if constexpr (KM) {
+    if (blockIdx.x == 0) {
+      if (threadIdx.x < D) k_mean_body<DT, true>(kma.sums, kma.tiles, kma.n, D, kma.km, kma.km_out, blockIdx.y, threadIdx.x);
+      return;
+    }
+  }
   constexpr int CPT = D / 16, NR = ROWS / 16;
   __shared__ float wmax[kThreads / 64];
-  const int64_t blk = blockIdx.x, bh = blockIdx.y, blocks = gridDim.x;
+  const int64_t blk = KM ? blockIdx.x - 1 : blockIdx.x, bh = blockIdx.y, blocks = KM ? gridDim.x - 1 : gridDim.x;
   const int tid = threadIdx.x, rr = tid >> 4, c = tid & 15, lane = tid & 63, w = tid >> 6;
   const uint16_t* base = head_base(x, bh, H, sb, sh);
-  // Every row of the thread is loaded before any is used.
+  // Every row of the thread is loaded before any is used; Q (read once) non-temporally, so
+  // that K stays in the memory-side cache for its own pass.
   Row<D> rows[NR];
 #pragma unroll
   for (int i = 0; i < NR; ++i) {
     const int64_t row = blk * ROWS + rr + 16 * i;
-    load_row<D>(base, sn, row < n ? row : 0, c, rows[i]);
+    load_row<D, !CENTER>(base, sn, row < n ? row : 0, c, rows[i]);
   }
   float mean[CPT];
 #pragma unroll
@@ -875,16 +885,17 @@ extern "C" int vcx_prepare_qk_fp8(const void* q, const void* k, int dtype, int64
   hipStream_t st = static_cast<hipStream_t>(stream);
   return dispatch(dtype, D, [&](auto dt, auto dd) -> int {
     constexpr int DT = decltype(dt)::value, DD = decltype(dd)::value;
-    quant_fp8_kernel<DT, DD, 64, false><<<dim3(cdiv(Nq, 64), BH), kThreads, 0, st>>>(q, H, Nq, q_sb, q_sh, q_sn,
-                                                                                   nullptr, q8, qs);
-    VCX_LAUNCHED("quant_fp8_kernel<Q>");
+    // K statistics, then the Q quantization with the K mean in its first blocks (Q read
+    // non-temporally, so K stays in the memory-side cache), then the K quantization.
     tile_stats_kernel<DT, DD, kKSum><<<dim3(tiles, BH), kThreads, 0, st>>>(k, H, Nk, k_sb, k_sh, k_sn, nullptr,
                                                                           ksum, nullptr, nullptr);
     VCX_LAUNCHED("tile_stats_kernel<K>");
-    k_mean_kernel<DT, true><<<dim3(BH), DD, 0, st>>>(ksum, tiles, Nk, DD, km, km_out);
-    VCX_LAUNCHED("k_mean_kernel");
+    const KMeanArgs kma{ksum, tiles, Nk, km, km_out};
+    quant_fp8_kernel<DT, DD, 64, false, true><<<dim3(cdiv(Nq, 64) + 1, BH), kThreads, 0, st>>>(
+        q, H, Nq, q_sb, q_sh, q_sn, nullptr, q8, qs, kma);
+    VCX_LAUNCHED("quant_fp8_kernel<Q>");
     quant_fp8_kernel<DT, DD, 128, true><<<dim3(tiles, BH), kThreads, 0, st>>>(k, H, Nk, k_sb, k_sh, k_sn, km, k8,
-                                                                              ks);
+                                                                              ks, KMeanArgs{});
     VCX_LAUNCHED("quant_fp8_kernel<K>");
     return VCX_OK;
   });

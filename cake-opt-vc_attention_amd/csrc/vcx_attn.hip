@@ -132,6 +132,10 @@ struct TileLoader {
   // ring needs kChunk + 1 slots; VM 1 keeps 32 (power of two), VM 2 (which also rings
   // 4*D bytes of V scales per tile) the minimum, to stay within two blocks' LDS per CU.
   static constexpr int NR = BSCALE ? kChunk + 1 : kRing;
+  // Slot strides of the rings, padded by 16 bytes: a flush reads slots 4 apart in the four
+  // lane groups, and 4 x (2D + 16) = 64 mod 256 puts those reads in four different 64-byte
+  // bank windows (unpadded, 4 x 2D is a multiple of 256: four-way bank conflicts).
+  static constexpr int RS = 2 * D + 16, VS = 4 * D + 16;
   // Meta region of a buffer: the tile's K scales (INT8: 4 Sage key-group scales, 16 bytes;
   // FP8 block: one scale, 4 bytes), loaded by wave 0 with the means; V scales by wave 1.
   static constexpr int MR = SMOOTH ? (2 * D) / 16 : 0;  // lanes that load the tile's means
@@ -175,7 +179,7 @@ struct TileLoader {
     const int lane = threadIdx.x & 63;
     if (wave == 0) {
       if constexpr (SMOOTH) {
-        uint8_t* dst = ring + (t % NR) * (2 * D);
+        uint8_t* dst = ring + (t % NR) * RS;
         if (lane < MR)
           __builtin_amdgcn_raw_ptr_buffer_load_lds(rm, (lds_void*)dst, 16, moff, static_cast<int>(t * D * 2), 0, 0);
       }
@@ -188,7 +192,7 @@ struct TileLoader {
     }
     if constexpr (BSCALE) {
       if (wave == 1 && lane < VL)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_void*)(vsring + (t % NR) * (4 * D)), 16, moff,
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_void*)(vsring + (t % NR) * VS), 16, moff,
                                                  static_cast<int>(t * D * 4), 0, 0);
     }
     const int kso = static_cast<int>(t * kTile * D);
@@ -204,6 +208,13 @@ struct TileLoader {
 
 __device__ inline v4f mfma_fp8(const v8i& a, const v8i& b, const v4f& c) {
   return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
+}
+// Row mass: A = 16 x 128 ones in FP4 E2M1 (0x2 = 1.0; 16 bytes per lane, so the compiler
+// keeps four registers instead of eight), B = the E4M3 probabilities. Same 8-pass timing as
+// the E4M3 x E4M3 product (measured) and the same sums: every product is exactly P.
+__device__ inline v4f mfma_mass(const v4i& ones4, const v8i& b, const v4f& c) {
+  const v8i a = {ones4[0], ones4[1], ones4[2], ones4[3], 0, 0, 0, 0};  // upper half unread
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 4, 0, 0, 0, 0, 0);
 }
 
 // v_max_f32 / v_max3_f32 as single instructions: fmaxf lowers to maxnum, around which the
@@ -302,14 +313,22 @@ struct Wave {
     else return static_cast<float>(x);
   }
 
+  // DACC: the row mass accumulates in the C operand of the all-ones MFMA (element 0 is the
+  // row's denominator; the history rescale scales only that element, the other three are
+  // never read) instead of a zero-started MFMA and one addition per tile: ExpCast without
+  // block values at D128 (D64's three waves per SIMD have no registers for it).
+  static constexpr bool DACC = EC && VM == 0 && D == 128;
   v4i qf[NQG][DS];
   float qsv[NQG];
   int64_t row[NQG];
   float m[NQG], den[NQG];
+  v4f dacc[NQG];
+  // Folded encode: fmaf(-m, A, B) of the running maximum, refreshed only when m moves
+  float fbias[NQG];
   v4f O[NQG][CB];
   float wts[NQG][4];  // VM 1, 2: pending mean weights of chunk tiles 4G..4G+3 (row li)
   int koff[DS], voff[2];
-  v8i ones;  // all-ones E4M3 A operand of the row-mass MFMA, kept in registers
+  v4i ones;  // all-ones FP4 (E2M1) A operand of the row-mass MFMA
   v4i bacc;  // kBias in every element: the initial QK accumulator of the biased paths
   // Folded encode (INT8 QK): the per-tile fold conditions are known to hold on every tile
   // but the last (set once per wave by fold_precheck; wave-uniform)
@@ -508,8 +527,8 @@ struct Wave {
   // Phase 3 of a tile for row group qg: the P bytes against the running maximum mx (and on
   // the control path the row's unrounded mass tmq).
   template <bool LAST, bool PRE>
-  __device__ __forceinline__ void bytes(const AttnArgs& a, const float (&bs)[8][4], float scl, float mx, v8i& Pq,
-                                        float& tmq) const {
+  __device__ __forceinline__ void bytes(const AttnArgs& a, const float (&bs)[8][4], float scl, float mx, float fb,
+                                        v8i& Pq, float& tmq) const {
     if constexpr (PM == 2) {
       // Folded ExpCast encode (the reference's default kernel modes without block
       // values, sal/csrc/vc/vc_math.cuh:16-111): code = RNE(fmaf(base, gain, bias)) with
@@ -528,7 +547,7 @@ struct Wave {
         fold = safe == __builtin_amdgcn_read_exec();
       }
       if (fold) {
-        const float bias = __builtin_fmaf(-mx, kExpA, kExpB);
+        const float bias = fb;  // fmaf(-mx, A, B), kept with the running maximum
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
           uint32_t w = 0;
@@ -690,7 +709,7 @@ struct Wave {
         resc[qg] = wave_any(m[qg] != mn);
         dm[qg] = m[qg] - mn;
         m[qg] = mn;
-        bytes<LAST, PRE>(a, bs[qg], scl[qg], m[qg], P[qg], tmass[qg]);
+        bytes<LAST, PRE>(a, bs[qg], scl[qg], m[qg], 0.0f, P[qg], tmass[qg]);
         if constexpr (DUMP) dump_p(a, t, qg, P[qg]);
       }
     } else {
@@ -709,11 +728,12 @@ struct Wave {
           resc[qg] = wave_any(m[qg] != mn[qg]);
           dm[qg] = m[qg] - mn[qg];
           m[qg] = mn[qg];
+          if constexpr (PM == 2) fbias[qg] = __builtin_fmaf(-mn[qg], kExpA, kExpB);
         }
       }
 #pragma unroll
       for (int qg = 0; qg < NQG; ++qg) {
-        bytes<LAST, PRE>(a, bs[qg], scl[qg], m[qg], P[qg], tmass[qg]);
+        bytes<LAST, PRE>(a, bs[qg], scl[qg], m[qg], fbias[qg], P[qg], tmass[qg]);
         if constexpr (DUMP) dump_p(a, t, qg, P[qg]);
       }
     }
@@ -727,7 +747,8 @@ struct Wave {
         const float alpha = EC ? __builtin_amdgcn_exp2f(dm[qg] * 1.44269504088896341f) : __builtin_amdgcn_exp2f(dm[qg]);
 #pragma unroll
         for (int cb = 0; cb < CB; ++cb) O[qg][cb] *= alpha;
-        den[qg] *= alpha;
+        if constexpr (DACC) dacc[qg][0] *= alpha;
+        else den[qg] *= alpha;
         if constexpr (SMOOTH) {
 #pragma unroll
           for (int j = 0; j < 4; ++j) wts[qg][j] *= alpha;
@@ -744,11 +765,11 @@ struct Wave {
       // deferred restore below.
 #pragma unroll
       for (int qg = 0; qg < NQG; ++qg) {
-        if constexpr (EC) mass[qg] = mfma_fp8(ones, P[qg], zero)[0];
+        if constexpr (EC) mass[qg] = mfma_mass(ones, P[qg], zero)[0];
         else mass[qg] = tmass[qg];
         den[qg] += mass[qg];
       }
-      const uint8_t* vsl = vsring + (t % LD::NR) * (4 * D);
+      const uint8_t* vsl = vsring + (t % LD::NR) * LD::VS;
       v8i vc = load_v(lv, 0), vn;
 #pragma unroll
       for (int cb = 0; cb < CB; ++cb) {
@@ -777,9 +798,13 @@ struct Wave {
       }
 #pragma unroll
       for (int qg = 0; qg < NQG; ++qg) {
-        if constexpr (EC) mass[qg] = mfma_fp8(ones, P[qg], zero)[0];
-        else mass[qg] = tmass[qg];
-        den[qg] += mass[qg];
+        if constexpr (DACC) {
+          dacc[qg] = mfma_mass(ones, P[qg], dacc[qg]);
+        } else {
+          if constexpr (EC) mass[qg] = mfma_mass(ones, P[qg], zero)[0];
+          else mass[qg] = tmass[qg];
+          den[qg] += mass[qg];
+        }
       }
     }
     if constexpr (SMOOTH) {
@@ -791,12 +816,23 @@ struct Wave {
       // parts).
       // Slots of tiles past the last hold w = 0.
       const int c = static_cast<int>(t & (kChunk - 1));
-#pragma unroll
-      for (int qg = 0; qg < NQG; ++qg)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) wts[qg][j] = (G == (c >> 2) && j == (c & 3)) ? mass[qg] : wts[qg][j];
+      // one select per row group: the slot c & 3 is wave-uniform (a scalar branch), only the
+      // lane-group test G == c / 4 is per lane
+      const bool mine = G == (c >> 2);
+      switch (c & 3) {
+        case 0: set_weight<0>(mine, mass); break;
+        case 1: set_weight<1>(mine, mass); break;
+        case 2: set_weight<2>(mine, mass); break;
+        default: set_weight<3>(mine, mass); break;
+      }
       if (LAST || c == kChunk - 1) flush_means(ring, t - c);
     }
+  }
+
+  template <int J>
+  __device__ __forceinline__ void set_weight(bool mine, const float (&mass)[NQG]) {
+#pragma unroll
+    for (int qg = 0; qg < NQG; ++qg) wts[qg][J] = mine ? mass[qg] : wts[qg][J];
   }
 
   // O += means (x) weights over the chunk that starts at tile `base` (VM 1, 2). Each weight
@@ -820,10 +856,10 @@ struct Wave {
       v4h av;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const int slot = static_cast<int>((base + 4 * G + j) % LD::NR);
-        const _Float16 mh = *reinterpret_cast<const _Float16*>(col + slot * (2 * D) + 32 * cb);
+        const uint32_t slot = (static_cast<uint32_t>(base) + 4 * G + j) % LD::NR;
+        const _Float16 mh = *reinterpret_cast<const _Float16*>(col + slot * LD::RS + 32 * cb);
         if constexpr (BSCALE) {
-          const float vsv = *reinterpret_cast<const float*>(vsring + slot * (4 * D) + 4 * (16 * cb + li));
+          const float vsv = *reinterpret_cast<const float*>(vsring + slot * LD::VS + 4 * (16 * cb + li));
           av[j] = static_cast<_Float16>(static_cast<float>(mh) * vsv);
         } else {
           av[j] = mh;
@@ -849,11 +885,11 @@ constexpr int kBlocksPerCU = (D == 64 && VM < 2) ? 3 : 2;
 
 // Tiles 0 .. tiles-2, two per iteration so each buffer is a fixed LDS object; on return t is
 // the last tile, whose K/V the DMA has been issued for (buffer t & 1).
-template <bool PRE, class W, class LD>
-__device__ __forceinline__ void body_tiles(W& w, const LD& ld, const AttnArgs& a, int64_t& t, uint8_t* lds0,
+template <bool PRE, class W, class LD, class TI>
+__device__ __forceinline__ void body_tiles(W& w, const LD& ld, const AttnArgs& a, TI& t, uint8_t* lds0,
                                            uint8_t* lds1, uint8_t* meta0, uint8_t* meta1) {
   constexpr int KB = kTile * W::kD;
-  const int64_t body = a.tiles - 1;
+  const TI body = static_cast<TI>(a.tiles) - 1;
   for (; t + 2 <= body; t += 2) {
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
@@ -880,8 +916,8 @@ __device__ __forceinline__ void attn_block(const AttnArgs& a, int64_t bh, int64_
   typedef TileLoader<D, VM, QF> LD;
   typedef Wave<D, VM, DUMP, PM, QF, NQG> W;
   constexpr int KB = kTile * D;
-  constexpr int RING_BYTES = LD::RING ? LD::NR * 2 * D : 16;
-  constexpr int VSRING_BYTES = LD::BSCALE ? LD::NR * 4 * D : 16;
+  constexpr int RING_BYTES = LD::RING ? LD::NR * LD::RS : 16;
+  constexpr int VSRING_BYTES = LD::BSCALE ? LD::NR * LD::VS : 16;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   W w;
   w.G = lane >> 4;
@@ -908,6 +944,8 @@ __device__ __forceinline__ void attn_block(const AttnArgs& a, int64_t bh, int64_
     }
     w.m[qg] = -5000000.0f;
     w.den[qg] = 0.0f;
+    w.dacc[qg] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    w.fbias[qg] = __builtin_fmaf(5000000.0f, kExpA, kExpB);
 #pragma unroll
     for (int j = 0; j < 4; ++j) w.wts[qg][j] = 0.0f;
 #pragma unroll
@@ -916,7 +954,7 @@ __device__ __forceinline__ void attn_block(const AttnArgs& a, int64_t bh, int64_
 
   // Without block values the opaque copy keeps the compiler from rebuilding the constant
   // operand every tile; the smoothing variants have no registers to spare for it.
-  w.ones = v8i{0x38383838, 0x38383838, 0x38383838, 0x38383838, 0x38383838, 0x38383838, 0x38383838, 0x38383838};
+  w.ones = v4i{0x22222222, 0x22222222, 0x22222222, 0x22222222};
   if constexpr (VM == 0 && (D == 128 || PM == 2)) asm volatile("" : "+v"(w.ones));
   w.bacc = v4i{kBias, kBias, kBias, kBias};
   if constexpr (W::IB && VM == 0 && D == 128) asm volatile("" : "+v"(w.bacc));
@@ -943,7 +981,10 @@ __device__ __forceinline__ void attn_block(const AttnArgs& a, int64_t bh, int64_
   ld.issue(0, lds0, lds0 + KB, meta0);
   // Tiles before the last; a wave whose fold conditions were prechecked runs the copy of
   // the loop without the tests.
-  int64_t t = 0;
+  // 32-bit tile index (tiles < 2^23), so the loop test stays on the scalar unit; the
+  // per-block-scale variants keep 64 bits (with 32 their register allocation spills)
+  typedef std::conditional_t<VM == 2, int64_t, int> TI;
+  TI t = 0;
   if constexpr (PM == 2 && QF == 0) {
     if (w.fold_ok) body_tiles<true>(w, ld, a, t, lds0, lds1, meta0, meta1);
     else body_tiles<false>(w, ld, a, t, lds0, lds1, meta0, meta1);
@@ -960,7 +1001,7 @@ __device__ __forceinline__ void attn_block(const AttnArgs& a, int64_t bh, int64_
 #pragma unroll
   for (int qg = 0; qg < NQG; ++qg) {
     if (w.row[qg] >= a.Nq) continue;
-    const float inv = 1.0f / w.den[qg];
+    const float inv = 1.0f / (W::DACC ? w.dacc[qg][0] : w.den[qg]);
     uint16_t* out = static_cast<uint16_t*>(a.out) + b * a.osb + h * a.osh + w.row[qg] * a.osn;
 #pragma unroll
     for (int cb = 0; cb < W::CB; ++cb) {
@@ -992,9 +1033,9 @@ __global__ __launch_bounds__(kThreadsPerBlock, (kBlocksPerCU<D, VM>)) void attn_
   __shared__ __attribute__((aligned(16))) uint8_t lds1[KB + VB];
   __shared__ __attribute__((aligned(16))) uint8_t meta0[LD::META_BYTES];
   __shared__ __attribute__((aligned(16))) uint8_t meta1[LD::META_BYTES];
-  constexpr int RING_BYTES = LD::RING ? LD::NR * 2 * D : 16;
+  constexpr int RING_BYTES = LD::RING ? LD::NR * LD::RS : 16;
   __shared__ __attribute__((aligned(16))) uint8_t ring[RING_BYTES];
-  constexpr int VSRING_BYTES = LD::BSCALE ? LD::NR * 4 * D : 16;
+  constexpr int VSRING_BYTES = LD::BSCALE ? LD::NR * LD::VS : 16;
   __shared__ __attribute__((aligned(16))) uint8_t vsring[VSRING_BYTES];
 
   // XCD-aware order: the hardware deals blocks round-robin over 8 XCDs; give each XCD a
@@ -1330,6 +1371,37 @@ extern "C" int vcx_kernel_resources(int64_t D, int block_values, int64_t* out) {
   else fn = block_values ? reinterpret_cast<const void*>(&attn_kernel<64, 1, false, VCX_BFLOAT16, 1>)
                          : reinterpret_cast<const void*>(&attn_kernel<64, 0, false, VCX_BFLOAT16, 2>);
   return resources_of(fn, out);
+}
+
+namespace {
+template <int D, int VM, int PM, int OUT>
+const void* kernel_of() { return reinterpret_cast<const void*>(&attn_kernel<D, VM, false, OUT, PM>); }
+
+template <int D, int OUT>
+const void* kernel_of(int vm, int pm) {
+  if (vm == 0) return pm == 2 ? kernel_of<D, 0, 2, OUT>() : pm == 1 ? kernel_of<D, 0, 1, OUT>() : kernel_of<D, 0, 0, OUT>();
+  if (vm == 1) return pm == 1 ? kernel_of<D, 1, 1, OUT>() : kernel_of<D, 1, 0, OUT>();
+  return pm == 1 ? kernel_of<D, 2, 1, OUT>() : kernel_of<D, 2, 0, OUT>();
+}
+}  // namespace
+
+extern "C" int vcx_kernel_resources_mode(int64_t D, int value_mode, int expcast, int out_dtype, int64_t* out) {
+  VCX_REQUIRE(out != nullptr, "out is null");
+  VCX_REQUIRE(D == 64 || D == 128, "D must be 64 or 128");
+  VCX_REQUIRE(value_mode >= 0 && value_mode <= 2, "value_mode must be 0, 1 or 2");
+  VCX_REQUIRE(expcast >= 0 && expcast <= 2, "expcast must be 0, 1 or 2");
+  VCX_REQUIRE(expcast != 2 || value_mode == 0, "the folded ExpCast encode (expcast = 2) is defined without block values");
+  VCX_REQUIRE(out_dtype == VCX_FLOAT16 || out_dtype == VCX_BFLOAT16, "out_dtype must be float16 or bfloat16");
+  const void* fn = D == 128 ? (out_dtype == VCX_BFLOAT16 ? kernel_of<128, VCX_BFLOAT16>(value_mode, expcast)
+                                                         : kernel_of<128, VCX_FLOAT16>(value_mode, expcast))
+                            : (out_dtype == VCX_BFLOAT16 ? kernel_of<64, VCX_BFLOAT16>(value_mode, expcast)
+                                                         : kernel_of<64, VCX_FLOAT16>(value_mode, expcast));
+  if (int rc = resources_of(fn, out)) return rc;
+  int blocks = 0;
+  hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, fn, kThreadsPerBlock, 0);
+  if (e != hipSuccess) return fail(VCX_EHIP, "hipOccupancyMaxActiveBlocksPerMultiprocessor: %s", hipGetErrorString(e));
+  out[6] = blocks;
+  return VCX_OK;
 }
 
 extern "C" int vcx_kernel_resources_fp8(int64_t D, int expcast, int64_t* out) {

@@ -107,9 +107,12 @@ __device__ inline uint32_t e4m3_sat(float x) {
 // within two ulps of p; only then does the lane recompute exp2 in binary64 and round it once
 // to binary32 (p is updated to that value). The +-2 ulp neighbours of two probabilities come
 // from one 64-bit add each way (v_lshl_add_u64); a borrow out of a low half below 2 ulps (p
-// = 0 or nearly) only widens the window or yields a NaN byte, i.e. a needless recheck.
-// SAT = true forms the lower neighbours with a saturating subtraction instead, for tiles
-// with masked keys (p = exp2(-inf) = 0). Reference: the probability byte of
+// = 0 or the smallest subnormal, i.e. x below about -149) only widens the window or yields a
+// NaN byte, i.e. a needless recheck with the right result. For N(0,1)-like scores that is a
+// few lanes per million; rows whose scores lie more than about 100 nats below the row
+// maximum meet it on most tiles (at D128 the whole tile is then redone), which costs time,
+// never bytes. SAT = true forms the lower neighbours with a saturating subtraction instead,
+// for tiles with masked keys (p = exp2(-inf) = 0). Reference: the probability byte of
 // sal/sageattention_local/vc_reference.py:68-75 and sal/csrc/qattn/attn_utils.cuh:355-455.
 // fp8_exp2_bounds gives the bytes of both neighbour sets (lo, hi); fp8_exp2_word resolves a
 // disagreement. Binary64 exp2 rounded once to binary32: one out-of-line copy for the rare

@@ -162,9 +162,11 @@ __global__ __launch_bounds__(kGroupThreads) void grp_assign_kernel(
         }
       }
     }
+    bool finite = true;  // a NaN distance (NaN in V or a center) fails every compare below
 #pragma unroll
     for (int c = 0; c < 8; ++c)
       if (c < count) {
+        finite = finite && acc[c] >= 0.0f;
         if (acc[c] < b32) {  // ties keep the lowest id (and make the order unsure)
           s32 = b32;
           b32 = acc[c];
@@ -174,10 +176,13 @@ __global__ __launch_bounds__(kGroupThreads) void grp_assign_kernel(
         }
       }
     constexpr float kOrder = 1.0f + 4.0e-5f;  // > (1 + e) / (1 - e), e = 130 * 2^-24
-    sure = s32 > b32 * kOrder + 1.0e-37f;       // false for NaN or an infinite b32
+    // NaN distances never enter b32 / s32, so they are tested separately: with one the fp64
+    // chains decide, as in the oracle; an infinite b32 also leaves the order unsure
+    sure = finite && s32 > b32 * kOrder + 1.0e-37f;
   }
   if (tok < n && !LDSC) {
     float b32 = INFINITY, s32 = INFINITY;
+    bool finite = true;  // a NaN distance (NaN in V or a center) fails every compare below
     for (int c0 = 0; c0 < count; c0 += 8) {
       const float* cen = centers32 + (bh * CS + c0) * D;  // wave-uniform: scalar loads
       float acc[8];
@@ -203,6 +208,7 @@ __global__ __launch_bounds__(kGroupThreads) void grp_assign_kernel(
 #pragma unroll
       for (int c = 0; c < 8; ++c)
         if (c0 + c < count) {
+          finite = finite && acc[c] >= 0.0f;
           if (acc[c] < b32) {  // ties keep the lowest id (and make the order unsure)
             s32 = b32;
             b32 = acc[c];
@@ -213,11 +219,13 @@ __global__ __launch_bounds__(kGroupThreads) void grp_assign_kernel(
         }
     }
     constexpr float kOrder = 1.0f + 4.0e-5f;  // > (1 + e) / (1 - e), e = 130 * 2^-24
-    sure = s32 > b32 * kOrder + 1.0e-37f;       // false for NaN or an infinite b32
+    sure = finite && s32 > b32 * kOrder + 1.0e-37f;  // NaN distances: the fp64 chains decide
   }
   if (tok < n && !sure) {
+    // first strict minimum from +inf: NaN and infinite distances never win, and a token with
+    // no finite distance keeps label 0 (the oracle's rule)
     best = 0;
-    double best_d = 0.0;
+    double best_d = INFINITY;
     for (int c0 = 0; c0 < count; c0 += 8) {
       const double* cen = centers64 + (bh * CS + c0) * D;  // wave-uniform: scalar loads
       // distance_c = sum over d (in order) of fma(x_d - c_d, x_d - c_d, acc) in fp64
@@ -263,7 +271,7 @@ __global__ __launch_bounds__(kGroupThreads) void grp_assign_kernel(
       }
 #pragma unroll
       for (int c = 0; c < 8; ++c)
-        if (c0 + c < count && ((c0 == 0 && c == 0) || acc[c] < best_d)) {  // ties keep the lowest id
+        if (c0 + c < count && acc[c] < best_d) {  // ties keep the lowest id
           best_d = acc[c];
           best = c0 + c;
         }
@@ -554,9 +562,9 @@ void linspace_ids(int64_t n, int count, Ids& ids) {
 }  // namespace
 
 // Workspace of one grouping call: the larger of the two schedules' needs for this count
-// (count = min(clusters, N)); clusters <= 0 means the fused schedule's 8.
+// (count = min(clusters, N)); the caller has checked clusters in [1, 256].
 size_t ws_group(int64_t BH, int64_t N, int64_t D, int clusters) {
-  const int count = static_cast<int>(std::min<int64_t>(clusters > 0 ? clusters : kFusedClusters, N));
+  const int count = static_cast<int>(std::min<int64_t>(clusters, N));
   size_t bytes = group_ws(nullptr, BH, N, D, center_slots(count, true), true).bytes;
   if (count <= kFusedClusters) bytes = std::max(bytes, group_ws(nullptr, BH, N, D, kFusedClusters, false).bytes);
   return bytes;

@@ -168,6 +168,27 @@ def test_grouping_bit_exact(dim, dtype, n, clusters, iterations):
     np.testing.assert_array_equal(perm.cpu().numpy(), eperm)
 
 
+@pytest.mark.parametrize("dim", [64, 128])
+@pytest.mark.parametrize("clusters", [8, 16])
+@pytest.mark.parametrize("bad", ["nan", "inf"])
+def test_grouping_non_finite_values_follow_the_oracle(dim, clusters, bad):
+    # A non-finite V value gives NaN / infinite distances; the kernel's binary32 pre-pass must
+    # leave such tokens to the fp64 chains (ties and NaN compares resolve to the lowest id), so
+    # labels, centers and the permutation equal the oracle's. Reference assignment rule:
+    # clustering.cu:32-137 (first minimum wins).
+    _print_case("grouping non-finite", dim, clusters, bad)
+    g = torch.Generator().manual_seed(5 + dim + clusters)
+    v = torch.randn(1, 2, 700, dim, generator=g)
+    v[0, 0, 123, 7] = float(bad)
+    v[0, 1, 0, 3] = -float(bad) if bad == "inf" else float(bad)  # an initial center of head 1
+    v = v.to(torch.bfloat16)
+    perm, labels, centers = vcx.group_values(v.to(DEV), clusters, 2, debug=True)
+    eperm, elabels, ecenters = o.group_values(bits(v), clusters, 2, "bfloat16")
+    np.testing.assert_array_equal(labels.cpu().numpy(), elabels)
+    np.testing.assert_array_equal(perm.cpu().numpy(), eperm)
+    np.testing.assert_array_equal(centers.cpu().numpy(), ecenters)  # NaN == NaN here
+
+
 def _near_tie_values(dim, dtype, n=1024, seed=0):
     """[1,2,n,dim] V whose tokens sit at or near the bisector of the two initial centers
     (V[0] = -e_0 + w, V[n-1] = +e_0 + w, with the same random tail w in the other channels):
@@ -484,37 +505,21 @@ FULL = [  # name, B, H, N, D, kind: the BASELINE smoothing configurations in ful
 ]
 
 
-def _device_inputs(B, H, N, D, kind, seed=0):
-    """The BASELINE input recipes (bench.make_inputs) drawn by a seeded device generator:
-    N(0,1); "outlier": K + a per-(head, channel) N(0, var 4) offset, V = one of 8 per-head
-    N(0, var 2) centroids + N(0, var 0.3); "student": Q, K = 0.5 * Student-t(4) as
-    Z / sqrt(chi2_4 / 4)."""
-    g = torch.Generator(device=DEV).manual_seed(seed)
-    n = lambda *shape: torch.randn(*shape, generator=g, device=DEV)
-    if kind == "normal":
-        q, k, v = n(B, H, N, D), n(B, H, N, D), n(B, H, N, D)
-    elif kind == "outlier":
-        q, k = n(B, H, N, D), n(B, H, N, D) + n(B, H, 1, D) * 2.0
-        cent = n(B, H, 8, D) * 2.0 ** 0.5
-        ids = torch.randint(0, 8, (B, H, N, 1), generator=g, device=DEV)
-        v = torch.take_along_dim(cent, ids, dim=2) + n(B, H, N, D) * 0.3 ** 0.5
-    else:
-        t = lambda: n(B, H, N, D) / torch.sqrt(sum(n(B, H, N, D).square() for _ in range(4)) / 4)
-        q, k, v = 0.5 * t(), 0.5 * t(), n(B, H, N, D)
-    return tuple(x.to(torch.bfloat16).contiguous() for x in (q, k, v))
-
-
+@pytest.mark.timeout(900)  # the long case draws 2 x 270M Student-t values on one CPU core (~1 min)
 @pytest.mark.parametrize("case", FULL, ids=lambda c: c[0])
 def test_full_length_baseline_configs_all_heads(case):
-    # The BASELINE smoothing shapes in full (all 28 / 40 heads, full sequence length): the
-    # permutation, every Q8/K8/V8 byte, every scale and fp16 mean of every head; then P bytes
-    # and output of sampled rows (first, middle, ragged end) in every head.
+    # The BASELINE smoothing shapes in full (all 28 / 40 heads, full sequence length) on the
+    # very bytes bench.py times (bench.make_inputs: CPU torch.Generator seed 0, numpy PCG64
+    # Student-t for "long"): the permutation, every Q8/K8/V8 byte, every scale and fp16 mean
+    # of every head; then P bytes and output of sampled rows (first, middle, ragged end) in
+    # every head.
+    from bench import make_inputs
     from sageattention_local import forward_prepared, prepare
     name, B, H, N, D, kind = case
-    _print_case("full config, all heads", name, (B, H, N, D))
-    qd, kd, vd = _device_inputs(B, H, N, D, kind)
+    _print_case("full config, all heads, bench inputs", name, (B, H, N, D))
+    q, k, v = make_inputs(B, H, N, D, kind)
+    qd, kd, vd = (x.to(DEV) for x in (q, k, v))
     st = prepare(qd, kd, vd, v_smooth=True)
-    q, k, v = (x.cpu() for x in (qd, kd, vd))
     ost = _oracle_state(q, k, v, True, torch.bfloat16)
     np.testing.assert_array_equal(st["permutation"].cpu().numpy(), ost["permutation"])
     for key in ("q", "k", "qs", "ks", "vs"):
@@ -588,9 +593,10 @@ def test_main_config_all_heads_payloads_and_sampled_rows():
     # The benchmark's main workload in full ([1,28,37741,128] bf16, smoothing off): every
     # payload byte and scale of all 28 heads, and the P bytes / output of 8 query rows
     # spread over every head (first, last and ragged-block rows included).
+    from bench import make_inputs
     B, H, N, D = 1, 28, 37741, 128
-    _print_case("main config, all heads")
-    q, k, v = make_qkv(B, H, N, N, D, torch.bfloat16, seed=0)
+    _print_case("main config, all heads, bench inputs")
+    q, k, v = make_inputs(B, H, N, D, "normal")
     qd, kd, vd = (x.to(DEV) for x in (q, k, v))
     q8, qs, k8, ks, _ = vcx.prepare_qk(qd, kd)
     v8, vs, _ = vcx.prepare_v(vd)

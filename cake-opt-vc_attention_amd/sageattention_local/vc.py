@@ -19,9 +19,10 @@ Differences a caller can observe, all deliberate:
   unfused one (``AFFINE_MODES``).
 * The prepared ``v`` payload is stored in the gfx950 tile order
   (``vcx.value_token``), not Sage's 16-token permutation.
-* ``expcast=False`` runs the Sage FP8 control path (E4M3 probabilities from
-  the hardware exp2, unrounded exp2 mass); its P bytes can differ from an
-  exactly rounded exp2 next to an E4M3 rounding midpoint.
+* ``expcast=False`` runs the Sage FP8 control path: each P byte is the E4M3 of
+  the correctly rounded binary32 exp2 (hardware ``v_exp_f32``, rechecked in
+  binary64 where an E4M3 rounding midpoint lies within two ulps), so the bytes
+  are exact; the row mass sums the unrounded exp2 values.
 """
 import math
 
@@ -200,10 +201,51 @@ def sageattn_vc(q, k, v, tensor_layout="HND", is_causal=False, sm_scale=None, re
         return out_nhd if out_nhd is not None else result
 
 
+# The reference's kernel_resources names (vc_sm90.cu:801-808,1123-1213 and vc.py:113-118), each
+# mapped to the (value mode, probability mode) of the gfx950 kernel this module launches for
+# that mode at D128: value mode 0 = no block values, 1 = block values with channel scales;
+# probability mode 0 = Sage FP8 control, 1 = unfused ExpCast, 2 = folded ExpCast
+# (AFFINE_MODES without block values). "smooth_*" / "full_*" are the reference's
+# block-value kernels without / with ExpCast; the sage-layout and vc31/vc32 entries follow
+# forward_prepared's choice for those modes (sage-layout modes run as vc15).
+_FOLDED, _UNFUSED, _CONTROL = (0, 2), (0, 1), (0, 0)
+RESOURCE_MODES = {
+    "smooth_vc7": (1, 0), "smooth_optimized": (1, 0), "full_vc7": (1, 1), "full_optimized": (1, 1),
+    "expcast_vc9": _UNFUSED, "expcast_vc10": _UNFUSED, "expcast_vc11": _UNFUSED,
+    "expcast_vc12": _FOLDED, "expcast_vc14": _FOLDED, "expcast_vc15": _FOLDED, "expcast_serial": _FOLDED,
+    "expcast_optimized": _FOLDED, "expcast_vc13_overlap": _FOLDED,
+    **{f"control_sage_layout_{n}": _CONTROL for n in (*range(1, 5), *range(10, 38))},
+    **{f"expcast_sage_layout_{n}": _FOLDED for n in (1, 2, *range(5, 38))},
+    "vc31_smooth": (1, 0), "vc31_both": (1, 1), "vc32_full_smooth": (1, 0), "vc32_full_both": (1, 1),
+    "vc32_packed_smooth": (1, 0), "vc32_packed_both": (1, 1),
+}
+# Entries of this build without a reference name: the D64 kernels and the per-block-scale
+# (v_scale_mode="block", value mode 2) kernels.
+EXTRA_RESOURCE_MODES = {
+    "d64_expcast_optimized": (64, 0, 2), "d64_expcast_vc9": (64, 0, 1), "d64_control": (64, 0, 0),
+    "d64_full_optimized": (64, 1, 1), "d64_smooth_optimized": (64, 1, 0),
+    "block_scale_full": (128, 2, 1), "block_scale_smooth": (128, 2, 0),
+}
+
+
 def kernel_resources(output_type=1):
-    """Compiled resources of the fused kernels (reference vc.py:113-118)."""
+    """Compiled resources per kernel mode under the reference's names (vc.py:113-118,
+    vc_sm90.cu:786-822): registers_per_thread, local_bytes_per_thread (spill),
+    static/dynamic_shared_bytes, threads_per_block, predicted_active_blocks_per_sm
+    (per CU here). Each name reports the gfx950 kernel this module runs for that mode."""
+    if output_type not in (0, 1) or isinstance(output_type, bool):
+        raise RuntimeError("Output type must be 0 (FP16) or 1 (BF16)")
     ext = _extension()
-    return {f"{'smooth' if bv else 'full'}_d{d}": ext.kernel_resources(d, bv) for d in (64, 128) for bv in (False, True)}
+    cache = {}
+
+    def res(d, vm, pm):
+        if (d, vm, pm) not in cache:
+            cache[(d, vm, pm)] = ext.kernel_resources_mode(d, vm, pm, output_type)
+        return dict(cache[(d, vm, pm)])
+
+    out = {name: res(128, vm, pm) for name, (vm, pm) in RESOURCE_MODES.items()}
+    out.update({name: res(d, vm, pm) for name, (d, vm, pm) in EXTRA_RESOURCE_MODES.items()})
+    return out
 
 
 def sage_vc_build_info():
@@ -217,7 +259,9 @@ def sage_vc_build_info():
             "expcast_probability": "without block values (default modes): folded encode RNE(fmaf(score, RN(scale*A), "
                                    "fmaf(-m, A, B))) with the 16-row |m| <= 128 fallback; otherwise exact FP32 RN "
                                    "multiply/subtract + single-rounding FMA + saturating RNE byte",
-            "control_probability": "log2-domain FMA with the 8.807 offset, hardware exp2, RNE E4M3; unrounded mass",
+            "control_probability": "log2-domain FMA with the 8.807 offset; E4M3 (RNE) of the correctly rounded "
+                                   "binary32 exp2 (v_exp_f32, binary64 recheck next to E4M3 midpoints); "
+                                   "unrounded mass",
             "mass": "FP8 MFMA row sum with an all-ones operand (same accumulation as PV)",
             "v_layout": "gfx950_tile128", "kernel_modes": list(BASE_MODES) + list(SAGE_LAYOUT_MODES),
             "default_kernel_mode": "optimized"}

@@ -36,6 +36,7 @@ from pathlib import Path
 import torch
 
 from .core import Config, attention
+from .hip_backend import preflight
 
 # arm name -> (v_smooth, expcast)
 ARMS = {"fp8_control": (False, False), "expcast": (False, True), "v_smooth": (True, False), "combined": (True, True)}
@@ -169,6 +170,9 @@ def run(args):
         source = {"kind": "synthetic_clustered" if args.clustered else "synthetic_gaussian", "seed": args.seed}
         scale = args.dim ** -0.5
     q, query_range = select_queries(q, *args.queries)
+    # the backend's known answers before any arm, recorded in the report (reference
+    # replay.py:66-73,134); the argument and input checks above run first
+    preflight_result = preflight(args.device) if device.type == "cuda" else None
     q, k, v = (x.to(dtype).to(device).contiguous() for x in (q, k, v))
     exact = exact_attention(q, k, v, scale)
     configs = {name: Config(backend="hip", qk_format="int8", q_block=64, k_quant_block=128, kv_block=128,
@@ -184,6 +188,7 @@ def run(args):
         "device_name": torch.cuda.get_device_name(device) if device.type == "cuda" else platform.processor(),
         "torch": torch.__version__,
         "host": platform.platform(),
+        "preflight": preflight_result,
         "dtype": args.dtype,
         "shape_q": list(q.shape),
         "shape_k": list(k.shape),

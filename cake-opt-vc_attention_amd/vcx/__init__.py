@@ -15,7 +15,7 @@ from pathlib import Path
 
 import torch
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 LIB_PATH = Path(__file__).resolve().parents[1] / "lib" / "libvcx.so"
 
 _OK, _EINVAL, _EUNSUPPORTED, _EHIP = 0, 1, 2, 3
@@ -76,6 +76,8 @@ def _declare(L):
     L.vcx_convert_probe.argtypes = [P, P, P, i64, P]
     L.vcx_kernel_resources.restype = i32
     L.vcx_kernel_resources.argtypes = [i64, i32, ctypes.POINTER(ctypes.c_int64)]
+    L.vcx_kernel_resources_mode.restype = i32
+    L.vcx_kernel_resources_mode.argtypes = [i64, i32, i32, i32, ctypes.POINTER(ctypes.c_int64)]
     L.vcx_kernel_resources_fp8.restype = i32
     L.vcx_kernel_resources_fp8.argtypes = [i64, i32, ctypes.POINTER(ctypes.c_int64)]
 
@@ -84,7 +86,8 @@ EXPORTED = ("vcx_abi_version", "vcx_last_error", "vcx_value_token", "vcx_workspa
             "vcx_group_values", "vcx_prepare_qk_int8", "vcx_prepare_qk_int8_noalloc", "vcx_prepare_qk_int8_rotated",
             "vcx_preprocess_qk",
             "vcx_prepare_qk_fp8", "vcx_prepare_v_fp8", "vcx_attention_fwd", "vcx_attention_fwd_fp8",
-            "vcx_expcast_codes", "vcx_fp8_exp2_codes", "vcx_convert_probe", "vcx_kernel_resources", "vcx_kernel_resources_fp8",
+            "vcx_expcast_codes", "vcx_fp8_exp2_codes", "vcx_convert_probe", "vcx_kernel_resources", "vcx_kernel_resources_mode",
+            "vcx_kernel_resources_fp8",
             "vcx_clock_probe")
 
 
@@ -508,6 +511,17 @@ def clock_probe(window_us: int, device=None) -> ClockProbe:
     """Launch one wave that counts engine-clock ticks against the constant-rate real-time
     counter for `window_us` microseconds (asynchronous; read the result with .ghz())."""
     return ClockProbe(window_us, device)
+
+
+def kernel_resources_mode(D: int, value_mode: int, expcast: int, output_type: int = 1) -> dict:
+    """Compiled resources of the fused kernel one launch mode runs (value_mode 0: no block
+    values, 1: block values with channel scales, 2: per-block scales; expcast 0 control,
+    1 unfused ExpCast, 2 folded), in the reference's key names (vc_sm90.cu:786-797)."""
+    arr = (ctypes.c_int64 * 7)()
+    _check(lib().vcx_kernel_resources_mode(D, value_mode, expcast, 1 if output_type else 0, arr),
+           "vcx_kernel_resources_mode")
+    return {"registers_per_thread": arr[0], "local_bytes_per_thread": arr[5], "static_shared_bytes": arr[2],
+            "dynamic_shared_bytes": arr[3], "threads_per_block": arr[4], "predicted_active_blocks_per_sm": arr[6]}
 
 
 def kernel_resources(D: int = 128, block_values: bool = False, *, qk_fp8: bool = False,

@@ -37,7 +37,7 @@
 extern "C" {
 #endif
 
-#define VCX_ABI_VERSION 2
+#define VCX_ABI_VERSION 3
 #define VCX_CLOCK_PROBE_BLOCKS 8
 #define VCX_NOALLOC_SCRATCH_BYTES (32u << 20) /* scratch of vcx_prepare_qk_int8_noalloc, per GPU */
 
@@ -118,8 +118,11 @@ int vcx_prepare_qk_int8(const void* q, const void* k, int dtype, int64_t B, int6
  * outputs and results as vcx_prepare_qk_int8; shapes whose ws_prepare_qk workspace
  * (8*B*H*ceil(Nk/128)*D + 4*B*H*D bytes, 256-byte aligned slices) exceeds the scratch are
  * rejected with VCX_EINVAL. All calls on one GPU share the scratch: calls that overlap on one
- * GPU (concurrent streams or threads) race. No counterpart in the reference; for callers that
- * cannot allocate (code under HIP graph capture, allocation-free serving loops). */
+ * GPU (concurrent streams or threads) race. The array's device address is resolved once per
+ * device (hipGetSymbolAddress on the first call there) and kept: a hipDeviceReset or an
+ * unload of the library's code object in the same process invalidates it, so such a
+ * process must not call this entry point afterwards. No counterpart in the reference; for
+ * callers that cannot allocate (code under HIP graph capture, allocation-free serving loops). */
 int vcx_prepare_qk_int8_noalloc(const void* q, const void* k, int dtype, int64_t B, int64_t H,
                                 int64_t Nq, int64_t Nk, int64_t D, int64_t q_sb, int64_t q_sh,
                                 int64_t q_sn, int64_t k_sb, int64_t k_sh, int64_t k_sn,
@@ -183,8 +186,10 @@ int vcx_prepare_v_fp8(const void* v, int dtype, int64_t B, int64_t H, int64_t N,
  * expcast = 2: the folded ExpCast encode of the reference's default modes
  * (vc12..vc15, "optimized"; vc_math.cuh:16-111), only with block_values = 0, with the
  * reference's per-16-row-group fallback to the unfused bytes when some |m'| > 128.
- * expcast = 0: the Sage FP8 control path, P = E4M3(exp2(.)) with the 8.807 offset and
- * an unrounded exp2 mass (hardware exp2). block_values = 1 consumes means/vs as written by
+ * expcast = 0: the Sage FP8 control path, P = E4M3 of the correctly rounded binary32
+ * exp2 (v_exp_f32, rechecked in binary64 where an E4M3 rounding midpoint lies within two
+ * ulps; the bytes are exact) with the 8.807 offset, and the unrounded v_exp_f32 values
+ * summed as the row mass. block_values = 1 consumes means/vs as written by
  * vcx_prepare_v_fp8(smooth=1, channel_scale): channel_scale = 1 applies vs
  * [B,H,D] in the epilogue, channel_scale = 0 scales every tile's contribution
  * by its vs [B,H,tiles,D]; block_values = 0 uses vs [B,H,D], ignores means and
@@ -240,6 +245,16 @@ int vcx_convert_probe(const float* x, uint8_t* u8, uint8_t* f8, int64_t n, void*
  * out[5] scratch (spill) bytes per lane.
  * Replaces _vc_sm90.kernel_resources (third_party/sageattention_local/csrc/vc/vc_sm90.cu:786-822). */
 int vcx_kernel_resources(int64_t D, int block_values, int64_t* out);
+
+/* Compiled resources of the fused kernel that one launch mode runs: value_mode 0 (no
+ * block values), 1 (block values, channel scales), 2 (block values, per-block scales);
+ * expcast 0/1/2 as for vcx_attention_fwd (2 only with value_mode 0); out_dtype
+ * VCX_FLOAT16 / VCX_BFLOAT16. out[0..5] as for vcx_kernel_resources, out[6] the
+ * occupancy-predicted active blocks per CU (256 threads per block; a device call).
+ * Replaces the per-mode entries of _vc_sm90.kernel_resources(output_type)
+ * (third_party/sageattention_local/csrc/vc/vc_sm90.cu:786-822,1123-1160), which
+ * sageattention_local.kernel_resources maps onto the reference's mode names. */
+int vcx_kernel_resources_mode(int64_t D, int value_mode, int expcast, int out_dtype, int64_t* out);
 
 /* The same six values for the FP8 block QK kernel (expcast = 1: folded ExpCast,
  * 0: control). Replaces _vc_sm90.fp8_kernel_resources

@@ -27,7 +27,7 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_abi_version_and_value_order():
-    assert vcx.abi_version() == vcx.ABI_VERSION == 2
+    assert vcx.abi_version() == vcx.ABI_VERSION == 3
     tok = vcx.value_token()
     assert sorted(tok) == list(range(128))
     # closed form: position p = 32G + b holds token 16(b/4) + 8((b/2)%2) + 2G + b%2

@@ -153,3 +153,42 @@ def test_prepare_qk_rejects_k_that_does_not_match_q(no_native, fn, kshape):
     k = torch.zeros(*kshape, dtype=torch.bfloat16)
     with pytest.raises(vcx.VcxError, match="must match in batch, heads and head dim"):
         getattr(vcx, fn)(q, k)
+
+
+def test_kernel_resources_answer_under_the_reference_names(monkeypatch):
+    # reference vc.py:113-118 and vc_sm90.cu:801-808,1123-1213: callers read
+    # resources["expcast_optimized"], ["smooth_optimized"], ["expcast_sage_layout_35"], ...
+    calls = []
+
+    def fake(d, vm, pm, out_type):
+        calls.append((d, vm, pm, out_type))
+        return {"registers_per_thread": 100 * vm + 10 * pm + d // 64, "local_bytes_per_thread": 0,
+                "static_shared_bytes": 0, "dynamic_shared_bytes": 0, "threads_per_block": 256,
+                "predicted_active_blocks_per_sm": 2}
+
+    monkeypatch.setattr(api, "_extension", lambda: SimpleNamespace(kernel_resources_mode=fake))
+    res = api.kernel_resources(0)
+    reg = lambda name: res[name]["registers_per_thread"]
+    # folded ExpCast without block values: the default and vc12..vc15 modes, and the
+    # sage-layout modes (which run as vc15)
+    for name in ("expcast_optimized", "expcast_vc15", "expcast_vc14", "expcast_vc12", "expcast_vc13_overlap",
+                 "expcast_serial", "expcast_sage_layout_35", "expcast_sage_layout_1"):
+        assert reg(name) == 22, name
+    for name in ("expcast_vc9", "expcast_vc10", "expcast_vc11"):  # unfused ExpCast
+        assert reg(name) == 12, name
+    for name in ("control_sage_layout_1", "control_sage_layout_37"):  # control path
+        assert reg(name) == 2, name
+    # block values: "smooth" without ExpCast, "full" and vc31/vc32 "both" with it
+    for name in ("smooth_vc7", "smooth_optimized", "vc31_smooth", "vc32_full_smooth", "vc32_packed_smooth"):
+        assert reg(name) == 102, name
+    for name in ("full_vc7", "full_optimized", "vc31_both", "vc32_full_both", "vc32_packed_both"):
+        assert reg(name) == 112, name
+    assert reg("d64_expcast_optimized") == 21 and reg("block_scale_full") == 212
+    assert {c[3] for c in calls} == {0} and {c[0] for c in calls} == {64, 128}
+    assert len(calls) == len(set(calls))  # each kernel queried once
+    assert set(res["expcast_optimized"]) == {"registers_per_thread", "local_bytes_per_thread", "static_shared_bytes",
+                                             "dynamic_shared_bytes", "threads_per_block",
+                                             "predicted_active_blocks_per_sm"}
+    for bad in (2, -1, True):
+        with pytest.raises(RuntimeError, match="Output type"):
+            api.kernel_resources(bad)

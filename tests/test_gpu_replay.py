@@ -21,6 +21,8 @@ def test_four_arms_against_fp32_softmax(tmp_path, clustered):
     assert json.loads(out.read_text()) == json.loads(json.dumps(report))
     assert report["shape_q"] == [1, 2, 256, 128] and report["shape_k"] == [1, 2, 1536, 128]
     assert report["query_range"] == [128, 384]
+    # the backend's known answers ran first and are recorded (reference replay.py:66-73,134)
+    assert report["preflight"]["preflight"] == "passed"
     for name, row in report["arms"].items():
         m = row["metrics"]
         # INT8 QK + FP8 P/V: a few percent relative RMSE against the unquantized softmax

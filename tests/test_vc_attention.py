@@ -175,3 +175,10 @@ def test_other_backends_and_cpu_tensors_have_no_fallback():
         attention(q, k, v, Config(**HIP))
     with pytest.raises(ValueError, match="gfx950"):
         attention(*(x.to(torch.bfloat16) for x in (q, k, v)), Config(**HIP))
+
+
+def test_preflight_requires_a_gfx950_device():
+    # reference cuda_backend.py:101-102: the preflight refuses anything but its GPU class
+    from vc_attention import preflight
+    with pytest.raises(RuntimeError, match="gfx950"):
+        preflight("cpu")

@@ -125,7 +125,7 @@ def cpu_baseline(q, k, v, smooth, rows, budget_s, qk="int8", rotate=False):
                   f"({'evenly spaced 16-row groups, folded ExpCast encode' if affine else 'evenly spaced, ExpCast'}"
                   f"{', FP8 block QK' if qk == 'fp8' else ''}) "
                   f"x all {N} keys x {B * H} heads (P bytes + decoded-payload fp64 accumulation), OpenMP over rows; "
-                  f"value = 4*B*H*rows*N*D / time. Full preprocessing of the same inputs (single thread) "
+                  f"value = 4*B*H*rows*N*D / time. Full preprocessing of the same inputs (OpenMP over heads and channels) "
                   f"took {prep_s:.2f} s; extrapolated full forward = {full_s:.1f} s",
         "attention_s": attn_s,
         "prep_s": prep_s,
@@ -137,6 +137,82 @@ def cpu_baseline(q, k, v, smooth, rows, budget_s, qk="int8", rotate=False):
         "omp_threads": threads,
         "torch_threads": torch.get_num_threads(),
     }
+
+
+class PowerSampler:
+    """Board telemetry beside a launch loop (amdsmi, the library behind amd-smi): socket power,
+    per-XCD engine clocks, GFX rail voltage and temperatures every `period` seconds, and the
+    firmware's throttle-residency accumulators read at start and stop, which say what held
+    the clock below its maximum: PPT (package power), socket / VR / HBM thermal or PROCHOT.
+    Residency = delta of a reason's accumulator / delta of accumulation_counter."""
+
+    REASONS = ("ppt_residency_acc", "socket_thm_residency_acc", "vr_thm_residency_acc",
+               "hbm_thm_residency_acc", "prochot_residency_acc")
+
+    def __init__(self, torch_device, period=0.25):
+        import threading
+        import amdsmi
+        self.smi = amdsmi
+        amdsmi.amdsmi_init(amdsmi.AmdSmiInitFlags.INIT_AMD_GPUS)
+        handles = amdsmi.amdsmi_get_processor_handles()
+        self.handle = handles[0]
+        try:  # the handle whose PCI bus matches the torch device (a box may list more GPUs)
+            import torch
+            bus = torch.cuda.get_device_properties(torch_device).pci_bus_id
+            for h in handles:
+                if int(amdsmi.amdsmi_get_gpu_device_bdf(h).split(":")[1], 16) == bus:
+                    self.handle = h
+        except Exception:
+            pass
+        self.period, self.samples, self.stop_ev = period, [], threading.Event()
+        self.thread = threading.Thread(target=self._run, daemon=True)
+
+    def _metrics(self):
+        return self.smi.amdsmi_get_gpu_metrics_info(self.handle)
+
+    def _run(self):
+        while not self.stop_ev.wait(self.period):
+            m = self._metrics()
+            self.samples.append({k: m.get(k) for k in ("current_socket_power", "current_gfxclks", "voltage_gfx",
+                                                        "temperature_hotspot", "temperature_vrgfx",
+                                                        "throttle_status", "indep_throttle_status")})
+
+    def start(self):
+        self.t0, self.m0 = time.perf_counter(), self._metrics()
+        self.thread.start()
+        return self
+
+    def stop(self):
+        self.stop_ev.set()
+        self.thread.join()
+        m1, t1 = self._metrics(), time.perf_counter()
+        num = lambda x: x if isinstance(x, (int, float)) else None
+        dacc = (num(m1.get("accumulation_counter")) or 0) - (num(self.m0.get("accumulation_counter")) or 0)
+        residency = {}
+        for r in self.REASONS:
+            a, b = num(self.m0.get(r)), num(m1.get(r))
+            residency[r.replace("_residency_acc", "")] = round((b - a) / dacc, 4) if dacc > 0 and a is not None and b is not None else None
+        s = [x for x in self.samples if isinstance(x["current_socket_power"], (int, float))]
+        mean = lambda xs: round(sum(xs) / len(xs), 1) if xs else None
+        clocks = [x["current_gfxclks"] for x in s if isinstance(x["current_gfxclks"], list)]
+        xcd = [mean([c[i] for c in clocks if isinstance(c[i], (int, float))]) for i in range(8)] if clocks else None
+        caps = {}
+        for ind, name in ((0, "ppt0"), (1, "ppt1")):
+            try:
+                ci = self.smi.amdsmi_get_power_cap_info(self.handle, ind)
+                caps[name] = {k: ci[k] / 1e6 if isinstance(ci[k], (int, float)) else ci[k] for k in ("power_cap", "default_power_cap", "max_power_cap")}
+            except Exception as e:  # a sensor the board does not have
+                caps[name] = str(e)[:80]
+        return {"window_s": round(t1 - self.t0, 2), "samples": len(s),
+                "socket_power_w_mean": mean([x["current_socket_power"] for x in s]),
+                "socket_power_w_max": max((x["current_socket_power"] for x in s), default=None),
+                "gfxclk_mhz_per_xcd_mean": xcd,
+                "voltage_gfx_mv_mean": mean([x["voltage_gfx"] for x in s if isinstance(x["voltage_gfx"], (int, float))]),
+                "temperature_hotspot_c_max": max((x["temperature_hotspot"] for x in s if isinstance(x["temperature_hotspot"], (int, float))), default=None),
+                "temperature_vrgfx_c_max": max((x["temperature_vrgfx"] for x in s if isinstance(x["temperature_vrgfx"], (int, float))), default=None),
+                "throttle_status_seen": sorted({str(x["throttle_status"]) for x in s}),
+                "indep_throttle_status_seen": sorted({str(x["indep_throttle_status"]) for x in s}),
+                "throttle_residency": residency, "accumulation_ticks": dacc, "power_caps_w": caps}
 
 
 def cpu_model():
@@ -172,6 +248,9 @@ def main():
     ap.add_argument("--ready-file", default=None,
                     help="kernel mode: create this file when the launch loop starts (a power or clock "
                          "sampler running beside the benchmark waits for it)")
+    ap.add_argument("--power", action="store_true",
+                    help="kernel mode: sample board power, engine clocks and the firmware's throttle "
+                         "residency (amdsmi) over the timed launches")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build runs the sageattn_vc path on ONE GPU; multi-GPU runs are not part of it "
@@ -232,10 +311,19 @@ def main():
         torch.cuda.synchronize()
         if args.ready_file:
             Path(args.ready_file).write_text("launching\n")
-        for _ in range(args.warmup + args.steps):
+        for _ in range(args.warmup):
             fused(p)
         torch.cuda.synchronize()
-        print(json.dumps({"mode": "kernel", "launches": args.warmup + args.steps, "config": args.config}))
+        sampler = PowerSampler(dev).start() if args.power else None
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            fused(p)
+        torch.cuda.synchronize()
+        res = {"mode": "kernel", "launches": args.warmup + args.steps, "config": args.config,
+               "ms_per_timed_launch": round((time.perf_counter() - t0) * 1e3 / max(args.steps, 1), 4)}
+        if sampler is not None:
+            res["power"] = sampler.stop()
+        print(json.dumps(res), flush=True)
         return
     for _ in range(args.warmup):
         fused(prep())

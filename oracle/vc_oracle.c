@@ -342,9 +342,11 @@ VCO_EXPORT int vco_group_values(const uint16_t* v, int dtype, int64_t BH, int64_
 VCO_EXPORT void vco_k_mean(const uint16_t* k, int dtype, int64_t BH, int64_t n, int D,
                            const int64_t* perm, uint16_t* km) {
   int64_t tiles = (n + 127) / 128;
-  double x[128];
+  /* every (head, channel) mean is independent: threads split them, results unchanged */
+#pragma omp parallel for schedule(static) collapse(2)
   for (int64_t h = 0; h < BH; ++h) {
     for (int d = 0; d < D; ++d) {
+      double x[128];
       double s = 0.0;
       for (int64_t t = 0; t < tiles; ++t) {
         for (int i = 0; i < 128; ++i) {
@@ -473,7 +475,11 @@ static inline int8_t int8_code(float x, float s) {
 static void quant_q_rows(const uint16_t* q, int dtype, int64_t BH, int64_t n, int D, int rotate,
                          int8_t* q8, float* qs) {
   int64_t groups16 = (n + 63) / 64 * 4;
+  /* groups are independent: threads split (head, group); each thread has its own rows */
+#pragma omp parallel
+  {
   float* rows = (float*)malloc(sizeof(float) * 2 * D);
+#pragma omp for schedule(static) collapse(2)
   for (int64_t h = 0; h < BH; ++h) {
     for (int64_t g = 0; g < groups16; ++g) {
       for (int t = 0; t < 8; ++t) {
@@ -496,6 +502,7 @@ static void quant_q_rows(const uint16_t* q, int dtype, int64_t BH, int64_t n, in
     }
   }
   free(rows);
+  }
 }
 
 VCO_EXPORT void vco_quant_q(const uint16_t* q, int dtype, int64_t BH, int64_t n, int D,
@@ -519,7 +526,11 @@ VCO_EXPORT void vco_quant_q_rot(const uint16_t* q, int dtype, int64_t BH, int64_
 static void quant_k_rows(const uint16_t* k, int dtype, int64_t BH, int64_t n, int D,
                          const int64_t* perm, const uint16_t* km, int rotate, int8_t* k8, float* ks) {
   int64_t tiles = (n + 127) / 128;
+  /* tiles are independent: threads split (head, tile); each thread has its own buffer */
+#pragma omp parallel
+  {
   float* buf = (float*)malloc(sizeof(float) * 32 * D);
+#pragma omp for schedule(static) collapse(2)
   for (int64_t h = 0; h < BH; ++h) {
     for (int64_t j = 0; j < tiles; ++j) {
       for (int t = 0; t < 4; ++t) {
@@ -552,6 +563,7 @@ static void quant_k_rows(const uint16_t* k, int dtype, int64_t BH, int64_t n, in
     }
   }
   free(buf);
+  }
 }
 
 VCO_EXPORT void vco_quant_k(const uint16_t* k, int dtype, int64_t BH, int64_t n, int D,
@@ -577,9 +589,10 @@ VCO_EXPORT void vco_quant_k_rot(const uint16_t* k, int dtype, int64_t BH, int64_
 VCO_EXPORT void vco_k_mean_f32(const uint16_t* k, int dtype, int64_t BH, int64_t n, int D,
                                float* km) {
   int64_t tiles = (n + 127) / 128;
-  double x[128];
+#pragma omp parallel for schedule(static) collapse(2)
   for (int64_t h = 0; h < BH; ++h) {
     for (int d = 0; d < D; ++d) {
+      double x[128];
       double s = 0.0;
       for (int64_t t = 0; t < tiles; ++t) {
         for (int i = 0; i < 128; ++i) {
@@ -601,6 +614,7 @@ VCO_EXPORT void vco_k_mean_f32(const uint16_t* k, int dtype, int64_t BH, int64_t
 VCO_EXPORT void vco_quant_fp8_block(const uint16_t* x, int dtype, int64_t BH, int64_t n, int D,
                                     int rows, const float* mean, uint8_t* codes, float* scales) {
   const int64_t blocks = (n + rows - 1) / rows;
+#pragma omp parallel for schedule(static) collapse(2)
   for (int64_t h = 0; h < BH; ++h) {
     for (int64_t b = 0; b < blocks; ++b) {
       float amax = 0.0f;
@@ -638,6 +652,7 @@ VCO_EXPORT void vco_quant_fp8_block(const uint16_t* x, int dtype, int64_t BH, in
 VCO_EXPORT void vco_quant_v_channel(const uint16_t* v, int dtype, int64_t BH, int64_t n, int D,
                                     const int64_t* perm, uint8_t* v8, float* vs) {
   int64_t npad = (n + 127) / 128 * 128;
+#pragma omp parallel for schedule(static) collapse(2)
   for (int64_t h = 0; h < BH; ++h) {
     for (int d = 0; d < D; ++d) {
       float amax = 0.0f;
@@ -680,10 +695,14 @@ VCO_EXPORT void vco_quant_v_smooth(const uint16_t* v, int dtype, int64_t BH, int
                                    const int64_t* perm, int channel_scale, uint8_t* v8, float* vs,
                                    uint16_t* means) {
   int64_t tiles = (n + 127) / 128, npad = tiles * 128;
+  /* (head, channel) pairs are independent: threads split them with private buffers */
+#pragma omp parallel
+  {
   float* mean = (float*)malloc(sizeof(float) * tiles);
   float* peak = (float*)malloc(sizeof(float) * tiles);
   float* xs = (float*)malloc(sizeof(float) * npad);
   double x[128];
+#pragma omp for schedule(static) collapse(2)
   for (int64_t h = 0; h < BH; ++h) {
     for (int d = 0; d < D; ++d) {
       for (int64_t t = 0; t < npad; ++t) {
@@ -728,6 +747,7 @@ VCO_EXPORT void vco_quant_v_smooth(const uint16_t* v, int dtype, int64_t BH, int
     }
   }
   free(mean); free(peak); free(xs);
+  }
 }
 
 /* ------------------------------------------------------------------ */

@@ -359,7 +359,7 @@ def main():
     prep_gbs = prep_bytes / (prep_med * 1e-3) / 1e9
     result = {
         "metric": ("sageattn_vc_fp8 (FP8 block QK) " if fp8 else "sageattn_vc ")
-                  + "fused-kernel TOPS at BNSD [1,28,37741,128] bf16 (4*B*H*N^2*D / kernel time); "
+                  + f"fused-kernel TOPS at BNSD [{B},{H},{N},{D}] bf16 (4*B*H*N^2*D / kernel time); "
                   "kernel ms and fraction of INT8/FP8 MFMA peak",
         "value": round(tops, 2),
         "unit": "TOPS",

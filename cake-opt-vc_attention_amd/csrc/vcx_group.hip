@@ -37,8 +37,49 @@ struct Ids {
   int32_t v[kMaxClusters];
 };
 
+// A workgroup barrier that orders LDS accesses only. __syncthreads() also waits for every
+// outstanding global load of the wave, which would drain the next tile's loads at each
+// barrier of the current tile. The assignment kernel shares data between its threads
+// through LDS alone.
+__device__ inline void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// Whether an assignment block runs a run of tiles, loading the next tile during the
+// current one (else one tile per block).
+constexpr bool assign_prefetch(int dt, bool general, bool wide) { return !general && dt == VCX_BFLOAT16 && wide; }
+
+typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+
 __device__ inline const uint16_t* head_ptr(const void* x, int64_t bh, int64_t H, int64_t sb, int64_t sh) {
   return reinterpret_cast<const uint16_t*>(x) + (bh / H) * sb + (bh % H) * sh;
+}
+
+// The fused schedule's centers also in the form its bf16 dot-product pre-pass reads: each
+// fp32 value c as two bf16 parts, hi = RN_bf16(c) and lo = RN_bf16(c - hi) (the
+// subtraction is exact), so |c - hi - lo| <= 2^-18 |c|, parts [BH][8][2][D] (bf16 bits);
+// and the norms |c|^2 [BH][8], RN_f32 of the fp64 sum of the D squares (each exact; the
+// summation order is free: only its error bound, far below 2^-24 relative, enters the
+// pre-pass).
+struct CenterForms {
+  uint16_t* parts;
+  float* norms;
+};
+
+__device__ inline void store_center_parts(float x, int64_t slot, int d, int D, const CenterForms& f) {
+  const uint32_t hi = f32_to_bf16_bits(x);
+  f.parts[slot * 2 * D + d] = static_cast<uint16_t>(hi);
+  f.parts[slot * 2 * D + D + d] = static_cast<uint16_t>(f32_to_bf16_bits(__fsub_rn(x, bf16_bits_to_f32(hi))));
+}
+
+__device__ inline void store_center_norm(const double* red, int64_t slot, int D, const CenterForms& f) {
+  double t = 0.0;
+  for (int i = 0; i < D; ++i) t += red[i];
+  f.norms[slot] = static_cast<float>(t);
 }
 
 // Centers are kept as fp32 (the contract's values) and as their exact fp64 widening,
@@ -48,7 +89,8 @@ __device__ inline const uint16_t* head_ptr(const void* x, int64_t bh, int64_t H,
 template <int DT>
 __global__ void grp_init_kernel(const void* v, int64_t H, int64_t sb, int64_t sh, int64_t sn, Ids ids,
                                 int count, int CS, int D, const float* centers_in, float* centers,
-                                double* centers64) {
+                                double* centers64, CenterForms forms) {
+  __shared__ double red[kFusedClusters][128];  // squares, for the norms (CS = 8 with forms)
   const int64_t bh = blockIdx.x;
   const uint16_t* base = head_ptr(v, bh, H, sb, sh);
   const int d = threadIdx.x;
@@ -57,6 +99,14 @@ __global__ void grp_init_kernel(const void* v, int64_t H, int64_t sb, int64_t sh
     if (c < count) x = centers_in ? centers_in[(bh * count + c) * D + d] : in_to_f32<DT>(base[ids.v[c] * sn + d]);
     centers[(bh * CS + c) * D + d] = x;
     centers64[(bh * CS + c) * D + d] = static_cast<double>(x);
+    if (forms.parts) {
+      store_center_parts(x, bh * CS + c, d, D, forms);
+      red[c][d] = static_cast<double>(x) * static_cast<double>(x);
+    }
+  }
+  if (forms.parts) {
+    __syncthreads();
+    if (d < CS) store_center_norm(red[d], bh * CS + d, D, forms);
   }
 }
 
@@ -64,130 +114,229 @@ __global__ void grp_init_kernel(const void* v, int64_t H, int64_t sb, int64_t sh
 // per-cluster counts (pcnt, CS slots per tile). Fused schedule (!GENERAL, count <= 8):
 // with STATS also the tile's per-cluster fp64 channel sums. General schedule: counts from
 // an LDS histogram.
-// The tile is staged through LDS with coalesced loads; each thread then reads its token's
-// row 16 bytes at a time and runs the distance chains of 8 clusters side by side (d
-// outermost), chunk after chunk of 8 centers, in binary32 and, where that does not settle
-// the argmin, in fp64. The fused schedule's binary32 centers sit in LDS channel-major and
-// come through broadcast reads (as scalar operands, 8 centers x 16 channels outgrew the
-// SGPRs and spilled into VGPR lanes); the general schedule and the fp64 chains read them
-// through scalar loads.
+// The tile is staged through LDS with coalesced loads. On bf16 rows the fused schedule
+// first runs a dot-product pre-pass on the MFMA. Where that does not settle a token, each
+// thread reads its token's row 16 bytes at a time and runs the distance chains of 8
+// clusters side by side (d outermost), chunk after chunk of 8 centers, in binary32 and,
+// where that does not settle the argmin either, in fp64. The fused schedule's binary32
+// centers sit in LDS channel-major at D64 and behind the bf16 pre-pass, and come through
+// broadcast reads (as scalar operands, 8 centers x 16 channels outgrew the SGPRs and
+// spilled into VGPR lanes); the fp16 D128 fused schedule, the general schedule and their
+// fp64 chains read them through scalar loads.
 template <int DT, int D, bool STATS, bool WIDE, bool GENERAL>
 __global__ __launch_bounds__(kGroupThreads) void grp_assign_kernel(
     const void* v, int64_t H, int64_t n, int64_t sb, int64_t sh, int64_t sn, int count, int CS,
-    const float* __restrict__ centers32, const double* __restrict__ centers64, int32_t* labels, double* psum,
-    int32_t* pcnt) {
+    const float* __restrict__ centers32, const double* __restrict__ centers64, CenterForms forms,
+    int32_t* labels, double* psum, int32_t* pcnt, int64_t tiles, int64_t items, int64_t per) {
   constexpr int kStride = D + 8;  // 16-bit elements per staged row (16-byte aligned rows)
-  __shared__ __attribute__((aligned(16))) uint16_t xs[kTile * kStride];
-  const int64_t tile = blockIdx.x, bh = blockIdx.y, tiles = gridDim.x;
+  constexpr bool FS = STATS && !GENERAL;  // per-cluster sums: one more row, of zeros (padding)
+  __shared__ __attribute__((aligned(16))) uint16_t xs[(kTile + (FS ? 1 : 0)) * kStride];
   const int tid = threadIdx.x;
-  const uint16_t* base = head_ptr(v, bh, H, sb, sh);
-  // Stage the tile with coalesced loads, all of a thread's loads issued before
-  // its LDS stores: 16-byte pieces when every row is 16-byte aligned (WIDE),
-  // else 4-byte pieces.
-  if constexpr (WIDE) {
-    constexpr int kPieces = D / 8, kPer = kTile * kPieces / kGroupThreads;
-    uint4 val[kPer];
-#pragma unroll
-    for (int k = 0; k < kPer; ++k) {
-      const int s = tid + k * kGroupThreads, row = s / kPieces, part = s % kPieces;
-      const int64_t tok = tile * kTile + row;
-      val[k] = tok < n ? *reinterpret_cast<const uint4*>(base + tok * sn + 8 * part) : make_uint4(0, 0, 0, 0);
-    }
-#pragma unroll
-    for (int k = 0; k < kPer; ++k) {
-      const int s = tid + k * kGroupThreads, row = s / kPieces, part = s % kPieces;
-      *reinterpret_cast<uint4*>(&xs[row * kStride + 8 * part]) = val[k];
-    }
-  } else {
-    constexpr int kPieces = D / 2, kPer = kTile * kPieces / kGroupThreads;
-    uint32_t val[kPer];
-#pragma unroll
-    for (int k = 0; k < kPer; ++k) {
-      const int s = tid + k * kGroupThreads, row = s / kPieces, part = s % kPieces;
-      const int64_t tok = tile * kTile + row;
-      val[k] = tok < n ? *reinterpret_cast<const uint32_t*>(base + tok * sn + 2 * part) : 0u;
-    }
-#pragma unroll
-    for (int k = 0; k < kPer; ++k) {
-      const int s = tid + k * kGroupThreads, row = s / kPieces, part = s % kPieces;
-      *reinterpret_cast<uint32_t*>(&xs[row * kStride + 2 * part]) = val[k];
-    }
+  // bf16 rows, fused schedule: a dot-product pre-pass on the MFMA settles most tokens
+  // (below); with 16-byte rows each block also runs several tiles with the next one's
+  // loads in flight
+  constexpr bool MF = !GENERAL && DT == VCX_BFLOAT16, PREFETCH = assign_prefetch(DT, GENERAL, WIDE);
+  // items (head, tile) first .. last - 1, in order: consecutive tiles of a head (one item
+  // per block without the prefetch)
+  const int64_t first = blockIdx.x * (PREFETCH ? per : 1);
+  const int64_t last = PREFETCH ? (first + per < items ? first + per : items) : first + 1;
+  if (first >= items) return;
+  if constexpr (FS) {
+    if (tid < kStride / 8) *reinterpret_cast<uint4*>(&xs[kTile * kStride + 8 * tid]) = make_uint4(0, 0, 0, 0);
   }
+  // Staging: coalesced loads of a tile into registers, then stored to LDS once every reader
+  // of the previous tile is done. Behind the bf16 pre-pass (whose block runs several tiles)
+  // the next tile's loads are issued before the current tile's work, so that their latency
+  // overlaps it; elsewhere a block runs one tile and the registers stay free for the
+  // chains. 16-byte pieces when every row is 16-byte aligned (WIDE), else 4-byte pieces; a
+  // full tile (every tile but a partial last one) loads without per-row tests.
+  using Piece = std::conditional_t<WIDE, uint4, uint32_t>;
+  constexpr int kElems = WIDE ? 8 : 2, kPieces = D / kElems, kPer = kTile * kPieces / kGroupThreads;
+  Piece val[kPer];
+  auto load = [&](int64_t item) {
+    const int64_t tile = item % tiles;
+    const uint16_t* base = head_ptr(v, item / tiles, H, sb, sh);
+    if ((tile + 1) * kTile <= n) {
+#pragma unroll
+      for (int k = 0; k < kPer; ++k) {
+        const int s = tid + k * kGroupThreads, row = s / kPieces, part = s % kPieces;
+        val[k] = *reinterpret_cast<const Piece*>(base + (tile * kTile + row) * sn + kElems * part);
+      }
+    } else {
+#pragma unroll
+      for (int k = 0; k < kPer; ++k) {
+        const int s = tid + k * kGroupThreads, row = s / kPieces, part = s % kPieces;
+        const int64_t tok = tile * kTile + row;
+        val[k] = tok < n ? *reinterpret_cast<const Piece*>(base + tok * sn + kElems * part) : Piece{};
+      }
+    }
+  };
   __shared__ int hist[GENERAL ? kMaxClusters : 1];
-  if constexpr (GENERAL) {
-    for (int c = tid; c < count; c += kGroupThreads) hist[c] = 0;
-  }
-  // Fused schedule: the head's 8 binary32 centers, channel-major ([d][8]), so that one
+  // Fused schedule at D64, and at D128 behind the bf16 pre-pass (where the chains are the
+  // rare path): the head's 8 binary32 centers, channel-major ([d][8]), so that one
   // wave-uniform (broadcast) 16-byte LDS read gives four clusters' values of a channel.
-  constexpr bool LDSC = !GENERAL && D == 64;
+  constexpr bool LDSC = !GENERAL && (D == 64 || DT == VCX_BFLOAT16);
   __shared__ __attribute__((aligned(16))) float cl[LDSC ? kFusedClusters * D : 4];
-  if constexpr (LDSC) {
-    const float* src = centers32 + bh * kFusedClusters * D;
-    for (int e = tid; e < kFusedClusters * D; e += kGroupThreads) cl[(e % D) * kFusedClusters + e / D] = src[e];
-  }
-  __syncthreads();
-  const int64_t tok = tile * kTile + tid;
-  int best = 0;
-  // The label is the argmin of the fp64 distances. The same distances are first formed in
-  // binary32 (x - c rounded, then a fused multiply-add chain): every term is non-negative,
-  // so each binary32 distance lies within (D + 2) * 2^-24 relative (plus a subnormal-sized
-  // absolute term) of the exact one. When the second smallest exceeds the smallest by more
-  // than twice that bound, the exact and the fp64 distances order the same way and the
-  // binary32 argmin is the label; otherwise (ties, near ties, overflow) the lane takes the
-  // fp64 chains below.
-  bool sure = false;
-  if (tok < n && LDSC) {
-    float b32 = INFINITY, s32 = INFINITY;
-    float acc[8];
+  // bf16 pre-pass state of the current head (fused schedule): the A operand (row r < 8
+  // holds cluster r's hi part, row r >= 8 cluster r - 8's lo part; lane group G holds
+  // channels 8G..8G+7 of each 32-channel step) and the norms of the four clusters whose
+  // result rows this lane receives (clusters 4(G & 1)..+3).
+  constexpr int KS = D / 32;
+  const int lane = tid & 63, G = lane >> 4, r = lane & 15, w = tid >> 6;
+  v8bf af[KS];
+  float cn[4];
+  if constexpr (PREFETCH) load(first);
+  int64_t head = -1;
+  for (int64_t item = first; item < last; ++item) {
+    const int64_t tile = item % tiles, bh = item / tiles;
+    if constexpr (!PREFETCH) load(item);
+    lds_barrier();  // every reader of the previous tile is done
 #pragma unroll
-    for (int c = 0; c < 8; ++c) acc[c] = 0.0f;
-    const float4* cl4 = reinterpret_cast<const float4*>(cl);
-#pragma unroll 2
-    for (int i = 0; i < D / 8; ++i) {
-      const uint4 q = *reinterpret_cast<const uint4*>(&xs[tid * kStride + 8 * i]);
-      const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+    for (int k = 0; k < kPer; ++k) {
+      const int s = tid + k * kGroupThreads, row = s / kPieces, part = s % kPieces;
+      *reinterpret_cast<Piece*>(&xs[row * kStride + kElems * part]) = val[k];
+    }
+    if constexpr (GENERAL) {
+      for (int c = tid; c < count; c += kGroupThreads) hist[c] = 0;
+    }
+    if (bh != head) {
+      head = bh;
+      if constexpr (LDSC) {
+        const float* src = centers32 + bh * kFusedClusters * D;
+        for (int e = tid; e < kFusedClusters * D; e += kGroupThreads) cl[(e % D) * kFusedClusters + e / D] = src[e];
+      }
+      if constexpr (MF) {
+        const int cr = r & 7;
+        const uint16_t* part = forms.parts + ((bh * kFusedClusters + cr) * 2 + (r >> 3)) * D;
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const int d = 8 * i + 2 * k;
-        const float x0 = in_to_f32<DT>(w[k] & 0xffffu), x1 = in_to_f32<DT>(w[k] >> 16);
-        const float4 a0 = cl4[2 * d], a1 = cl4[2 * d + 1], b0 = cl4[2 * d + 2], b1 = cl4[2 * d + 3];
-        const float c0v[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
-        const float c1v[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
-#pragma unroll
-        for (int c = 0; c < 8; ++c) {
-          const float d0 = __fsub_rn(x0, c0v[c]);
-          acc[c] = __fmaf_rn(d0, d0, acc[c]);
-          const float d1 = __fsub_rn(x1, c1v[c]);
-          acc[c] = __fmaf_rn(d1, d1, acc[c]);
+        for (int k = 0; k < KS; ++k) {
+          uint4 a = make_uint4(0, 0, 0, 0);
+          if (cr < count) a = *reinterpret_cast<const uint4*>(part + 32 * k + 8 * G);
+          af[k] = __builtin_bit_cast(v8bf, a);
         }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int c = 4 * (G & 1) + j;
+          cn[j] = c < count ? forms.norms[bh * kFusedClusters + c] : 0.0f;
+        }
+        // wait for these loads here: a use of the values on this path keeps the compiler
+        // from waiting for every load (the next tile's included) where the tile work uses
+        // them
+        asm volatile("" ::"v"(af[0]), "v"(cn[0]), "v"(cn[1]), "v"(cn[2]), "v"(cn[3]));
+#pragma unroll
+        for (int k = 1; k < KS; ++k) asm volatile("" ::"v"(af[k]));
       }
     }
-    bool finite = true;  // a NaN distance (NaN in V or a center) fails every compare below
+    lds_barrier();
+    if constexpr (PREFETCH) {
+      if (item + 1 < last) load(item + 1);
+    }
+    const int64_t tok = tile * kTile + tid;
+    int best = 0;
+    // The label is the argmin of the fp64 distances. The same distances are first formed in
+    // binary32 (x - c rounded, then a fused multiply-add chain): every term is non-negative,
+    // so each binary32 distance lies within (D + 2) * 2^-24 relative (plus a subnormal-sized
+    // absolute term) of the exact one. When the second smallest exceeds the smallest by more
+    // than twice that bound, the exact and the fp64 distances order the same way and the
+    // binary32 argmin is the label; otherwise (ties, near ties, overflow) the lane takes the
+    // fp64 chains below.
+    bool sure = false;
+    // bf16 rows, fused schedule: the dot-product pre-pass. distance_c = X + C_c - 2 P_c with
+    // X = |x|^2 (bf16 dot2 chains of exact squares, then the four lane groups' partial sums;
+    // each of its D/8 + 2 steps allowed an error of 2u, so within D u X), C_c = |c|^2
+    // (precomputed) and P_c = x.c on the bf16 MFMA: x is exact in bf16 and c enters as its
+    // two bf16 parts, so every product is exact in fp32. With A = sum |x_d c_d| <= (X + C) /
+    // 2, each of the D + D/32 accumulations of either part allowed an error of 2u (u = 2^-24,
+    // whatever the MFMA's internal order, rounding or denormal flushing), the parts' 2^-18 |c|
+    // and the roundings of C, S = X + C, P and S - 2P, the computed
+    // distance lies within ((3D + 2D/32 + 8) u + 2^-18) S + 1e-30 of the exact one; kKappa is
+    // that factor with a 2 % margin. A token whose best center b (lowest id on equal values)
+    // has D_b + E_b < D_c - E_c for every other center c has b as its exact argmin, with a gap
+    // about 10^7 times the fp64 chains' own error, so b is the fp64 argmin too. Ties, near
+    // ties and non-finite values go on to the binary32 and fp64 chains below.
+    if constexpr (MF) {
+      constexpr float kKappa = ((3 * D + 2 * KS + 8) * 5.9604645e-8f + 3.8146973e-6f) * 1.02f;
+      __shared__ uint8_t pre[kTile];  // the pre-pass's label, bit 7 set when it is settled
+#pragma unroll 1
+      for (int nb = 0; nb < 4; ++nb) {
+        const int t = 64 * w + 16 * nb + r;  // this lane's B column: token t of the tile
+        v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
+        float x2 = 0.0f;
 #pragma unroll
-    for (int c = 0; c < 8; ++c)
-      if (c < count) {
-        finite = finite && acc[c] >= 0.0f;
-        if (acc[c] < b32) {  // ties keep the lowest id (and make the order unsure)
-          s32 = b32;
-          b32 = acc[c];
-          best = c;
-        } else if (acc[c] < s32) {
-          s32 = acc[c];
+        for (int k = 0; k < KS; ++k) {
+          const uint4 q = *reinterpret_cast<const uint4*>(&xs[t * kStride + 32 * k + 8 * G]);
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[k], __builtin_bit_cast(v8bf, q), acc, 0, 0, 0);
+          const uint32_t wq[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            x2 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(v2bf, wq[e]), __builtin_bit_cast(v2bf, wq[e]), x2, false);
         }
+        // Sums over lane pairs: a permlane swap returns {own, partner} on the lower lane
+        // group of each pair and {partner, own} on the upper one, and both add the same two
+        // values (addition is commutative), so every lane of a token holds the same X and P.
+        {
+          const auto s16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(x2), __float_as_uint(x2), false, false);
+          x2 = __uint_as_float(s16[0]) + __uint_as_float(s16[1]);
+          const auto s32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(x2), __float_as_uint(x2), false, false);
+          x2 = __uint_as_float(s32[0]) + __uint_as_float(s32[1]);
+        }
+        // D_c and E_c of this lane's four clusters; a non-finite D_c or E_c becomes NaN (it then
+        // fails every comparison below), a slot past count +inf with E = 0 (never the best,
+        // always separated)
+        float dd[4], ee[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const auto s = __builtin_amdgcn_permlane32_swap(__float_as_uint(acc[j]), __float_as_uint(acc[j]), false, false);
+          const float p = __fadd_rn(__uint_as_float(s[0]), __uint_as_float(s[1]));  // hi + lo
+          const float S = __fadd_rn(x2, cn[j]);
+          dd[j] = __fsub_rn(S, 2.0f * p);
+          ee[j] = __fmaf_rn(kKappa, S, 1.0e-30f);
+          if (!(__builtin_isfinite(dd[j]) && __builtin_isfinite(ee[j]))) dd[j] = __builtin_nanf("");
+          if (4 * (G & 1) + j >= count) {
+            dd[j] = INFINITY;
+            ee[j] = 0.0f;
+          }
+        }
+        // clusters 4..7 from lane group 1 to lane group 0 (the other groups compute the same
+        // decision on other values and do not store it)
+        float D8[8], E8[8];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const auto sd = __builtin_amdgcn_permlane16_swap(__float_as_uint(dd[j]), __float_as_uint(dd[j]), false, false);
+          const auto se = __builtin_amdgcn_permlane16_swap(__float_as_uint(ee[j]), __float_as_uint(ee[j]), false, false);
+          D8[j] = dd[j];
+          E8[j] = ee[j];
+          D8[4 + j] = __uint_as_float(sd[1]);
+          E8[4 + j] = __uint_as_float(se[1]);
+        }
+        // b = the first strict minimum of D; settled when no other center's D_c - E_c fails to
+        // exceed D_b + E_b (a NaN fails, so does everything when D_b + E_b is NaN; with one
+        // cluster the label is 0 either way)
+        float bv = D8[0], be = E8[0];
+        int b = 0;
+#pragma unroll
+        for (int c = 1; c < 8; ++c)
+          if (D8[c] < bv) {
+            bv = D8[c];
+            be = E8[c];
+            b = c;
+          }
+        const float ub = __fadd_rn(bv, be);
+        int open = 0;
+#pragma unroll
+        for (int c = 0; c < 8; ++c) open += !(__fsub_rn(D8[c], E8[c]) > ub);
+        if (G == 0) pre[t] = static_cast<uint8_t>(b | (open == 1 ? 0x80 : 0));
       }
-    constexpr float kOrder = 1.0f + 4.0e-5f;  // > (1 + e) / (1 - e), e = 130 * 2^-24
-    // NaN distances never enter b32 / s32, so they are tested separately: with one the fp64
-    // chains decide, as in the oracle; an infinite b32 also leaves the order unsure
-    sure = finite && s32 > b32 * kOrder + 1.0e-37f;
-  }
-  if (tok < n && !LDSC) {
-    float b32 = INFINITY, s32 = INFINITY;
-    bool finite = true;  // a NaN distance (NaN in V or a center) fails every compare below
-    for (int c0 = 0; c0 < count; c0 += 8) {
-      const float* cen = centers32 + (bh * CS + c0) * D;  // wave-uniform: scalar loads
+      lds_barrier();
+      best = pre[tid] & 7;
+      sure = (pre[tid] & 0x80) != 0;
+    }
+    if (tok < n && LDSC && !sure) {
+      float b32 = INFINITY, s32 = INFINITY;
       float acc[8];
 #pragma unroll
       for (int c = 0; c < 8; ++c) acc[c] = 0.0f;
+      const float4* cl4 = reinterpret_cast<const float4*>(cl);
 #pragma unroll 2
       for (int i = 0; i < D / 8; ++i) {
         const uint4 q = *reinterpret_cast<const uint4*>(&xs[tid * kStride + 8 * i]);
@@ -196,144 +345,199 @@ __global__ __launch_bounds__(kGroupThreads) void grp_assign_kernel(
         for (int k = 0; k < 4; ++k) {
           const int d = 8 * i + 2 * k;
           const float x0 = in_to_f32<DT>(w[k] & 0xffffu), x1 = in_to_f32<DT>(w[k] >> 16);
+          const float4 a0 = cl4[2 * d], a1 = cl4[2 * d + 1], b0 = cl4[2 * d + 2], b1 = cl4[2 * d + 3];
+          const float c0v[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+          const float c1v[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
 #pragma unroll
           for (int c = 0; c < 8; ++c) {
-            const float d0 = __fsub_rn(x0, cen[c * D + d]);
+            const float d0 = __fsub_rn(x0, c0v[c]);
             acc[c] = __fmaf_rn(d0, d0, acc[c]);
-            const float d1 = __fsub_rn(x1, cen[c * D + d + 1]);
+            const float d1 = __fsub_rn(x1, c1v[c]);
             acc[c] = __fmaf_rn(d1, d1, acc[c]);
           }
         }
       }
+      bool finite = true;  // a NaN distance (NaN in V or a center) fails every compare below
 #pragma unroll
       for (int c = 0; c < 8; ++c)
-        if (c0 + c < count) {
+        if (c < count) {
           finite = finite && acc[c] >= 0.0f;
           if (acc[c] < b32) {  // ties keep the lowest id (and make the order unsure)
             s32 = b32;
             b32 = acc[c];
-            best = c0 + c;
+            best = c;
           } else if (acc[c] < s32) {
             s32 = acc[c];
           }
         }
+      constexpr float kOrder = 1.0f + 4.0e-5f;  // > (1 + e) / (1 - e), e = 130 * 2^-24
+      // NaN distances never enter b32 / s32, so they are tested separately: with one the fp64
+      // chains decide, as in the oracle; an infinite b32 also leaves the order unsure
+      sure = finite && s32 > b32 * kOrder + 1.0e-37f;
     }
-    constexpr float kOrder = 1.0f + 4.0e-5f;  // > (1 + e) / (1 - e), e = 130 * 2^-24
-    sure = finite && s32 > b32 * kOrder + 1.0e-37f;  // NaN distances: the fp64 chains decide
-  }
-  if (tok < n && !sure) {
-    // first strict minimum from +inf: NaN and infinite distances never win, and a token with
-    // no finite distance keeps label 0 (the oracle's rule)
-    best = 0;
-    double best_d = INFINITY;
-    for (int c0 = 0; c0 < count; c0 += 8) {
-      const double* cen = centers64 + (bh * CS + c0) * D;  // wave-uniform: scalar loads
-      // distance_c = sum over d (in order) of fma(x_d - c_d, x_d - c_d, acc) in fp64
-      double acc[8];
+    if (tok < n && !LDSC && !sure) {
+      float b32 = INFINITY, s32 = INFINITY;
+      bool finite = true;  // a NaN distance (NaN in V or a center) fails every compare below
+      for (int c0 = 0; c0 < count; c0 += 8) {
+        const float* cen = centers32 + (bh * CS + c0) * D;  // wave-uniform: scalar loads
+        float acc[8];
 #pragma unroll
-      for (int c = 0; c < 8; ++c) acc[c] = 0.0;
+        for (int c = 0; c < 8; ++c) acc[c] = 0.0f;
 #pragma unroll 2
-      for (int i = 0; i < D / 8; ++i) {
-        const uint4 q = *reinterpret_cast<const uint4*>(&xs[tid * kStride + 8 * i]);
-        const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+        for (int i = 0; i < D / 8; ++i) {
+          const uint4 q = *reinterpret_cast<const uint4*>(&xs[tid * kStride + 8 * i]);
+          const uint32_t w[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          const int d = 8 * i + 2 * k;
-          const double x0 = static_cast<double>(in_to_f32<DT>(w[k] & 0xffffu));
-          const double x1 = static_cast<double>(in_to_f32<DT>(w[k] >> 16));
-          // fused schedule: the fp64 centers are the exact widenings of the LDS fp32 ones
-          double c0v[8], c1v[8];
-          if constexpr (LDSC) {
-            const float4* cl4 = reinterpret_cast<const float4*>(cl);
-            const float4 a0 = cl4[2 * d], a1 = cl4[2 * d + 1], b0 = cl4[2 * d + 2], b1 = cl4[2 * d + 3];
-            const float f0[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
-            const float f1[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+          for (int k = 0; k < 4; ++k) {
+            const int d = 8 * i + 2 * k;
+            const float x0 = in_to_f32<DT>(w[k] & 0xffffu), x1 = in_to_f32<DT>(w[k] >> 16);
 #pragma unroll
             for (int c = 0; c < 8; ++c) {
-              c0v[c] = static_cast<double>(f0[c]);
-              c1v[c] = static_cast<double>(f1[c]);
+              const float d0 = __fsub_rn(x0, cen[c * D + d]);
+              acc[c] = __fmaf_rn(d0, d0, acc[c]);
+              const float d1 = __fsub_rn(x1, cen[c * D + d + 1]);
+              acc[c] = __fmaf_rn(d1, d1, acc[c]);
             }
-          } else {
-#pragma unroll
-            for (int c = 0; c < 8; ++c) {
-              c0v[c] = cen[c * D + d];
-              c1v[c] = cen[c * D + d + 1];
-            }
-          }
-#pragma unroll
-          for (int c = 0; c < 8; ++c) {
-            const double d0 = __dsub_rn(x0, c0v[c]);
-            acc[c] = __fma_rn(d0, d0, acc[c]);
-            const double d1 = __dsub_rn(x1, c1v[c]);
-            acc[c] = __fma_rn(d1, d1, acc[c]);
           }
         }
+#pragma unroll
+        for (int c = 0; c < 8; ++c)
+          if (c0 + c < count) {
+            finite = finite && acc[c] >= 0.0f;
+            if (acc[c] < b32) {  // ties keep the lowest id (and make the order unsure)
+              s32 = b32;
+              b32 = acc[c];
+              best = c0 + c;
+            } else if (acc[c] < s32) {
+              s32 = acc[c];
+            }
+          }
       }
+      constexpr float kOrder = 1.0f + 4.0e-5f;  // > (1 + e) / (1 - e), e = 130 * 2^-24
+      sure = finite && s32 > b32 * kOrder + 1.0e-37f;  // NaN distances: the fp64 chains decide
+    }
+    if (tok < n && !sure) {
+      // first strict minimum from +inf: NaN and infinite distances never win, and a token with
+      // no finite distance keeps label 0 (the oracle's rule)
+      best = 0;
+      double best_d = INFINITY;
+      for (int c0 = 0; c0 < count; c0 += 8) {
+        const double* cen = centers64 + (bh * CS + c0) * D;  // wave-uniform: scalar loads
+        // distance_c = sum over d (in order) of fma(x_d - c_d, x_d - c_d, acc) in fp64
+        double acc[8];
 #pragma unroll
-      for (int c = 0; c < 8; ++c)
-        if (c0 + c < count && acc[c] < best_d) {  // ties keep the lowest id
-          best_d = acc[c];
-          best = c0 + c;
+        for (int c = 0; c < 8; ++c) acc[c] = 0.0;
+#pragma unroll 2
+        for (int i = 0; i < D / 8; ++i) {
+          const uint4 q = *reinterpret_cast<const uint4*>(&xs[tid * kStride + 8 * i]);
+          const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            const int d = 8 * i + 2 * k;
+            const double x0 = static_cast<double>(in_to_f32<DT>(w[k] & 0xffffu));
+            const double x1 = static_cast<double>(in_to_f32<DT>(w[k] >> 16));
+            // fused schedule: the fp64 centers are the exact widenings of the LDS fp32 ones
+            double c0v[8], c1v[8];
+            if constexpr (LDSC) {
+              const float4* cl4 = reinterpret_cast<const float4*>(cl);
+              const float4 a0 = cl4[2 * d], a1 = cl4[2 * d + 1], b0 = cl4[2 * d + 2], b1 = cl4[2 * d + 3];
+              const float f0[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+              const float f1[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+#pragma unroll
+              for (int c = 0; c < 8; ++c) {
+                c0v[c] = static_cast<double>(f0[c]);
+                c1v[c] = static_cast<double>(f1[c]);
+              }
+            } else {
+#pragma unroll
+              for (int c = 0; c < 8; ++c) {
+                c0v[c] = cen[c * D + d];
+                c1v[c] = cen[c * D + d + 1];
+              }
+            }
+#pragma unroll
+            for (int c = 0; c < 8; ++c) {
+              const double d0 = __dsub_rn(x0, c0v[c]);
+              acc[c] = __fma_rn(d0, d0, acc[c]);
+              const double d1 = __dsub_rn(x1, c1v[c]);
+              acc[c] = __fma_rn(d1, d1, acc[c]);
+            }
+          }
         }
-    }
-  }
-  if (tok < n) labels[bh * n + tok] = best;
-  const int64_t meta = (bh * tiles + tile) * CS;
-  if constexpr (GENERAL) {
-    if (tok < n) atomicAdd(&hist[best], 1);
-    __syncthreads();
-    for (int c = tid; c < count; c += kGroupThreads) pcnt[meta + c] = hist[c];
-    return;
-  } else {
-    // Stable order of the tile's tokens by label: wave ballots give each token its
-    // rank among the earlier tokens with the same label.
-    __shared__ int wcount[2][kFusedClusters];
-    __shared__ int start[kFusedClusters + 1];
-    __shared__ uint8_t order[kTile];
-    const int L = tok < n ? best : -1;
-    const int lane = tid & 63, wv = tid >> 6;
-    int rank = 0;
 #pragma unroll
-    for (int c = 0; c < kFusedClusters; ++c) {
-      const uint64_t m = __ballot(L == c);
-      if (L == c)
-        rank = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m >> 32), __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m), 0));
-      if (lane == 0) wcount[wv][c] = __popcll(m);
+        for (int c = 0; c < 8; ++c)
+          if (c0 + c < count && acc[c] < best_d) {  // ties keep the lowest id
+            best_d = acc[c];
+            best = c0 + c;
+          }
+      }
     }
-    __syncthreads();
-    if (tid == 0) {
-      int acc = 0;
+    if (tok < n) labels[bh * n + tok] = best;
+    const int64_t meta = (bh * tiles + tile) * CS;
+    if constexpr (GENERAL) {
+      if (tok < n) atomicAdd(&hist[best], 1);
+      lds_barrier();
+      for (int c = tid; c < count; c += kGroupThreads) pcnt[meta + c] = hist[c];
+    } else {
+      // Per-tile counts from wave ballots, which also give each token its rank among the
+      // earlier tokens of its wave with the same label.
+      __shared__ int wcount[2][kFusedClusters];
+      const int L = tok < n ? best : -1;
+      const int wv = tid >> 6;
+      int rank = 0;
+#pragma unroll
       for (int c = 0; c < kFusedClusters; ++c) {
-        start[c] = acc;
-        acc += wcount[0][c] + wcount[1][c];
+        const uint64_t m = __ballot(L == c);
+        if (L == c)
+          rank = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m >> 32), __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m), 0));
+        if (lane == 0) wcount[wv][c] = __popcll(m);
       }
-      start[kFusedClusters] = acc;
-    }
-    __syncthreads();
-    if (L >= 0) order[start[L] + (wv ? wcount[0][L] : 0) + rank] = static_cast<uint8_t>(tid);
-    if (tid < count) pcnt[meta + tid] = wcount[0][tid] + wcount[1][tid];
-    if constexpr (STATS) {
-      __syncthreads();
-      if (tid < D) {
-        // per-cluster sums over the tile's tokens in token order, 8 tokens a step: their
-        // indices (the same on every lane) and then their values are all loaded before the
-        // additions, which keep the list order
+      lds_barrier();
+      if (tid < count) pcnt[meta + tid] = wcount[0][tid] + wcount[1][tid];
+      if constexpr (STATS) {
+        // Per-cluster sums over the tile's tokens in token order. Each cluster's list holds
+        // the LDS byte offsets of its tokens' staged rows, padded to a multiple of 8 entries
+        // with the zero row: adding +0.0 leaves a partial sum unchanged (it starts at +0.0 and
+        // is never -0.0). A step reads 8 offsets at once, then the 8 values, then adds them
+        // in list order.
         constexpr int kB = 8;
-        for (int c = 0; c < count; ++c) {
-          double acc = 0.0;
-          const int b = __builtin_amdgcn_readfirstlane(start[c]), e = __builtin_amdgcn_readfirstlane(start[c + 1]);
-          for (int k = b; k < e; k += kB) {
-            int ti[kB];
-            float xv[kB];
-#pragma unroll
-            for (int i = 0; i < kB; ++i) ti[i] = __builtin_amdgcn_readfirstlane(order[k + i < e ? k + i : e - 1]);
-#pragma unroll
-            for (int i = 0; i < kB; ++i) xv[i] = in_to_f32<DT>(xs[ti[i] * kStride + tid]);
-#pragma unroll
-            for (int i = 0; i < kB; ++i)
-              if (k + i < e) acc = __dadd_rn(acc, static_cast<double>(xv[i]));
+        constexpr uint16_t kZeroRow = kTile * kStride * 2;
+        __shared__ int start[kFusedClusters + 1];
+        __shared__ __attribute__((aligned(16))) uint16_t order[kTile + kB * kFusedClusters];
+        if (tid == 0) {
+          int acc = 0;
+          for (int c = 0; c < kFusedClusters; ++c) {
+            start[c] = acc;
+            acc += (wcount[0][c] + wcount[1][c] + kB - 1) & ~(kB - 1);
           }
-          psum[(meta + c) * D + tid] = acc;
+          start[kFusedClusters] = acc;
+        }
+        lds_barrier();
+        if (L >= 0) order[start[L] + (wv ? wcount[0][L] : 0) + rank] = static_cast<uint16_t>(tid * kStride * 2);
+        if (tid < kB * kFusedClusters) {
+          const int c = tid / kB, slot = start[c] + wcount[0][c] + wcount[1][c] + tid % kB;
+          if (slot < start[c + 1]) order[slot] = kZeroRow;
+        }
+        lds_barrier();
+        if (tid < D) {
+          const uint8_t* col = reinterpret_cast<const uint8_t*>(xs) + 2 * tid;
+          for (int c = 0; c < count; ++c) {
+            double acc = 0.0;
+            const int b = __builtin_amdgcn_readfirstlane(start[c]), e = __builtin_amdgcn_readfirstlane(start[c + 1]);
+            for (int k = b; k < e; k += kB) {
+              const uint4 o = *reinterpret_cast<const uint4*>(&order[k]);
+              const uint32_t ow[4] = {o.x, o.y, o.z, o.w};
+              float xv[kB];
+#pragma unroll
+              for (int i = 0; i < kB / 2; ++i) {
+                xv[2 * i] = in_to_f32<DT>(*reinterpret_cast<const uint16_t*>(col + (ow[i] & 0xffffu)));
+                xv[2 * i + 1] = in_to_f32<DT>(*reinterpret_cast<const uint16_t*>(col + (ow[i] >> 16)));
+              }
+#pragma unroll
+              for (int i = 0; i < kB; ++i) acc = __dadd_rn(acc, static_cast<double>(xv[i]));
+            }
+            psum[(meta + c) * D + tid] = acc;
+          }
         }
       }
     }
@@ -346,7 +550,9 @@ __global__ __launch_bounds__(kGroupThreads) void grp_assign_kernel(
 // puts 64 tiles' partials in flight before adding them in order (5 round trips for 295
 // tiles instead of 19 with batches of 16).
 __global__ __launch_bounds__(128) void grp_update_kernel(float* centers, double* centers64, const double* psum,
-                                                         const int32_t* pcnt, int64_t tiles, int D) {
+                                                         const int32_t* pcnt, int64_t tiles, int D,
+                                                         CenterForms forms) {
+  __shared__ double red[128];
   const int64_t bh = blockIdx.x;
   const int c = blockIdx.y, d = threadIdx.x;
   // Token count of the cluster: an integer sum (exact in any order), spread over the lanes
@@ -372,10 +578,16 @@ __global__ __launch_bounds__(128) void grp_update_kernel(float* centers, double*
     for (int i = 0; i < kBatch; ++i) s = __dadd_rn(s, v[i]);
   }
   for (; t < tiles; ++t) s = __dadd_rn(s, col[t * stride]);
-  if (total > 0) {
+  if (total > 0) {  // the same on every thread of the block
     const float x = static_cast<float>(__ddiv_rn(s, static_cast<double>(total)));
     centers[(bh * kFusedClusters + c) * D + d] = x;
     centers64[(bh * kFusedClusters + c) * D + d] = static_cast<double>(x);
+    if (forms.parts) {
+      store_center_parts(x, bh * kFusedClusters + c, d, D, forms);
+      red[d] = static_cast<double>(x) * static_cast<double>(x);
+      __syncthreads();
+      if (d == 0) store_center_norm(red, bh * kFusedClusters + c, D, forms);
+    }
   }
 }
 
@@ -523,6 +735,7 @@ struct GroupWs {
   int32_t* pcnt;
   int32_t* labels;
   int64_t* offsets;
+  CenterForms forms;  // fused schedule only (the pre-pass runs on bf16 rows)
   size_t bytes;
 };
 
@@ -541,6 +754,10 @@ GroupWs group_ws(void* base, int64_t BH, int64_t N, int64_t D, int CS, bool gene
   w.pcnt = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * BH * tiles * CS));
   w.labels = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * BH * N));
   w.offsets = reinterpret_cast<int64_t*>(take(sizeof(int64_t) * BH * tiles * CS));
+  if (!general) {
+    w.forms.parts = reinterpret_cast<uint16_t*>(take(sizeof(uint16_t) * BH * CS * 2 * D));
+    w.forms.norms = reinterpret_cast<float*>(take(sizeof(float) * BH * CS));
+  }
   w.bytes = off;
   return w;
 }
@@ -580,7 +797,8 @@ extern "C" int vcx_group_values(const void* v, int dtype, int64_t B, int64_t H, 
                                 float* centers_next, void* workspace, size_t workspace_bytes, void* stream) {
   VCX_REQUIRE(B >= 1 && H >= 1 && N >= 1, "B, H, N must be positive");
   VCX_REQUIRE(D == 64 || D == 128, "D must be 64 or 128");
-  VCX_REQUIRE(B * H <= 65535 && N < (int64_t(1) << 30), "shape exceeds launch bounds");
+  VCX_REQUIRE(B * H <= 65535 && N < (int64_t(1) << 30) && B * H * cdiv(N, kTile) < (int64_t(1) << 31),
+              "shape exceeds launch bounds");
   VCX_REQUIRE(dtype == VCX_FLOAT16 || dtype == VCX_BFLOAT16, "dtype must be float16 or bfloat16");
   VCX_REQUIRE(clusters >= 1 && clusters <= kMaxClusters && iterations >= 1 && iterations <= 100,
               "clusters must be in [1, 256] and iterations in [1, 100]");
@@ -611,14 +829,33 @@ extern "C" int vcx_group_values(const void* v, int dtype, int64_t B, int64_t H, 
   };
   auto run = [&](auto dt, auto dd) -> int {
     constexpr int DT = decltype(dt)::value, DD = decltype(dd)::value;
-    auto assign = [&](auto stats, auto gen, double* psum) {
+    // Assignment items are the BH * tiles (head, tile) pairs. With the prefetch (bf16 rows,
+    // fused schedule, 16-byte rows) a block takes a run of two consecutive items, loading
+    // the second during the first; otherwise one item per block. Same-box A/B on the
+    // [1,28,37741,128] smoothing workload, grouping call: runs of 2 290 us, one item per
+    // block 309 us, runs of 4 306 us, one run per resident block (9 items) 328 us; the
+    // longer runs lose the hardware's dynamic balancing of slow (fallback-heavy) tiles.
+    auto assign = [&](auto stats, auto gen, double* psum) -> int {
       constexpr bool ST = decltype(stats)::value, GE = decltype(gen)::value;
-      if (wide)
-        grp_assign_kernel<DT, DD, ST, true, GE><<<dim3(tiles, BH), kGroupThreads, 0, st>>>(
-            v, H, N, v_sb, v_sh, v_sn, count, CS, ws.centers, ws.centers64, lab, psum, ws.pcnt);
-      else
-        grp_assign_kernel<DT, DD, ST, false, GE><<<dim3(tiles, BH), kGroupThreads, 0, st>>>(
-            v, H, N, v_sb, v_sh, v_sn, count, CS, ws.centers, ws.centers64, lab, psum, ws.pcnt);
+      auto launch = [&](auto kernel, bool runs) -> int {
+        const int64_t items = BH * tiles;
+        int64_t per = 1;
+        if (runs) {  // only where more items than resident blocks
+          int dev = 0, cus = 0, occ = 0;
+          if (hipGetDevice(&dev) != hipSuccess ||
+              hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+              hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kernel, kGroupThreads, 0) != hipSuccess)
+            return fail(VCX_EHIP, "grouping: device query failed");
+          per = std::min<int64_t>(cdiv(items, static_cast<int64_t>(std::max(cus, 1)) * std::max(occ, 1)), 2);
+        }
+        const int64_t grid = cdiv(items, per);
+        kernel<<<dim3(static_cast<unsigned>(grid)), kGroupThreads, 0, st>>>(
+            v, H, N, v_sb, v_sh, v_sn, count, CS, ws.centers, ws.centers64, ws.forms, lab, psum, ws.pcnt, tiles,
+            items, per);
+        return VCX_OK;
+      };
+      if (wide) return launch(grp_assign_kernel<DT, DD, ST, true, GE>, assign_prefetch(DT, GE, true));
+      return launch(grp_assign_kernel<DT, DD, ST, false, GE>, assign_prefetch(DT, GE, false));
     };
     auto sort = [&]() -> int {
       grp_offsets_kernel<<<dim3(BH), kOffsetThreads, 0, st>>>(ws.pcnt, tiles, count, CS, ws.offsets);
@@ -628,13 +865,15 @@ extern "C" int vcx_group_values(const void* v, int dtype, int64_t B, int64_t H, 
       return VCX_OK;
     };
     grp_init_kernel<DT><<<dim3(BH), DD, 0, st>>>(v, H, v_sb, v_sh, v_sn, ids, count, CS, DD, centers_in,
-                                                  ws.centers, ws.centers64);
+                                                  ws.centers, ws.centers64,
+                                                  DT == VCX_BFLOAT16 ? ws.forms : CenterForms{});
     VCX_LAUNCHED("grp_init_kernel");
     for (int it = 0; it < iterations; ++it) {
       const bool last = it + 1 == iterations, update = !last || centers_next != nullptr;
       if (!general) {
-        if (update) assign(std::true_type(), std::false_type(), ws.psum);
-        else assign(std::false_type(), std::false_type(), nullptr);
+        if (int rc = update ? assign(std::true_type(), std::false_type(), ws.psum)
+                            : assign(std::false_type(), std::false_type(), nullptr))
+          return rc;
         VCX_LAUNCHED("grp_assign_kernel");
         if (last) {
           if (int rc = sort()) return rc;
@@ -642,11 +881,12 @@ extern "C" int vcx_group_values(const void* v, int dtype, int64_t B, int64_t H, 
             if (int rc = copy_centers(centers)) return rc;
         }
         if (update) {
-          grp_update_kernel<<<dim3(BH, count), DD, 0, st>>>(ws.centers, ws.centers64, ws.psum, ws.pcnt, tiles, DD);
+          grp_update_kernel<<<dim3(BH, count), DD, 0, st>>>(ws.centers, ws.centers64, ws.psum, ws.pcnt, tiles, DD,
+                                                           DT == VCX_BFLOAT16 ? ws.forms : CenterForms{});
           VCX_LAUNCHED("grp_update_kernel");
         }
       } else {
-        assign(std::false_type(), std::true_type(), nullptr);
+        if (int rc = assign(std::false_type(), std::true_type(), nullptr)) return rc;
         VCX_LAUNCHED("grp_assign_kernel<general>");
         if (int rc = sort()) return rc;
         if (last && centers)

@@ -189,6 +189,24 @@ def test_grouping_non_finite_values_follow_the_oracle(dim, clusters, bad):
     np.testing.assert_array_equal(centers.cpu().numpy(), ecenters)  # NaN == NaN here
 
 
+@pytest.mark.parametrize("dim", [64, 128])
+@pytest.mark.parametrize("offset", [0.0, 40.0, 3.0e4])
+def test_grouping_offset_values_follow_the_oracle(dim, offset):
+    # V = offset + N(0, 1) in bf16: with a large offset |x|^2 + |c|^2 dwarfs |x - c|^2, so the
+    # kernel's dot-product pre-pass (x.c on the MFMA) cannot settle many tokens and leaves
+    # them to the binary32 and fp64 chains, inside waves where others are settled; bf16's
+    # coarse steps at the offset also make exact distance ties. Labels, centers and the
+    # permutation must still be the oracle's.
+    _print_case("grouping offset", dim, offset)
+    g = torch.Generator().manual_seed(17 + dim)
+    v = (offset + torch.randn(1, 2, 3000, dim, generator=g)).to(torch.bfloat16)
+    perm, labels, centers = vcx.group_values(v.to(DEV), 8, 3, debug=True)
+    eperm, elabels, ecenters = o.group_values(bits(v), 8, 3, "bfloat16")
+    np.testing.assert_array_equal(labels.cpu().numpy(), elabels)
+    np.testing.assert_array_equal(centers.cpu().numpy().view(np.uint32), ecenters.view(np.uint32))
+    np.testing.assert_array_equal(perm.cpu().numpy(), eperm)
+
+
 def _near_tie_values(dim, dtype, n=1024, seed=0):
     """[1,2,n,dim] V whose tokens sit at or near the bisector of the two initial centers
     (V[0] = -e_0 + w, V[n-1] = +e_0 + w, with the same random tail w in the other channels):

@@ -157,11 +157,13 @@ __global__ __launch_bounds__(kGroupThreads) void grp_assign_kernel(
     const int64_t tile = item % tiles;
     const uint16_t* base = head_ptr(v, item / tiles, H, sb, sh);
     if ((tile + 1) * kTile <= n) {
+      // a wave-uniform base per load plus one 32-bit lane offset (kGroupThreads is a
+      // multiple of kPieces, so a thread keeps its piece and moves down whole rows)
+      const char* tb = reinterpret_cast<const char*>(base + tile * kTile * sn);
+      const uint32_t lane_off = static_cast<uint32_t>(((tid / kPieces) * sn + kElems * (tid % kPieces)) * 2);
 #pragma unroll
-      for (int k = 0; k < kPer; ++k) {
-        const int s = tid + k * kGroupThreads, row = s / kPieces, part = s % kPieces;
-        val[k] = *reinterpret_cast<const Piece*>(base + (tile * kTile + row) * sn + kElems * part);
-      }
+      for (int k = 0; k < kPer; ++k)
+        val[k] = *reinterpret_cast<const Piece*>(tb + k * (kGroupThreads / kPieces) * sn * 2 + lane_off);
     } else {
 #pragma unroll
       for (int k = 0; k < kPer; ++k) {

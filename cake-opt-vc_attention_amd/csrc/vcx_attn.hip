@@ -580,8 +580,10 @@ struct Wave {
       }
     } else {
       const float f = scl;
-      // Bytes of the +-2 ulp neighbours of every probability; an E4M3 midpoint within two
-      // ulps (the neighbours disagree, a few lanes per million) takes the binary64 recheck.
+      // Bytes of the +-2 ulp neighbours of every probability (the lower ones by a saturating
+      // subtraction on every tile, so that p = 0, i.e. a score more than about 103 nats
+      // below the row maximum, never forces a recheck); an E4M3 midpoint within two ulps
+      // (the neighbours disagree, a few lanes per million) takes the binary64 recheck.
       // At D128 the recheck is one branch per tile (a lane that missed redoes its tile from
       // the scores, which stay live), so the loop stays one block that the MFMAs
       // interleave with; D64's three waves per SIMD have no registers for that and branch
@@ -595,7 +597,7 @@ struct Wave {
 #pragma unroll
           for (int r = 0; r < 4; ++r) pr[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(bs[j][r], f, -mx));
           uint32_t lo, hi;
-          fp8_exp2_bounds<LAST, true>(pr, lo, hi);
+          fp8_exp2_bounds<true, true>(pr, lo, hi);
           Pq[j] = static_cast<int>(lo);
           miss |= lo ^ hi;
 #pragma unroll
@@ -613,7 +615,7 @@ struct Wave {
               xs[r] = __builtin_fmaf(b, f, -mx);
               pr[r] = __builtin_amdgcn_exp2f(xs[r]);
             }
-            Pq[j] = static_cast<int>(fp8_exp2_word<LAST>(xs, pr));
+            Pq[j] = static_cast<int>(fp8_exp2_word<true>(xs, pr));
 #pragma unroll
             for (int r = 0; r < 4; ++r) ls += pr[r];
           }
@@ -627,7 +629,7 @@ struct Wave {
             xs[r] = __builtin_fmaf(bs[j][r], f, -mx);
             pr[r] = __builtin_amdgcn_exp2f(xs[r]);
           }
-          Pq[j] = static_cast<int>(fp8_exp2_word<LAST>(xs, pr));
+          Pq[j] = static_cast<int>(fp8_exp2_word<true>(xs, pr));
 #pragma unroll
           for (int r = 0; r < 4; ++r) ls += pr[r];
         }
@@ -1316,7 +1318,7 @@ extern "C" int vcx_attention_fwd_fp8(const uint8_t* q8, const uint8_t* k8, const
 namespace vcx {
 namespace {
 // One thread per four inputs: the control path's probability bytes via fp8_exp2_word
-// (SAT: the form of the tiles with masked keys).
+// (SAT: the saturating lower neighbours the fused kernel uses; else the 64-bit pair form).
 template <bool SAT>
 __global__ void fp8_exp2_probe_kernel(const float* x, uint8_t* y, int64_t n) {
   const int64_t i = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) * 4;

@@ -105,15 +105,16 @@ __device__ inline uint32_t e4m3_sat(float x) {
 // On entry p holds the hardware exp2 (v_exp_f32, within one ulp of exp2 on every binary32
 // input). The bytes of p - 2 ulps and p + 2 ulps agree unless an E4M3 rounding midpoint lies
 // within two ulps of p; only then does the lane recompute exp2 in binary64 and round it once
-// to binary32 (p is updated to that value). The +-2 ulp neighbours of two probabilities come
-// from one 64-bit add each way (v_lshl_add_u64); a borrow out of a low half below 2 ulps (p
-// = 0 or the smallest subnormal, i.e. x below about -149) only widens the window or yields a
-// NaN byte, i.e. a needless recheck with the right result. For N(0,1)-like scores that is a
-// few lanes per million; rows whose scores lie more than about 100 nats below the row
-// maximum meet it on most tiles (at D128 the whole tile is then redone), which costs time,
-// never bytes. SAT = true forms the lower neighbours with a saturating subtraction instead,
-// for tiles with masked keys (p = exp2(-inf) = 0). Reference: the probability byte of
-// sal/sageattention_local/vc_reference.py:68-75 and sal/csrc/qattn/attn_utils.cuh:355-455.
+// to binary32 (p is updated to that value). The upper neighbours of two probabilities come
+// from one 64-bit add (v_lshl_add_u64). SAT = true (what the fused kernel uses) forms the
+// lower neighbours with a saturating subtraction per probability. SAT = false uses one 64-bit
+// subtraction per pair, half the instructions, but a borrow out of a low half below 2 ulps (p
+// = 0 or the smallest subnormal, i.e. x below about -149) then yields a NaN byte and a
+// needless recheck: bytes stay right, but rows whose scores lie more than about 103 nats
+// below the row maximum recheck on most tiles. Same-box A/B of the control path: SAT costs
+// 5.8 % (D128) and 11 % (D64) on N(0,1) scores and is 4-5 times faster with Q scaled by 25.
+// Reference: the probability byte of sal/sageattention_local/vc_reference.py:68-75 and
+// sal/csrc/qattn/attn_utils.cuh:355-455.
 // fp8_exp2_bounds gives the bytes of both neighbour sets (lo, hi); fp8_exp2_word resolves a
 // disagreement. Binary64 exp2 rounded once to binary32: one out-of-line copy for the rare
 // recheck.

@@ -461,7 +461,8 @@ def expcast_codes(x):
 @_device_call
 def fp8_exp2_codes(x, last_tile: bool = False):
     """E4M3 bytes of the control path's probabilities exp2(x), from the fused kernel's device
-    code (last_tile: the variant of the tile with masked keys)."""
+    code (last_tile: the saturating window form, which the kernel runs on every tile; else
+    the 64-bit pair form; the bytes are the same)."""
     dev = _require_device(x)
     x = x.float().contiguous()
     y = torch.empty(x.shape, dtype=torch.uint8, device=dev)

@@ -228,7 +228,9 @@ int vcx_expcast_codes(const float* x, uint8_t* y, int64_t n, void* stream);
 /* Control-path probability probe: y[i] = E4M3_RNE(RN_f32(exp2(x[i]))), the P byte of the
  * Sage FP8 control path (vcx_attention_fwd expcast = 0) computed by the fused kernel's own
  * device function (hardware exp2, rechecked in binary64 next to an E4M3 rounding midpoint);
- * form 0 is the variant of the tiles before the last, 1 that of the last tile.
+ * form 1 forms the lower window neighbours by saturating subtraction (what the fused kernel
+ * runs on every tile), form 0 by one 64-bit subtraction per pair (same bytes, more
+ * rechecks for probabilities below two subnormal ulps).
  * Replaces the probability byte of third_party/sageattention_local/sageattention_local/
  * vc_reference.py:68-75 (torch.exp2 then float8_e4m3fn), for the parity tests. */
 int vcx_fp8_exp2_codes(const float* x, uint8_t* y, int64_t n, int form, void* stream);

@@ -683,6 +683,28 @@ def test_control_path_p_bytes_and_output(case):
     assert torch.equal(out2, out)
 
 
+@pytest.mark.parametrize("dim", [64, 128])
+def test_control_path_far_logits_p_bytes_and_output(dim):
+    # Q scaled by 25: many scores lie more than 103 nats below their row maximum, so p =
+    # exp2(x) is 0 or subnormal; the window check must still give the oracle's bytes (and not
+    # fall back to the binary64 recheck on every tile).
+    _print_case("control path far logits", dim)
+    q, k, v = make_qkv(1, 2, 200, 700, dim, torch.bfloat16, seed=29)
+    q = (q.float() * 25).to(torch.bfloat16)
+    st = o.prepare(bits(q), bits(k), bits(v), expcast=False, v_smooth=False, dtype="bfloat16")
+    to = _to_dev
+    v8 = to(logical_to_storage(st["v"], vcx.value_token())).view(torch.float8_e4m3fn)
+    out, pd = vcx.forward(to(st["q"]), to(st["k"]), v8, to(st["qs"]), to(st["ks"]), to(st["vs"]), None,
+                          False, False, st["output_type"], st["scale"], p_rows=(0, 200))
+    eout, ecodes = o.reference(st, return_codes=True)
+    np.testing.assert_array_equal(pd.cpu().numpy(), ecodes)
+    assert (ecodes == 0).mean() > 0.5  # most probabilities round to byte 0
+    got = out.float().cpu().numpy()
+    err, bound = output_bound(got, eout)
+    assert np.all(err <= bound), float((err - bound).max())
+    assert cosine(got, eout) >= 0.9999
+
+
 def test_control_path_uniform_attention_known_answer_and_end_to_end():
     # scripts/validate_sage_vc.py:161-182: q = k = 0 gives every key p = 2^8.807 (byte 0x7E),
     # so the output is the decoded V mean times 448 / 2^8.807f.

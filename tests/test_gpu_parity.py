@@ -207,6 +207,27 @@ def test_grouping_offset_values_follow_the_oracle(dim, offset):
     np.testing.assert_array_equal(perm.cpu().numpy(), eperm)
 
 
+@pytest.mark.parametrize("dim", [64, 128])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_grouping_rows_not_16_byte_aligned(dim, dtype):
+    # a token stride of dim + 2 elements leaves rows 4-byte aligned only: the tile is staged in
+    # 4-byte pieces, one tile per block (the bf16 pre-pass without the next tile's loads in
+    # flight); labels, centers, next centers and the permutation are still the oracle's.
+    _print_case("grouping unaligned rows", dim, dtype)
+    g = torch.Generator().manual_seed(31 + dim)
+    v = torch.randn(1, 2, 1500, dim, generator=g).to(dtype)
+    wide = torch.zeros(1, 2, 1500, dim + 2, dtype=dtype)
+    wide[..., :dim] = v
+    dv = wide.to(DEV)[..., :dim]
+    assert dv.stride(2) % 8 != 0
+    perm, labels, centers, nxt = vcx.group_values(dv, 8, 2, debug=True, return_centers=True)
+    eperm, elabels, ecenters, enext = o.group_values(bits(v), 8, 2, dtype_name(dtype), return_next=True)
+    np.testing.assert_array_equal(labels.cpu().numpy(), elabels)
+    np.testing.assert_array_equal(centers.cpu().numpy().view(np.uint32), ecenters.view(np.uint32))
+    np.testing.assert_array_equal(nxt.cpu().numpy().view(np.uint32), enext.view(np.uint32))
+    np.testing.assert_array_equal(perm.cpu().numpy(), eperm)
+
+
 def _near_tie_values(dim, dtype, n=1024, seed=0):
     """[1,2,n,dim] V whose tokens sit at or near the bisector of the two initial centers
     (V[0] = -e_0 + w, V[n-1] = +e_0 + w, with the same random tail w in the other channels):

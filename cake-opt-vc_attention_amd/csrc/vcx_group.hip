@@ -61,7 +61,9 @@ __device__ inline const uint16_t* head_ptr(const void* x, int64_t bh, int64_t H,
 
 // The fused schedule's centers also in the form its bf16 dot-product pre-pass reads: each
 // fp32 value c as two bf16 parts, hi = RN_bf16(c) and lo = RN_bf16(c - hi) (the
-// subtraction is exact), so |c - hi - lo| <= 2^-18 |c|, parts [BH][8][2][D] (bf16 bits);
+// subtraction is exact; |c - hi| <= 2^-8 |c| and, unless c - hi is a power of two (then lo
+// takes it exactly), c - hi lies below 2^(e-8) for 2^e <= |c|, so lo leaves at most half its
+// ulp, 2^(e-17)): |c - hi - lo| <= 2^-17 |c|; parts [BH][8][2][D] (bf16 bits);
 // and the norms |c|^2 [BH][8], RN_f32 of the fp64 sum of the D squares (each exact; the
 // summation order is free: only its error bound, far below 2^-24 relative, enters the
 // pre-pass).
@@ -80,6 +82,119 @@ __device__ inline void store_center_norm(const double* red, int64_t slot, int D,
   double t = 0.0;
   for (int i = 0; i < D; ++i) t += red[i];
   f.norms[slot] = static_cast<float>(t);
+}
+
+// Open tokens of the bf16 pre-pass, resolved by the whole wave. cl: the head's 8 binary32
+// centers, channel-major ([D][8]).
+//
+// wave_row_b32: the 8 binary32 distances of one staged row; lane (c = lane / 8, s = lane % 8)
+// forms the sum over channels [s D/8, (s + 1) D/8) of fma(x_d - c_d, x_d - c_d, acc), and
+// three butterfly additions give every lane of cluster c the same total. Every term is
+// non-negative, so in any order each distance lies within 2 * 130 * 2^-24 relative of the
+// exact one (each term passes at most D/8 + 3 + 2 roundings), and a second smallest above
+// kOrder times the smallest settles the argmin, as in the per-thread chains. Returns whether
+// it is settled, with the argmin (ties to the lowest id) in lab.
+template <int DT, int D>
+__device__ bool wave_row_b32(const uint16_t* row, const float* cl, int count, int lane, int& lab) {
+  constexpr int CH = D / 8;
+  const int c = lane >> 3, s = lane & 7;
+  float acc = 0.0f;
+#pragma unroll
+  for (int i = 0; i < CH / 8; ++i) {
+    const uint4 q = *reinterpret_cast<const uint4*>(row + s * CH + 8 * i);
+    const uint32_t wq[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int d = s * CH + 8 * i + 2 * k;
+      const float d0 = __fsub_rn(in_to_f32<DT>(wq[k] & 0xffffu), cl[d * kFusedClusters + c]);
+      acc = __fmaf_rn(d0, d0, acc);
+      const float d1 = __fsub_rn(in_to_f32<DT>(wq[k] >> 16), cl[(d + 1) * kFusedClusters + c]);
+      acc = __fmaf_rn(d1, d1, acc);
+    }
+  }
+  // a + b and b + a are the same value, so both lanes of each pair hold the same sum
+  acc = __fadd_rn(acc, __shfl_xor(acc, 1, 64));
+  acc = __fadd_rn(acc, __shfl_xor(acc, 2, 64));
+  acc = __fadd_rn(acc, __shfl_xor(acc, 4, 64));
+  float b32 = INFINITY, s32 = INFINITY;
+  lab = 0;
+  bool finite = true;  // a NaN distance fails every compare below
+#pragma unroll
+  for (int k = 0; k < kFusedClusters; ++k) {
+    const float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(acc), 8 * k));
+    if (k < count) {
+      finite = finite && a >= 0.0f;
+      if (a < b32) {  // ties keep the lowest id (and make the order unsure)
+        s32 = b32;
+        b32 = a;
+        lab = k;
+      } else if (a < s32) {
+        s32 = a;
+      }
+    }
+  }
+  constexpr float kOrder = 1.0f + 4.0e-5f;  // > (1 + e) / (1 - e), e = 130 * 2^-24
+  return finite && s32 > b32 * kOrder + 1.0e-37f;
+}
+
+// wave_rows_b64: the contract's fp64 chains for up to 8 open rows at once, taken from open
+// in token order (and cleared there). Lane (j = lane / 8, c = lane % 8) runs row j's chain
+// for cluster c: distance_c = sum over d (in order) of fma(x_d - c_d, x_d - c_d, acc), the
+// centers the exact widenings of the binary32 ones. The label is the first strict minimum
+// from +inf (NaN and infinite distances never win; no finite distance keeps label 0), i.e. the
+// smallest (value, id) pair with every such distance and every slot past count read as +inf:
+// a butterfly over the 8 lanes of a row, the same in each. Lane t of the wave takes the label
+// of its own token.
+template <int DT, int D, int kStride>
+__device__ void wave_rows_b64(const uint16_t* xs, int row0, uint64_t& open, const float* cl, int count, int lane,
+                              int& best) {
+  int rows[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    rows[j] = open ? __builtin_ctzll(open) : -1;
+    open &= open - 1;
+  }
+  const int j = lane >> 3, c = lane & 7;
+  int t = -1;
+#pragma unroll
+  for (int k = 0; k < 8; ++k)
+    if (j == k) t = rows[k];
+  double a = INFINITY;
+  if (t >= 0) {
+    const uint16_t* row = xs + (row0 + t) * kStride;
+    a = 0.0;
+#pragma unroll 1
+    for (int i = 0; i < D / 8; ++i) {
+      const uint4 q = *reinterpret_cast<const uint4*>(row + 8 * i);
+      const uint32_t wq[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int d = 8 * i + 2 * k;
+        const double d0 = __dsub_rn(static_cast<double>(in_to_f32<DT>(wq[k] & 0xffffu)),
+                                    static_cast<double>(cl[d * kFusedClusters + c]));
+        a = __fma_rn(d0, d0, a);
+        const double d1 = __dsub_rn(static_cast<double>(in_to_f32<DT>(wq[k] >> 16)),
+                                    static_cast<double>(cl[(d + 1) * kFusedClusters + c]));
+        a = __fma_rn(d1, d1, a);
+      }
+    }
+  }
+  double v = (c < count && a < INFINITY) ? a : INFINITY;
+  int id = c;
+#pragma unroll
+  for (int m = 1; m < 8; m <<= 1) {
+    const double ov = __shfl_xor(v, m, 64);
+    const int oid = __shfl_xor(id, m, 64);
+    if (ov < v || (ov == v && oid < id)) {
+      v = ov;
+      id = oid;
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const int lab = __builtin_amdgcn_readlane(id, 8 * k);
+    if (lane == rows[k]) best = lab;
+  }
 }
 
 // Centers are kept as fp32 (the contract's values) and as their exact fp64 widening,
@@ -244,20 +359,27 @@ __global__ __launch_bounds__(kGroupThreads) void grp_assign_kernel(
     // fp64 chains below.
     bool sure = false;
     // bf16 rows, fused schedule: the dot-product pre-pass. distance_c = X + C_c - 2 P_c with
-    // X = |x|^2 (bf16 dot2 chains of exact squares, then the four lane groups' partial sums;
-    // each of its D/8 + 2 steps allowed an error of 2u, so within D u X), C_c = |c|^2
-    // (precomputed) and P_c = x.c on the bf16 MFMA: x is exact in bf16 and c enters as its
-    // two bf16 parts, so every product is exact in fp32. With A = sum |x_d c_d| <= (X + C) /
-    // 2, each of the D + D/32 accumulations of either part allowed an error of 2u (u = 2^-24,
-    // whatever the MFMA's internal order, rounding or denormal flushing), the parts' 2^-18 |c|
-    // and the roundings of C, S = X + C, P and S - 2P, the computed
-    // distance lies within ((3D + 2D/32 + 8) u + 2^-18) S + 1e-30 of the exact one; kKappa is
-    // that factor with a 2 % margin. A token whose best center b (lowest id on equal values)
-    // has D_b + E_b < D_c - E_c for every other center c has b as its exact argmin, with a gap
+    // u = 2^-24 and
+    //   X = |x|^2: per lane a chain of D/8 bf16 dot2 steps over exact squares, then the sums
+    //     of the four lane groups' partials; each of the D/8 + 2 steps may err by 2u of the
+    //     running sum, so |X' - X| <= (D/4 + 4) u X;
+    //   C_c = |c|^2, precomputed (one rounding of a sum far more accurate than u);
+    //   P_c = x.c on the bf16 MFMA: x is exact in bf16 and c enters as its two bf16 parts
+    //     (|c - hi - lo| <= 2^-17 |c|), so every product is exact in fp32. With A = sum
+    //     |x_d c_d| <= (X + C) / 2, each of the D + D/32 accumulations (D products and the
+    //     running sum at each 32-channel step) may err by 2u (whatever the MFMA's internal
+    //     order, rounding or denormal flushing) of the part's sum of magnitudes: at most
+    //     (1 + 2^-8) A for the hi part, 2^-8 (1 + 2^-8) A for the lo part; and the parts
+    //     leave 2^-17 A out;
+    //   plus one rounding each for S = X + C, hi + lo and S - 2P (|S - 2P| <= 2S).
+    // Doubling the P terms (2A <= S) gives |D'_c - D_c| <= ((D/4 + 9 + 2.016 (D + D/32)) u +
+    // 2^-17) S + 1e-30 (the absolute term covers flushed subnormal products); kKappa is that
+    // factor with a 2 % margin. A token whose best center b (lowest id on equal values) has
+    // D_b + E_b < D_c - E_c for every other center c has b as its exact argmin, with a gap
     // about 10^7 times the fp64 chains' own error, so b is the fp64 argmin too. Ties, near
-    // ties and non-finite values go on to the binary32 and fp64 chains below.
+    // ties and non-finite values go on to the binary32 and fp64 stages below.
     if constexpr (MF) {
-      constexpr float kKappa = ((3 * D + 2 * KS + 8) * 5.9604645e-8f + 3.8146973e-6f) * 1.02f;
+      constexpr float kKappa = ((D / 4 + 9 + 2.016f * (D + KS)) * 5.9604645e-8f + 7.6293945e-6f) * 1.02f;
       __shared__ uint8_t pre[kTile];  // the pre-pass's label, bit 7 set when it is settled
 #pragma unroll 1
       for (int nb = 0; nb < 4; ++nb) {
@@ -332,6 +454,31 @@ __global__ __launch_bounds__(kGroupThreads) void grp_assign_kernel(
       lds_barrier();
       best = pre[tid] & 7;
       sure = (pre[tid] & 0x80) != 0;
+    }
+    // The wave's open tokens. A few go through the binary32 stage one at a time, by the whole
+    // wave (each about 100 instructions), and what that leaves open through the fp64 chains 8
+    // rows at a time; with more than kWaveRows every lane runs its own chains below (binary32,
+    // then fp64 where needed: about 2300 and 3200 instructions for the wave, whatever the
+    // count).
+    constexpr int kWaveRows = 8;
+    uint64_t open = 0;
+    bool many = false;
+    if constexpr (MF) {
+      open = __ballot(tok < n && !sure);
+      many = __popcll(open) > kWaveRows;
+      if (!many) {
+        uint64_t left = 0;
+        for (uint64_t o = open; o; o &= o - 1) {
+          const int t = __builtin_ctzll(o);
+          int lab;
+          if (!wave_row_b32<DT, D>(&xs[(64 * w + t) * kStride], cl, count, lane, lab)) left |= 1ull << t;
+          if (lane == t) best = lab;
+        }
+        open = left;
+        sure = true;
+      } else {
+        open = 0;
+      }
     }
     if (tok < n && LDSC && !sure) {
       float b32 = INFINITY, s32 = INFINITY;
@@ -418,17 +565,25 @@ __global__ __launch_bounds__(kGroupThreads) void grp_assign_kernel(
       constexpr float kOrder = 1.0f + 4.0e-5f;  // > (1 + e) / (1 - e), e = 130 * 2^-24
       sure = finite && s32 > b32 * kOrder + 1.0e-37f;  // NaN distances: the fp64 chains decide
     }
+    if constexpr (MF) {
+      // what the wave-wide binary32 stage left open (at most kWaveRows tokens): the fp64
+      // chains, 8 rows at a time
+      while (open) wave_rows_b64<DT, D, kStride>(xs, 64 * w, open, cl, count, lane, best);
+    }
     if (tok < n && !sure) {
       // first strict minimum from +inf: NaN and infinite distances never win, and a token with
       // no finite distance keeps label 0 (the oracle's rule)
       best = 0;
       double best_d = INFINITY;
-      for (int c0 = 0; c0 < count; c0 += 8) {
+      // kC clusters side by side (4 behind the D64 pre-pass, which keeps the registers of a
+      // third wave per SIMD)
+      constexpr int kC = (MF && D == 64) ? 4 : 8;
+      for (int c0 = 0; c0 < count; c0 += kC) {
         const double* cen = centers64 + (bh * CS + c0) * D;  // wave-uniform: scalar loads
         // distance_c = sum over d (in order) of fma(x_d - c_d, x_d - c_d, acc) in fp64
-        double acc[8];
+        double acc[kC];
 #pragma unroll
-        for (int c = 0; c < 8; ++c) acc[c] = 0.0;
+        for (int c = 0; c < kC; ++c) acc[c] = 0.0;
 #pragma unroll 2
         for (int i = 0; i < D / 8; ++i) {
           const uint4 q = *reinterpret_cast<const uint4*>(&xs[tid * kStride + 8 * i]);
@@ -439,26 +594,25 @@ __global__ __launch_bounds__(kGroupThreads) void grp_assign_kernel(
             const double x0 = static_cast<double>(in_to_f32<DT>(w[k] & 0xffffu));
             const double x1 = static_cast<double>(in_to_f32<DT>(w[k] >> 16));
             // fused schedule: the fp64 centers are the exact widenings of the LDS fp32 ones
-            double c0v[8], c1v[8];
+            double c0v[kC], c1v[kC];
             if constexpr (LDSC) {
-              const float4* cl4 = reinterpret_cast<const float4*>(cl);
-              const float4 a0 = cl4[2 * d], a1 = cl4[2 * d + 1], b0 = cl4[2 * d + 2], b1 = cl4[2 * d + 3];
-              const float f0[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
-              const float f1[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+              const float* r0 = cl + d * kFusedClusters + c0;
 #pragma unroll
-              for (int c = 0; c < 8; ++c) {
-                c0v[c] = static_cast<double>(f0[c]);
-                c1v[c] = static_cast<double>(f1[c]);
+              for (int c = 0; c < kC; c += 4) {
+                const float4 a = *reinterpret_cast<const float4*>(r0 + c);
+                const float4 b = *reinterpret_cast<const float4*>(r0 + kFusedClusters + c);
+                c0v[c] = a.x, c0v[c + 1] = a.y, c0v[c + 2] = a.z, c0v[c + 3] = a.w;
+                c1v[c] = b.x, c1v[c + 1] = b.y, c1v[c + 2] = b.z, c1v[c + 3] = b.w;
               }
             } else {
 #pragma unroll
-              for (int c = 0; c < 8; ++c) {
+              for (int c = 0; c < kC; ++c) {
                 c0v[c] = cen[c * D + d];
                 c1v[c] = cen[c * D + d + 1];
               }
             }
 #pragma unroll
-            for (int c = 0; c < 8; ++c) {
+            for (int c = 0; c < kC; ++c) {
               const double d0 = __dsub_rn(x0, c0v[c]);
               acc[c] = __fma_rn(d0, d0, acc[c]);
               const double d1 = __dsub_rn(x1, c1v[c]);
@@ -467,7 +621,7 @@ __global__ __launch_bounds__(kGroupThreads) void grp_assign_kernel(
           }
         }
 #pragma unroll
-        for (int c = 0; c < 8; ++c)
+        for (int c = 0; c < kC; ++c)
           if (c0 + c < count && acc[c] < best_d) {  // ties keep the lowest id
             best_d = acc[c];
             best = c0 + c;

@@ -228,6 +228,46 @@ def test_grouping_rows_not_16_byte_aligned(dim, dtype):
     np.testing.assert_array_equal(perm.cpu().numpy(), eperm)
 
 
+@pytest.mark.parametrize("dim", [64, 128])
+def test_grouping_zero_padding_rows(dim):
+    # Zero rows at the end of each head (padding): four initial centers are the same zero row,
+    # so most tokens tie between them exactly, in every wave (each lane's own binary32 and fp64
+    # chains). Labels, centers, next centers and the permutation are the oracle's.
+    _print_case("grouping zero padding", dim)
+    g = torch.Generator().manual_seed(43 + dim)
+    v = torch.randn(1, 2, 1400, dim, generator=g)
+    v[:, :, 700:] = 0.0
+    v = v.to(torch.bfloat16)
+    perm, labels, centers, nxt = vcx.group_values(v.to(DEV), 8, 2, debug=True, return_centers=True)
+    eperm, elabels, ecenters, enext = o.group_values(bits(v), 8, 2, "bfloat16", return_next=True)
+    np.testing.assert_array_equal(labels.cpu().numpy(), elabels)
+    np.testing.assert_array_equal(centers.cpu().numpy().view(np.uint32), ecenters.view(np.uint32))
+    np.testing.assert_array_equal(nxt.cpu().numpy().view(np.uint32), enext.view(np.uint32))
+    np.testing.assert_array_equal(perm.cpu().numpy(), eperm)
+
+
+@pytest.mark.parametrize("dim", [64, 128])
+@pytest.mark.parametrize("every", [16, 64])
+def test_grouping_few_near_ties_per_wave(dim, every):
+    # The near-tie tokens below, but only every 16th (4 per 64-token wave) or 64th stays on
+    # the bisector; the others move to one side (settled by the bf16 pre-pass). A wave's few
+    # open tokens go through the wave-wide binary32 stage one at a time and, exact and near
+    # ties, through the fp64 chains 8 rows at a time; labels and permutation are the oracle's.
+    _print_case("grouping few near ties", dim, every)
+    v = _near_tie_values(dim, torch.bfloat16).float()
+    n = v.shape[2]
+    t = torch.arange(n)
+    side = (t % every != 5) & (t > 0) & (t < n - 1)
+    v[0, :, side, 0] = torch.where(t[side] % 2 == 0, 0.75, -0.75)
+    v = v.to(torch.bfloat16)
+    perm, labels, centers = vcx.group_values(v.to(DEV), 2, 1, debug=True)
+    eperm, elabels, ecenters = o.group_values(bits(v), 2, 1, "bfloat16")
+    np.testing.assert_array_equal(labels.cpu().numpy(), elabels)
+    np.testing.assert_array_equal(perm.cpu().numpy(), eperm)
+    tie = (t.numpy() % every == 5) & (t.numpy() % 3 == 1) & (t.numpy() % 7 != 0)
+    assert tie.any() and np.all(elabels[..., tie] == 0)
+
+
 def _near_tie_values(dim, dtype, n=1024, seed=0):
     """[1,2,n,dim] V whose tokens sit at or near the bisector of the two initial centers
     (V[0] = -e_0 + w, V[n-1] = +e_0 + w, with the same random tail w in the other channels):

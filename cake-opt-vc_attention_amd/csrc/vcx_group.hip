@@ -78,10 +78,12 @@ __device__ inline void store_center_parts(float x, int64_t slot, int d, int D, c
   f.parts[slot * 2 * D + D + d] = static_cast<uint16_t>(f32_to_bf16_bits(__fsub_rn(x, bf16_bits_to_f32(hi))));
 }
 
-__device__ inline void store_center_norm(const double* red, int64_t slot, int D, const CenterForms& f) {
-  double t = 0.0;
-  for (int i = 0; i < D; ++i) t += red[i];
-  f.norms[slot] = static_cast<float>(t);
+// One wave's sum of x^2 (fp64, a butterfly: the order is free), left in every lane.
+__device__ inline double wave_square_sum(float x) {
+  double q = static_cast<double>(x) * static_cast<double>(x);
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) q += __shfl_xor(q, o, 64);
+  return q;
 }
 
 // Open tokens of the bf16 pre-pass, resolved by the whole wave. cl: the head's 8 binary32
@@ -221,7 +223,11 @@ __global__ void grp_init_kernel(const void* v, int64_t H, int64_t sb, int64_t sh
   }
   if (forms.parts) {
     __syncthreads();
-    if (d < CS) store_center_norm(red[d], bh * CS + d, D, forms);
+    if (d < CS) {  // thread c sums cluster c's squares (the order is free)
+      double q = 0.0;
+      for (int i = 0; i < D; ++i) q += red[d][i];
+      forms.norms[bh * CS + d] = static_cast<float>(q);
+    }
   }
 }
 
@@ -708,18 +714,19 @@ __global__ __launch_bounds__(kGroupThreads) void grp_assign_kernel(
 __global__ __launch_bounds__(128) void grp_update_kernel(float* centers, double* centers64, const double* psum,
                                                          const int32_t* pcnt, int64_t tiles, int D,
                                                          CenterForms forms) {
-  __shared__ double red[128];
+  __shared__ double red[2];
   const int64_t bh = blockIdx.x;
   const int c = blockIdx.y, d = threadIdx.x;
-  // Token count of the cluster: an integer sum (exact in any order), spread over the lanes
-  // and combined in LDS.
-  __shared__ int64_t cnt_sh[128];
+  // Token count of the cluster: an integer sum (exact in any order), spread over the lanes,
+  // then a butterfly per wave and the waves' totals through LDS.
+  __shared__ int64_t cnt_sh[2];
   int64_t part = 0;
   for (int64_t t = d; t < tiles; t += D) part += pcnt[(bh * tiles + t) * kFusedClusters + c];
-  cnt_sh[d] = part;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) part += __shfl_xor(part, o, 64);
+  if ((d & 63) == 0) cnt_sh[d >> 6] = part;
   __syncthreads();
-  int64_t total = 0;
-  for (int i = 0; i < D; ++i) total += cnt_sh[i];
+  const int64_t total = D > 64 ? cnt_sh[0] + cnt_sh[1] : cnt_sh[0];
   constexpr int kBatch = 64;
   const double* col = psum + (bh * tiles * kFusedClusters + c) * D + d;
   const int64_t stride = static_cast<int64_t>(kFusedClusters) * D;
@@ -733,16 +740,25 @@ __global__ __launch_bounds__(128) void grp_update_kernel(float* centers, double*
 #pragma unroll
     for (int i = 0; i < kBatch; ++i) s = __dadd_rn(s, v[i]);
   }
-  for (; t < tiles; ++t) s = __dadd_rn(s, col[t * stride]);
+  if (t < tiles) {  // the partial last batch (the tile count is uniform), its loads issued together too
+    double v[kBatch];
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i) v[i] = col[(t + i < tiles ? t + i : t) * stride];
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i)
+      if (t + i < tiles) s = __dadd_rn(s, v[i]);
+  }
   if (total > 0) {  // the same on every thread of the block
     const float x = static_cast<float>(__ddiv_rn(s, static_cast<double>(total)));
     centers[(bh * kFusedClusters + c) * D + d] = x;
     centers64[(bh * kFusedClusters + c) * D + d] = static_cast<double>(x);
     if (forms.parts) {
       store_center_parts(x, bh * kFusedClusters + c, d, D, forms);
-      red[d] = static_cast<double>(x) * static_cast<double>(x);
+      const double q = wave_square_sum(x);
+      if ((d & 63) == 0) red[d >> 6] = q;
       __syncthreads();
-      if (d == 0) store_center_norm(red, bh * kFusedClusters + c, D, forms);
+      if (d == 0) forms.norms[bh * kFusedClusters + c] = static_cast<float>(D > 64 ? red[0] + red[1] : red[0]);
     }
   }
 }
@@ -817,7 +833,13 @@ __global__ __launch_bounds__(kOffsetThreads) void grp_offsets_kernel(const int32
 #pragma unroll
       for (int i = 0; i < kBatch; ++i) s += v[i];
     }
-    for (; t < t1; ++t) s += head[t * CS + c];
+    if (t < t1) {  // the partial last batch, its loads issued together too
+      int v[kBatch];
+#pragma unroll
+      for (int i = 0; i < kBatch; ++i) v[i] = head[(t + i < t1 ? t + i : t) * CS + c];
+#pragma unroll
+      for (int i = 0; i < kBatch; ++i) s += t + i < t1 ? v[i] : 0;
+    }
     return s;
   };
   // exclusive start of this lane's segment inside its label (all 32 lanes take part)

@@ -208,7 +208,14 @@ __device__ inline void k_mean_body(const double* sums, int64_t tiles, int64_t n,
 #pragma unroll
     for (int i = 0; i < kBatch; ++i) s = __dadd_rn(s, v[i]);
   }
-  for (; t < tiles; ++t) s = __dadd_rn(s, col[t * D]);
+  if (t < tiles) {  // the partial last batch, its loads issued together too
+    double v[kBatch];
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i) v[i] = col[(t + i < tiles ? t + i : t) * D];
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i)
+      if (t + i < tiles) s = __dadd_rn(s, v[i]);
+  }
   float mean = static_cast<float>(__ddiv_rn(s, static_cast<double>(n)));
   if constexpr (RAW) {
     km_f32[bh * D + ch] = mean;
@@ -242,13 +249,15 @@ __global__ __launch_bounds__(kScaleThreads) void v_scale_kernel(const float* a0,
   const float* c1 = SMOOTH ? a1 + bh * tiles * D + ch : nullptr;
   constexpr int kBatch = 8;
   float m0 = 0.0f, m1 = 0.0f;  // smoothing off: amax; on: M (|mean|) and P (peak)
-  int64_t t = sl;
-  for (; t + (kBatch - 1) * S < tiles; t += kBatch * S) {
+  // batches of kBatch tiles of this slice, the last one partial (a missing tile repeats the
+  // batch's first, which no maximum changes), all loads issued together
+  for (int64_t t = sl; t < tiles; t += kBatch * S) {
     float v0[kBatch], v1[kBatch];
 #pragma unroll
     for (int i = 0; i < kBatch; ++i) {
-      v0[i] = c0[(t + i * S) * D];
-      if constexpr (SMOOTH) v1[i] = c1[(t + i * S) * D];
+      const int64_t ti = t + i * S < tiles ? t + i * S : t;  // a missing tile repeats tile t
+      v0[i] = c0[ti * D];
+      if constexpr (SMOOTH) v1[i] = c1[ti * D];
     }
 #pragma unroll
     for (int i = 0; i < kBatch; ++i) {
@@ -258,14 +267,6 @@ __global__ __launch_bounds__(kScaleThreads) void v_scale_kernel(const float* a0,
       } else {
         m0 = fmaxf(m0, v0[i]);
       }
-    }
-  }
-  for (; t < tiles; t += S) {
-    if constexpr (SMOOTH) {
-      m0 = fmaxf(m0, fabsf(c0[t * D]));
-      m1 = fmaxf(m1, c1[t * D]);
-    } else {
-      m0 = fmaxf(m0, c0[t * D]);
     }
   }
   red[0][threadIdx.x] = m0;

@@ -661,7 +661,7 @@ __global__ __launch_bounds__(kGroupThreads) void grp_assign_kernel(
         // the LDS byte offsets of its tokens' staged rows, padded to a multiple of 8 entries
         // with the zero row: adding +0.0 leaves a partial sum unchanged (it starts at +0.0 and
         // is never -0.0). A step reads 8 offsets at once, then the 8 values, then adds them
-        // in list order.
+        // in list order; each wave takes half of the clusters.
         constexpr int kB = 8;
         constexpr uint16_t kZeroRow = kTile * kStride * 2;
         __shared__ int start[kFusedClusters + 1];
@@ -681,24 +681,42 @@ __global__ __launch_bounds__(kGroupThreads) void grp_assign_kernel(
           if (slot < start[c + 1]) order[slot] = kZeroRow;
         }
         lds_barrier();
-        if (tid < D) {
-          const uint8_t* col = reinterpret_cast<const uint8_t*>(xs) + 2 * tid;
-          for (int c = 0; c < count; ++c) {
-            double acc = 0.0;
+        {
+          // wave wv sums clusters 4 wv .. 4 wv + 3, each lane D/64 adjacent channels (one
+          // 2- or 4-byte read per token, as many independent chains)
+          constexpr int CPL = D / 64;
+          using Word = std::conditional_t<CPL == 2, uint32_t, uint16_t>;
+          const uint8_t* col = reinterpret_cast<const uint8_t*>(xs) + 2 * CPL * lane;
+          const int c_end = 4 * wv + 4 < count ? 4 * wv + 4 : count;
+          for (int c = 4 * wv; c < c_end; ++c) {
+            double acc[CPL];
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) acc[j] = 0.0;
             const int b = __builtin_amdgcn_readfirstlane(start[c]), e = __builtin_amdgcn_readfirstlane(start[c + 1]);
             for (int k = b; k < e; k += kB) {
               const uint4 o = *reinterpret_cast<const uint4*>(&order[k]);
               const uint32_t ow[4] = {o.x, o.y, o.z, o.w};
-              float xv[kB];
+              uint32_t xw[kB];
 #pragma unroll
               for (int i = 0; i < kB / 2; ++i) {
-                xv[2 * i] = in_to_f32<DT>(*reinterpret_cast<const uint16_t*>(col + (ow[i] & 0xffffu)));
-                xv[2 * i + 1] = in_to_f32<DT>(*reinterpret_cast<const uint16_t*>(col + (ow[i] >> 16)));
+                xw[2 * i] = *reinterpret_cast<const Word*>(col + (ow[i] & 0xffffu));
+                xw[2 * i + 1] = *reinterpret_cast<const Word*>(col + (ow[i] >> 16));
               }
 #pragma unroll
-              for (int i = 0; i < kB; ++i) acc = __dadd_rn(acc, static_cast<double>(xv[i]));
+              for (int i = 0; i < kB; ++i)
+#pragma unroll
+                for (int j = 0; j < CPL; ++j)
+                  acc[j] = __dadd_rn(acc[j], static_cast<double>(in_to_f32<DT>((xw[i] >> (16 * j)) & 0xffffu)));
             }
-            psum[(meta + c) * D + tid] = acc;
+            double* dst = &psum[(meta + c) * D + CPL * lane];
+            if constexpr (CPL == 2) {
+              double2 pr;
+              pr.x = acc[0];
+              pr.y = acc[1];
+              *reinterpret_cast<double2*>(dst) = pr;
+            } else {
+              dst[0] = acc[0];
+            }
           }
         }
       }

@@ -53,19 +53,25 @@ __device__ inline int64_t source_token(const int64_t* perm, int64_t bh, int64_t 
 // Rows of the NR keys key0 + 16*i (i < NR) of one head, for channel chunk c.
 // All permutation lookups are issued first, then all row loads, so that their
 // latencies overlap; a key past n loads row 0 and reads as zero.
-template <int DT, int D, int NR>
-__device__ inline void load_key_rows(const uint16_t* base, int64_t sn, const int64_t* perm, int64_t bh, int64_t n,
-                                     int64_t key0, int c, float (&v)[NR][D / 16]) {
-  constexpr int CPT = D / 16;
+template <int D, int NR>
+__device__ inline void load_key_rows_packed(const uint16_t* base, int64_t sn, const int64_t* perm, int64_t bh,
+                                            int64_t n, int64_t key0, int c, Row<D> (&r)[NR]) {
   int64_t src[NR];
 #pragma unroll
   for (int i = 0; i < NR; ++i) {
     const int64_t key = key0 + 16 * i;
     src[i] = key < n ? source_token(perm, bh, n, key) : 0;
   }
-  Row<D> r[NR];
 #pragma unroll
   for (int i = 0; i < NR; ++i) load_row<D>(base, sn, src[i], c, r[i]);
+}
+
+template <int DT, int D, int NR>
+__device__ inline void load_key_rows(const uint16_t* base, int64_t sn, const int64_t* perm, int64_t bh, int64_t n,
+                                     int64_t key0, int c, float (&v)[NR][D / 16]) {
+  constexpr int CPT = D / 16;
+  Row<D> r[NR];
+  load_key_rows_packed<D, NR>(base, sn, perm, bh, n, key0, c, r);
 #pragma unroll
   for (int i = 0; i < NR; ++i) {
     const bool valid = key0 + 16 * i < n;
@@ -127,8 +133,11 @@ __global__ __launch_bounds__(kThreads) void tile_stats_kernel(
   const int64_t tile = blockIdx.x, bh = blockIdx.y, tiles = gridDim.x;
   const int tid = threadIdx.x, kk = tid >> 4, c = tid & 15, lane = tid & 63, w = tid >> 6;
   const uint16_t* base = head_base(x, bh, H, sb, sh);
-  float v[8][CPT];
-  load_key_rows<DT, D, 8>(base, sn, perm, bh, n, tile * kTile + kk, c, v);
+  // the rows stay packed (16-bit values) and are widened where used: the smoothing
+  // statistics read them twice, and packed they take half the registers
+  Row<D> rows[8];
+  load_key_rows_packed<D, 8>(base, sn, perm, bh, n, tile * kTile + kk, c, rows);
+  auto v = [&](int i, int j) -> float { return tile * kTile + kk + 16 * i < n ? row_val<DT, D>(rows[i], j) : 0.0f; };
   const int64_t meta = (bh * tiles + tile) * D;
   if constexpr (MODE == kVAmax) {
     float m[CPT];
@@ -136,7 +145,7 @@ __global__ __launch_bounds__(kThreads) void tile_stats_kernel(
     for (int j = 0; j < CPT; ++j) {
       m[j] = 0.0f;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) m[j] = fmaxf(m[j], fabsf(v[i][j]));
+      for (int i = 0; i < 8; ++i) m[j] = fmaxf(m[j], fabsf(v(i, j)));
       m[j] = max_xor32(max_xor16(m[j]));
     }
     if (lane < 16)
@@ -151,7 +160,7 @@ __global__ __launch_bounds__(kThreads) void tile_stats_kernel(
     for (int j = 0; j < CPT; ++j) {
       a[j] = 0.0;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) a[j] = __dadd_rn(a[j], static_cast<double>(v[i][j]));
+      for (int i = 0; i < 8; ++i) a[j] = __dadd_rn(a[j], static_cast<double>(v(i, j)));
     }
     double total;
     tile_tree<D>(a, red, &total);
@@ -166,6 +175,11 @@ __global__ __launch_bounds__(kThreads) void tile_stats_kernel(
         f_out0[meta + tid] = mu;
       }
       __syncthreads();
+      // widen the packed rows again rather than keep the first pass's floats live
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int k = 0; k < CPT / 2; ++k) asm volatile("" : "+v"(rows[i].w[k]));
       float pk[CPT];
 #pragma unroll
       for (int j = 0; j < CPT; ++j) {
@@ -173,7 +187,7 @@ __global__ __launch_bounds__(kThreads) void tile_stats_kernel(
         pk[j] = 0.0f;
 #pragma unroll
         for (int i = 0; i < 8; ++i)
-          if (tile * kTile + kk + 16 * i < n) pk[j] = fmaxf(pk[j], fabsf(__fsub_rn(v[i][j], mu)));
+          if (tile * kTile + kk + 16 * i < n) pk[j] = fmaxf(pk[j], fabsf(__fsub_rn(v(i, j), mu)));
         pk[j] = max_xor32(max_xor16(pk[j]));
       }
       if (lane < 16)

@@ -727,8 +727,7 @@ __global__ __launch_bounds__(kGroupThreads) void grp_assign_kernel(
 // Fused schedule. grid (B*H, count), D threads: new center = RN_f32(sum / n) for a
 // non-empty cluster, the fp64 sum taken over tiles in order. The launch is small (one
 // block per head and cluster), so its time is the chain of load round trips: each batch
-// puts 64 tiles' partials in flight before adding them in order (5 round trips for 295
-// tiles instead of 19 with batches of 16).
+// puts 80 tiles' partials in flight before adding them in order.
 __global__ __launch_bounds__(128) void grp_update_kernel(float* centers, double* centers64, const double* psum,
                                                          const int32_t* pcnt, int64_t tiles, int D,
                                                          CenterForms forms) {
@@ -745,27 +744,26 @@ __global__ __launch_bounds__(128) void grp_update_kernel(float* centers, double*
   if ((d & 63) == 0) cnt_sh[d >> 6] = part;
   __syncthreads();
   const int64_t total = D > 64 ? cnt_sh[0] + cnt_sh[1] : cnt_sh[0];
-  constexpr int kBatch = 64;
-  const double* col = psum + (bh * tiles * kFusedClusters + c) * D + d;
-  const int64_t stride = static_cast<int64_t>(kFusedClusters) * D;
+  // Batches of kBatch tiles by buffer loads from the batch's first tile: the lane's channel
+  // in the vector offset, the tile (wave-uniform, kept below the tile count) in the scalar
+  // one, so that a batch costs only its data registers (295 tiles: 4 round trips, 5 with
+  // batches of 64 by flat loads).
+  constexpr int kBatch = 80;
+  const double* hb = psum + (bh * tiles * kFusedClusters + c) * D;
+  const int stride = kFusedClusters * D;
   double s = 0.0;
-  int64_t t = 0;
-  for (; t + kBatch <= tiles; t += kBatch) {
+  for (int64_t t = 0; t < tiles; t += kBatch) {
+    const int last = static_cast<int>((tiles - t < kBatch ? tiles - t : kBatch) - 1);
+    const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(const_cast<double*>(hb + t * stride), 0,
+                                                                        (last * stride + D) * 8, 0x00020000);
     double v[kBatch];
-#pragma unroll
-    for (int i = 0; i < kBatch; ++i) v[i] = col[(t + i) * stride];
-    __builtin_amdgcn_sched_barrier(0);  // every load of the batch issued before the first add
-#pragma unroll
-    for (int i = 0; i < kBatch; ++i) s = __dadd_rn(s, v[i]);
-  }
-  if (t < tiles) {  // the partial last batch (the tile count is uniform), its loads issued together too
-    double v[kBatch];
-#pragma unroll
-    for (int i = 0; i < kBatch; ++i) v[i] = col[(t + i < tiles ? t + i : t) * stride];
-    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int i = 0; i < kBatch; ++i)
-      if (t + i < tiles) s = __dadd_rn(s, v[i]);
+      v[i] = __builtin_bit_cast(double, __builtin_amdgcn_raw_buffer_load_b64(rp, d * 8, (i < last ? i : last) * stride * 8, 0));
+    __builtin_amdgcn_sched_barrier(0);  // every load of the batch issued before the first add
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i)
+      if (i <= last) s = __dadd_rn(s, v[i]);
   }
   if (total > 0) {  // the same on every thread of the block
     const float x = static_cast<float>(__ddiv_rn(s, static_cast<double>(total)));

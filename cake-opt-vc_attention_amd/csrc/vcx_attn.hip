@@ -524,6 +524,22 @@ struct Wave {
     return tmo;
   }
 
+  // Rescale the history of row group qg, in which some maximum moved (dm = m - m' on each
+  // lane): alpha = exp(dm) (exp2 of the log2-domain difference on the control path) is
+  // exactly 1 on the other lanes, and O, den (and the pending mean weights) are scaled before
+  // the tile's PV adds in.
+  __device__ __forceinline__ void rescale(int qg, float dm) {
+    const float alpha = EC ? __builtin_amdgcn_exp2f(dm * 1.44269504088896341f) : __builtin_amdgcn_exp2f(dm);
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb) O[qg][cb] *= alpha;
+    if constexpr (DACC) dacc[qg][0] *= alpha;
+    else den[qg] *= alpha;
+    if constexpr (SMOOTH) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) wts[qg][j] *= alpha;
+    }
+  }
+
   // Phase 3 of a tile for row group qg: the P bytes against the running maximum mx (and on
   // the control path the row's unrounded mass tmq).
   template <bool LAST, bool PRE>
@@ -696,11 +712,25 @@ struct Wave {
     // ---- logits, online max, P bytes (ExpCast codes, or E4M3 probabilities on the control path)
     v8i P[NQG];
     float tmass[NQG], bs[NQG][8][4], tmax[NQG], scl[NQG];
-    // resc: some maximum of the row group moved; dm: m - m' on each lane
+    // The history of a row group in which some maximum moved is rescaled before this tile's
+    // PV adds in. At D64 the scaling sits inside the branches where a maximum can move, so
+    // the common tile carries no rescale state (two instructions per tile; same-box D64 with
+    // smoothing 0.4-0.7 % faster); at D128 that placement costs the main kernel 0.3 % (its
+    // register allocation moves), so there the flags resc / dm carry it to one place after
+    // the bytes.
+    constexpr bool kEarly = D == 64;
     bool resc[NQG];
     float dm[NQG];
 #pragma unroll
     for (int qg = 0; qg < NQG; ++qg) resc[qg] = false;
+    auto moved = [&](int qg, float mn) {
+      if constexpr (kEarly) {
+        if (wave_any(m[qg] != mn)) rescale(qg, m[qg] - mn);
+      } else {
+        resc[qg] = wave_any(m[qg] != mn);
+        dm[qg] = m[qg] - mn;
+      }
+    };
     if constexpr (PM == 0) {
       // Control path, one row group at a time (D64's three waves per SIMD have no registers
       // for both groups' probabilities at once).
@@ -708,8 +738,7 @@ struct Wave {
       for (int qg = 0; qg < NQG; ++qg) {
         tmax[qg] = logits<LAST>(a, t, qg, S[qg], ksv, bs[qg], scl[qg]);
         const float mn = running_max(m[qg], tmax[qg]);
-        resc[qg] = wave_any(m[qg] != mn);
-        dm[qg] = m[qg] - mn;
+        moved(qg, mn);
         m[qg] = mn;
         bytes<LAST, PRE>(a, bs[qg], scl[qg], m[qg], 0.0f, P[qg], tmass[qg]);
         if constexpr (DUMP) dump_p(a, t, qg, P[qg]);
@@ -727,8 +756,7 @@ struct Wave {
         else mn[0] = running_max(m[0], tmax[0]);
 #pragma unroll
         for (int qg = 0; qg < NQG; ++qg) {
-          resc[qg] = wave_any(m[qg] != mn[qg]);
-          dm[qg] = m[qg] - mn[qg];
+          moved(qg, mn[qg]);
           m[qg] = mn[qg];
           if constexpr (PM == 2) fbias[qg] = __builtin_fmaf(-mn[qg], kExpA, kExpB);
         }
@@ -740,22 +768,10 @@ struct Wave {
       }
     }
 
-    // ---- rescale the history of a row group in which some maximum moved: alpha = exp(m - m')
-    // (exp2 of the log2-domain difference on the control path) is exactly 1 on the other
-    // lanes, and O, den (and the pending mean weights) are scaled before this tile adds in.
+    if constexpr (!kEarly) {
 #pragma unroll
-    for (int qg = 0; qg < NQG; ++qg) {
-      if (resc[qg]) {
-        const float alpha = EC ? __builtin_amdgcn_exp2f(dm[qg] * 1.44269504088896341f) : __builtin_amdgcn_exp2f(dm[qg]);
-#pragma unroll
-        for (int cb = 0; cb < CB; ++cb) O[qg][cb] *= alpha;
-        if constexpr (DACC) dacc[qg][0] *= alpha;
-        else den[qg] *= alpha;
-        if constexpr (SMOOTH) {
-#pragma unroll
-          for (int j = 0; j < 4; ++j) wts[qg][j] *= alpha;
-        }
-      }
+      for (int qg = 0; qg < NQG; ++qg)
+        if (resc[qg]) rescale(qg, dm[qg]);
     }
 
     // ---- O^T += V^T P^T, mass = 1^T P^T

@@ -36,14 +36,14 @@ PEAK_HBM_GBS = 8000.0   # MI355X HBM3E, GB/s (published)
 # commands are in profiles/attn_kernel_<config>_hbm_bytes.txt (FP8 QK variant:
 # profiles/attn_kernel_fp8_main_hbm_bytes.txt). Counters cannot be read from inside this
 # process, so the figure is keyed by QK format and configuration and null where unmeasured.
-MEASURED_TRAFFIC_BYTES = {("int8", "main"): 3.174e9, ("int8", "d64"): 1.771e9, ("int8", "smooth"): 3.133e9,
+MEASURED_TRAFFIC_BYTES = {("int8", "main"): 3.174e9, ("int8", "d64"): 1.769e9, ("int8", "smooth"): 3.133e9,
                           ("int8", "long"): 1.1465e10, ("fp8", "main"): 3.133e9}
 # VALU instructions per wave and 128-key tile of the fused kernel ((SQ_INSTS_VALU -
 # SQ_INSTS_MFMA) / (waves x tiles), rocprofv3 --pmc; profiles/attn_kernel_<config>_counters.txt),
 # and the best issue rate measured for the kernel's
 # per-score VALU chain with two waves per SIMD (3.0 cycles per instruction per SIMD,
 # register-only microbenchmark). Together they give the VALU issue bound of a launch.
-MEASURED_VALU_PER_WAVE_TILE = {("int8", "main"): 261.1, ("int8", "d64"): 388.0, ("int8", "smooth"): 395.4,
+MEASURED_VALU_PER_WAVE_TILE = {("int8", "main"): 261.1, ("int8", "d64"): 386.1, ("int8", "smooth"): 395.4,
                                ("int8", "long"): 385.3}
 VALU_CYCLES_PER_INSTR = 3.0
 SIMDS = 1024            # 256 CUs x 4 SIMDs
